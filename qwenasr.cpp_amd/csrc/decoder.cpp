@@ -1,0 +1,659 @@
+// qa_decoder: device weights, KV cache, workspaces and the step drivers of the C ABI runtime layer.
+//
+// Follows the control flow of the reference's cached backend (src/text-decoder.cpp):
+//   init            1476-1592 (validate, upload f32 weights) + alloc_kv_cache 1420-1474 (zeroed cache)
+//   cached forward  1641-1755 (capacity check, positions n_past + i, 28 layers, last-row logits,
+//                   cur_len = n_past + T)
+//   greedy generate 2209-2311 (prefill, then argmax / stop check / break before the last forward)
+// with the data path replaced by the kernels of this library.
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "ops.hpp"
+
+namespace {
+
+using namespace qa;
+
+struct DevLayer {
+    float * attn_norm = nullptr;
+    float * ffn_norm = nullptr;
+    float * qkv = nullptr;     // [q_dim + 2 kv_dim][hidden]  (q rows, k rows, v rows)
+    float * o = nullptr;       // [hidden][q_dim]
+    float * q_norm = nullptr;
+    float * k_norm = nullptr;
+    float * gu = nullptr;      // [2 intermediate][hidden]     (gate rows, up rows)
+    float * down = nullptr;    // [hidden][intermediate]
+};
+
+enum Kind { kDecode = 0, kPrefill = 1, kNoCache = 2 };
+
+enum Family { kFamAppend = 0, kFamDecodeAttn, kFamPrefillAttn, kFamProj, kFamLogits, kFamCount };
+const char * kFamNames[kFamCount] = {"kv_append", "decode_attn", "prefill_attn", "projections", "logits"};
+
+}  // namespace
+
+struct qa_decoder {
+    qa_text_config cfg{};
+    int32_t n_streams = 0, max_seq = 0, cache_type = 0;
+    hipStream_t stream = nullptr;
+    rocblas_handle blas = nullptr;
+    std::vector<DevLayer> layers;
+    float * embd = nullptr;
+    float * out_norm = nullptr;
+    float * out_w = nullptr;
+    std::vector<void *> weight_allocs;
+    void * cache = nullptr;
+    qa_kv_layout layout{};
+    int32_t * d_lens = nullptr;
+    std::vector<int32_t> cur_len;
+    // activations, sized for cap_rows rows
+    int32_t cap_rows = 0;
+    std::vector<void *> act_allocs;
+    float *x = nullptr, *xn = nullptr, *qkv = nullptr, *qrot = nullptr, *attn = nullptr, *gu = nullptr, *act = nullptr;
+    float * logits = nullptr;    // [n_streams][vocab]
+    void * attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+    void * am_ws = nullptr;
+    size_t am_ws_bytes = 0;
+    int32_t * d_ids = nullptr;
+    int32_t * h_ids = nullptr;   // pinned
+    float * staging = nullptr;
+    size_t staging_bytes = 0;
+    float scale = 0.0f;
+    // profiling
+    bool prof = false;
+    struct Rec { int fam; hipEvent_t a, b; };
+    std::vector<Rec> recs;
+    size_t n_recs = 0;
+};
+
+namespace {
+
+int dmalloc(std::vector<void *> & list, size_t bytes, void ** out) {
+    void * p = nullptr;
+    if (bytes == 0) bytes = 256;
+    if (hipMalloc(&p, bytes) != hipSuccess) return fail(QA_ERR_ALLOC, "device allocation failed");
+    list.push_back(p);
+    *out = p;
+    return QA_OK;
+}
+
+template <typename T>
+int dmalloc_t(std::vector<void *> & list, size_t count, T ** out) {
+    void * p = nullptr;
+    const int rc = dmalloc(list, sizeof(T) * count, &p);
+    *out = static_cast<T *>(p);
+    return rc;
+}
+
+int upload(float * dst, const float * src, size_t n) {
+    if (!src) return fail(QA_ERR_INVALID, "missing weight tensor");
+    QA_HIP(hipMemcpy(dst, src, sizeof(float) * n, hipMemcpyHostToDevice));
+    return QA_OK;
+}
+
+struct Prof {
+    qa_decoder * d;
+    int fam;
+    int idx = -1;
+    Prof(qa_decoder * dec, int family) : d(dec), fam(family) {
+        if (!d->prof) return;
+        if (d->n_recs == d->recs.size()) {
+            qa_decoder::Rec r{family, nullptr, nullptr};
+            if (hipEventCreate(&r.a) != hipSuccess || hipEventCreate(&r.b) != hipSuccess) return;
+            d->recs.push_back(r);
+        }
+        idx = static_cast<int>(d->n_recs++);
+        d->recs[idx].fam = family;
+        (void)hipEventRecord(d->recs[idx].a, d->stream);
+    }
+    ~Prof() {
+        if (idx >= 0) (void)hipEventRecord(d->recs[idx].b, d->stream);
+    }
+};
+
+void free_acts(qa_decoder * d) {
+    for (void * p : d->act_allocs) (void)hipFree(p);
+    d->act_allocs.clear();
+    d->cap_rows = 0;
+}
+
+int ensure_rows(qa_decoder * d, int32_t rows) {
+    if (rows <= d->cap_rows) return QA_OK;
+    (void)hipStreamSynchronize(d->stream);
+    free_acts(d);
+    const size_t H = d->cfg.hidden, QD = static_cast<size_t>(d->cfg.n_heads) * kHeadDim,
+                 KD = static_cast<size_t>(d->cfg.n_kv_heads) * kHeadDim, I = d->cfg.intermediate;
+    const size_t R = static_cast<size_t>(rows);
+    int rc = QA_OK;
+    rc = rc ? rc : dmalloc_t(d->act_allocs, R * H, &d->x);
+    rc = rc ? rc : dmalloc_t(d->act_allocs, R * H, &d->xn);
+    rc = rc ? rc : dmalloc_t(d->act_allocs, R * (QD + 2 * KD), &d->qkv);
+    rc = rc ? rc : dmalloc_t(d->act_allocs, R * QD, &d->qrot);
+    rc = rc ? rc : dmalloc_t(d->act_allocs, R * QD, &d->attn);
+    rc = rc ? rc : dmalloc_t(d->act_allocs, R * 2 * I, &d->gu);
+    rc = rc ? rc : dmalloc_t(d->act_allocs, R * I, &d->act);
+    if (rc != QA_OK) {
+        free_acts(d);
+        return rc;
+    }
+    d->cap_rows = rows;
+    return QA_OK;
+}
+
+int sgemm(qa_decoder * d, const float * W, int32_t out_dim, int32_t in_dim, const float * X, int32_t rows, float * Y,
+          float beta) {
+    // Y[rows][out] (+)= X[rows][in] * W[out][in]^T, as column-major C(out x rows) = W^T(out x in) * X(in x rows)
+    const float alpha = 1.0f;
+    const rocblas_status st = rocblas_sgemm(d->blas, rocblas_operation_transpose, rocblas_operation_none, out_dim,
+                                            rows, in_dim, &alpha, W, in_dim, X, in_dim, &beta, Y, out_dim);
+    if (st != rocblas_status_success) {
+        return fail(QA_ERR_DEVICE, std::string("rocblas_sgemm failed: ") + rocblas_status_to_string(st));
+    }
+    return QA_OK;
+}
+
+int32_t host_max_len(const qa_decoder * d, int32_t n, int32_t add) {
+    int32_t m = 0;
+    for (int32_t s = 0; s < n; ++s) m = std::max(m, d->cur_len[s] + add);
+    return m;
+}
+
+// One layer over `rows` token rows held in d->x.
+//   kDecode : rows = number of streams (one token each), positions d_lens[s], keys [0, d_lens[s] + 1)
+//   kPrefill: rows = T tokens of stream 0 at positions n_past.., keys [0, n_past + t]
+//   kNoCache: rows = T tokens, positions 0..T-1, f32 K/V never stored
+int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past) {
+    const qa_text_config & c = d->cfg;
+    const DevLayer & L = d->layers[l];
+    const int32_t H = c.hidden, QD = c.n_heads * kHeadDim, KD = c.n_kv_heads * kHeadDim, I = c.intermediate;
+    const int32_t W3 = QD + 2 * KD;
+    hipStream_t s = d->stream;
+    int rc;
+    {
+        Prof pr(d, kFamProj);
+        if (rows == 1) {
+            rc = gemv_launch(kEpiStoreOp, true, L.qkv, W3, H, d->x, d->qkv, L.attn_norm, c.rms_norm_eps, s);
+        } else {
+            rc = rmsnorm_rows_launch(d->x, L.attn_norm, rows, H, c.rms_norm_eps, d->xn, s);
+            if (rc == QA_OK) rc = sgemm(d, L.qkv, W3, H, d->xn, rows, d->qkv, 0.0f);
+        }
+        if (rc != QA_OK) return rc;
+    }
+    if (kind == kNoCache) {
+        {
+            Prof pr(d, kFamAppend);
+            rc = qa_qk_prep(d->qkv, rows, c.n_heads, c.n_kv_heads, L.q_norm, L.k_norm, 0, c.rope_theta,
+                            c.rms_norm_eps, s);
+            if (rc != QA_OK) return rc;
+        }
+        Prof pr(d, kFamPrefillAttn);
+        rc = causal_f32_launch(d->qkv, W3, d->qkv + QD, d->qkv + QD + KD, W3, rows, c.n_heads, c.n_kv_heads,
+                               d->scale, d->attn, s);
+        if (rc != QA_OK) return rc;
+    } else {
+        {
+            Prof pr(d, kFamAppend);
+            rc = qa_kv_append(d->qkv, L.q_norm, L.k_norm, d->qrot, d->cache, &d->layout, l, d->d_lens,
+                              kind == kDecode ? rows : 1, kind == kDecode ? 1 : rows, c.n_heads, c.rope_theta,
+                              c.rms_norm_eps, s);
+            if (rc != QA_OK) return rc;
+        }
+        if (kind == kDecode) {
+            Prof pr(d, kFamDecodeAttn);
+            rc = decode_attn_launch(d->qrot, QD, d->cache, d->layout, l, d->d_lens, 1, rows,
+                                    host_max_len(d, rows, 1), c.n_heads, d->scale, d->attn, d->attn_ws,
+                                    d->attn_ws_bytes, s);
+        } else {
+            Prof pr(d, kFamPrefillAttn);
+            rc = prefill_attn_launch(d->qrot, QD, d->cache, d->layout, l, 0, n_past, rows, c.n_heads, d->scale,
+                                     d->attn, nullptr, 0, s);
+        }
+        if (rc != QA_OK) return rc;
+    }
+    Prof pr(d, kFamProj);
+    if (rows == 1) {
+        rc = gemv_launch(kEpiAccumOp, false, L.o, H, QD, d->attn, d->x, nullptr, 0.0f, s);
+        if (rc == QA_OK) rc = gemv_launch(kEpiSwigluOp, true, L.gu, I, H, d->x, d->act, L.ffn_norm, c.rms_norm_eps, s);
+        if (rc == QA_OK) rc = gemv_launch(kEpiAccumOp, false, L.down, H, I, d->act, d->x, nullptr, 0.0f, s);
+    } else {
+        rc = sgemm(d, L.o, H, QD, d->attn, rows, d->x, 1.0f);
+        if (rc == QA_OK) rc = rmsnorm_rows_launch(d->x, L.ffn_norm, rows, H, c.rms_norm_eps, d->xn, s);
+        if (rc == QA_OK) rc = sgemm(d, L.gu, 2 * I, H, d->xn, rows, d->gu, 0.0f);
+        if (rc == QA_OK) rc = swiglu_rows_launch(d->gu, rows, I, d->act, s);
+        if (rc == QA_OK) rc = sgemm(d, L.down, H, I, d->act, rows, d->x, 1.0f);
+    }
+    return rc;
+}
+
+// Logits of `rows` rows starting at row `first` of d->x into d->logits[0..rows), then greedy ids.
+int logits_and_pick(qa_decoder * d, int32_t first, int32_t rows, bool pick) {
+    const qa_text_config & c = d->cfg;
+    if (!d->out_w || !d->out_norm) return fail(QA_ERR_INVALID, "decoder has no output weights");
+    int rc;
+    {
+        Prof pr(d, kFamLogits);
+        const float * xr = d->x + static_cast<int64_t>(first) * c.hidden;
+        if (rows == 1) {
+            rc = gemv_launch(kEpiStoreOp, true, d->out_w, c.vocab, c.hidden, xr, d->logits, d->out_norm,
+                             c.rms_norm_eps, d->stream);
+        } else {
+            rc = rmsnorm_rows_launch(xr, d->out_norm, rows, c.hidden, c.rms_norm_eps, d->xn, d->stream);
+            if (rc == QA_OK) rc = sgemm(d, d->out_w, c.vocab, c.hidden, d->xn, rows, d->logits, 0.0f);
+        }
+        if (rc != QA_OK) return rc;
+    }
+    if (!pick) return QA_OK;
+    return argmax_launch(d->logits, rows, c.vocab, d->d_ids, d->am_ws, d->stream);
+}
+
+int check_forward(const qa_decoder * d, int32_t n_tokens, int32_t n_past) {
+    if (n_tokens <= 0 || n_past < 0 || n_past + n_tokens > d->max_seq) {
+        return fail(n_past + n_tokens > d->max_seq ? QA_ERR_CAPACITY : QA_ERR_INVALID,
+                    "invalid text decoder cached forward configuration");
+    }
+    return QA_OK;
+}
+
+// Cached call of stream 0 with x already on the device.
+int forward_device(qa_decoder * d, int32_t n_tokens, int32_t n_past, bool pick) {
+    int rc = set_values_launch(d->d_lens, 1, n_past, d->stream);
+    if (rc != QA_OK) return rc;
+    d->cur_len[0] = n_past;
+    const int kind = n_tokens == 1 ? kDecode : kPrefill;
+    for (int32_t l = 0; l < d->cfg.n_layers; ++l) {
+        rc = run_layer(d, l, n_tokens, kind, n_past);
+        if (rc != QA_OK) return rc;
+    }
+    rc = logits_and_pick(d, n_tokens - 1, 1, pick);
+    if (rc != QA_OK) return rc;
+    rc = set_values_launch(d->d_lens, 1, n_past + n_tokens, d->stream);
+    d->cur_len[0] = n_past + n_tokens;
+    return rc;
+}
+
+float top2_margin(const std::vector<float> & v, int32_t best) {
+    float second = -INFINITY;
+    for (size_t i = 0; i < v.size(); ++i) {
+        if (static_cast<int32_t>(i) != best && v[i] > second) second = v[i];
+    }
+    return v[best] - second;
+}
+
+}  // namespace
+
+extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weights * w, int32_t n_streams,
+                                 int32_t max_seq, int32_t cache_type, qa_decoder ** out) {
+    if (!out) return fail(QA_ERR_INVALID, "qa_decoder_create: null output");
+    *out = nullptr;
+    if (!cfg || !w || !w->layers || cfg->n_layers <= 0 || cfg->hidden <= 0 || cfg->n_heads <= 0 ||
+        cfg->n_kv_heads <= 0 || cfg->intermediate <= 0 || cfg->vocab <= 0 || cfg->n_heads % cfg->n_kv_heads != 0) {
+        return fail(QA_ERR_INVALID, "invalid text decoder backend configuration");
+    }
+    if (cfg->head_dim != kHeadDim || cfg->n_heads != 2 * cfg->n_kv_heads) {
+        return fail(QA_ERR_INVALID, "this build implements head_dim 128 with 2 query heads per KV head");
+    }
+    if (n_streams <= 0 || max_seq <= 0 || (cache_type != QA_CACHE_F32 && cache_type != QA_CACHE_F16)) {
+        return fail(QA_ERR_INVALID, "invalid text decoder KV-cache configuration");
+    }
+    if (qa_device_count() <= 0) return fail(QA_ERR_NO_DEVICE, "no HIP device visible");
+    QA_HIP(hipSetDevice(0));
+
+    qa_decoder * d = new qa_decoder();
+    d->cfg = *cfg;
+    d->n_streams = n_streams;
+    d->max_seq = max_seq;
+    d->cache_type = cache_type;
+    d->scale = 1.0f / std::sqrt(static_cast<float>(cfg->head_dim));
+    d->cur_len.assign(static_cast<size_t>(n_streams), 0);
+    auto bail = [&](int rc) {
+        qa_decoder_destroy(d);
+        return rc;
+    };
+    if (hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking) != hipSuccess) {
+        return bail(fail(QA_ERR_DEVICE, "hipStreamCreate failed"));
+    }
+    if (rocblas_create_handle(&d->blas) != rocblas_status_success ||
+        rocblas_set_stream(d->blas, d->stream) != rocblas_status_success) {
+        return bail(fail(QA_ERR_DEVICE, "rocblas handle creation failed"));
+    }
+
+    const size_t H = cfg->hidden, QD = static_cast<size_t>(cfg->n_heads) * kHeadDim,
+                 KD = static_cast<size_t>(cfg->n_kv_heads) * kHeadDim, I = cfg->intermediate;
+    int rc = QA_OK;
+    d->layers.resize(static_cast<size_t>(cfg->n_layers));
+    for (int32_t l = 0; l < cfg->n_layers && rc == QA_OK; ++l) {
+        const qa_layer_weights & lw = w->layers[l];
+        DevLayer & L = d->layers[static_cast<size_t>(l)];
+        rc = rc ? rc : dmalloc_t(d->weight_allocs, H, &L.attn_norm);
+        rc = rc ? rc : dmalloc_t(d->weight_allocs, H, &L.ffn_norm);
+        rc = rc ? rc : dmalloc_t(d->weight_allocs, (QD + 2 * KD) * H, &L.qkv);
+        rc = rc ? rc : dmalloc_t(d->weight_allocs, H * QD, &L.o);
+        rc = rc ? rc : dmalloc_t(d->weight_allocs, kHeadDim, &L.q_norm);
+        rc = rc ? rc : dmalloc_t(d->weight_allocs, kHeadDim, &L.k_norm);
+        rc = rc ? rc : dmalloc_t(d->weight_allocs, 2 * I * H, &L.gu);
+        rc = rc ? rc : dmalloc_t(d->weight_allocs, H * I, &L.down);
+        rc = rc ? rc : upload(L.attn_norm, lw.attn_norm, H);
+        rc = rc ? rc : upload(L.ffn_norm, lw.ffn_norm, H);
+        rc = rc ? rc : upload(L.qkv, lw.q, QD * H);
+        rc = rc ? rc : upload(L.qkv + QD * H, lw.k, KD * H);
+        rc = rc ? rc : upload(L.qkv + (QD + KD) * H, lw.v, KD * H);
+        rc = rc ? rc : upload(L.o, lw.o, H * QD);
+        rc = rc ? rc : upload(L.q_norm, lw.q_norm, kHeadDim);
+        rc = rc ? rc : upload(L.k_norm, lw.k_norm, kHeadDim);
+        rc = rc ? rc : upload(L.gu, lw.gate, I * H);
+        rc = rc ? rc : upload(L.gu + I * H, lw.up, I * H);
+        rc = rc ? rc : upload(L.down, lw.down, H * I);
+    }
+    if (rc != QA_OK) return bail(rc);
+    const size_t VH = static_cast<size_t>(cfg->vocab) * H;
+    if (w->output && w->output_norm) {
+        rc = rc ? rc : dmalloc_t(d->weight_allocs, VH, &d->out_w);
+        rc = rc ? rc : upload(d->out_w, w->output, VH);
+        rc = rc ? rc : dmalloc_t(d->weight_allocs, H, &d->out_norm);
+        rc = rc ? rc : upload(d->out_norm, w->output_norm, H);
+    }
+    if (rc == QA_OK && w->token_embd) {
+        if (w->token_embd == w->output && d->out_w) {
+            d->embd = d->out_w;     // tied embeddings: one device copy
+        } else {
+            rc = dmalloc_t(d->weight_allocs, VH, &d->embd);
+            rc = rc ? rc : upload(d->embd, w->token_embd, VH);
+        }
+    }
+    if (rc != QA_OK) return bail(rc);
+
+    d->layout.n_layers = cfg->n_layers;
+    d->layout.n_streams = n_streams;
+    d->layout.n_kv_heads = cfg->n_kv_heads;
+    d->layout.head_dim = kHeadDim;
+    d->layout.max_seq = max_seq;
+    d->layout.cache_type = cache_type;
+    rc = qa_kv_cache_alloc(&d->layout, &d->cache);
+    if (rc != QA_OK) return bail(rc);
+
+    rc = rc ? rc : dmalloc_t(d->weight_allocs, static_cast<size_t>(n_streams), &d->d_lens);
+    rc = rc ? rc : dmalloc_t(d->weight_allocs, static_cast<size_t>(n_streams), &d->d_ids);
+    rc = rc ? rc : dmalloc_t(d->weight_allocs, static_cast<size_t>(n_streams) * cfg->vocab, &d->logits);
+    d->attn_ws_bytes = decode_attn_workspace(n_streams, cfg->n_heads, max_seq);
+    rc = rc ? rc : dmalloc(d->weight_allocs, d->attn_ws_bytes, &d->attn_ws);
+    d->am_ws_bytes = argmax_workspace_bytes(n_streams);
+    rc = rc ? rc : dmalloc(d->weight_allocs, d->am_ws_bytes, &d->am_ws);
+    if (rc != QA_OK) return bail(rc);
+    if (hipHostMalloc(reinterpret_cast<void **>(&d->h_ids), sizeof(int32_t) * 4096 * static_cast<size_t>(n_streams)) !=
+        hipSuccess) {
+        d->h_ids = nullptr;
+        return bail(fail(QA_ERR_ALLOC, "pinned host allocation failed"));
+    }
+    if (hipMemset(d->d_lens, 0, sizeof(int32_t) * n_streams) != hipSuccess ||
+        hipMemset(d->attn_ws, 0, d->attn_ws_bytes) != hipSuccess || hipMemset(d->am_ws, 0, d->am_ws_bytes) != hipSuccess) {
+        return bail(fail(QA_ERR_DEVICE, "workspace clear failed"));
+    }
+    rc = ensure_rows(d, n_streams);
+    if (rc != QA_OK) return bail(rc);
+    *out = d;
+    return QA_OK;
+}
+
+extern "C" void qa_decoder_destroy(qa_decoder * d) {
+    if (!d) return;
+    if (d->stream) (void)hipStreamSynchronize(d->stream);
+    for (auto & r : d->recs) {
+        if (r.a) (void)hipEventDestroy(r.a);
+        if (r.b) (void)hipEventDestroy(r.b);
+    }
+    free_acts(d);
+    for (void * p : d->weight_allocs) (void)hipFree(p);
+    if (d->staging) (void)hipFree(d->staging);
+    if (d->cache) (void)hipFree(d->cache);
+    if (d->h_ids) (void)hipHostFree(d->h_ids);
+    if (d->blas) rocblas_destroy_handle(d->blas);
+    if (d->stream) (void)hipStreamDestroy(d->stream);
+    delete d;
+}
+
+extern "C" int qa_decoder_cur_len(const qa_decoder * d, int32_t stream, int32_t * cur_len) {
+    if (!d || !cur_len || stream < 0 || stream >= d->n_streams) return fail(QA_ERR_INVALID, "qa_decoder_cur_len");
+    *cur_len = d->cur_len[static_cast<size_t>(stream)];
+    return QA_OK;
+}
+
+extern "C" int qa_decoder_set_cur_len(qa_decoder * d, int32_t stream, int32_t cur_len) {
+    if (!d || stream < 0 || stream >= d->n_streams || cur_len < 0 || cur_len > d->max_seq) {
+        return fail(QA_ERR_INVALID, "qa_decoder_set_cur_len");
+    }
+    d->cur_len[static_cast<size_t>(stream)] = cur_len;
+    return set_values_launch(d->d_lens + stream, 1, cur_len, d->stream);
+}
+
+extern "C" int qa_decoder_device_lens(qa_decoder * d, int32_t * lens) {
+    if (!d || !lens) return fail(QA_ERR_INVALID, "qa_decoder_device_lens");
+    QA_HIP(hipMemcpyAsync(lens, d->d_lens, sizeof(int32_t) * d->n_streams, hipMemcpyDeviceToHost, d->stream));
+    QA_HIP(hipStreamSynchronize(d->stream));
+    return QA_OK;
+}
+
+extern "C" void * qa_decoder_cache(qa_decoder * d, qa_kv_layout * layout) {
+    if (!d) return nullptr;
+    if (layout) *layout = d->layout;
+    return d->cache;
+}
+
+extern "C" void * qa_decoder_stream(qa_decoder * d) { return d ? d->stream : nullptr; }
+
+extern "C" int qa_decoder_forward(qa_decoder * d, const float * x, int32_t n_tokens, int32_t n_past, float * logits) {
+    if (!d || !x) return fail(QA_ERR_INVALID, "text_decoder_backend_cached_logits: invalid arguments");
+    int rc = check_forward(d, n_tokens, n_past);
+    if (rc != QA_OK) return rc;
+    rc = ensure_rows(d, n_tokens);
+    if (rc != QA_OK) return rc;
+    QA_HIP(hipMemcpyAsync(d->x, x, sizeof(float) * n_tokens * d->cfg.hidden, hipMemcpyHostToDevice, d->stream));
+    rc = forward_device(d, n_tokens, n_past, false);
+    if (rc != QA_OK) return rc;
+    if (logits) {
+        QA_HIP(hipMemcpyAsync(logits, d->logits, sizeof(float) * d->cfg.vocab, hipMemcpyDeviceToHost, d->stream));
+    }
+    QA_HIP(hipStreamSynchronize(d->stream));
+    return QA_OK;
+}
+
+extern "C" int qa_decoder_generate(qa_decoder * d, const float * x, int32_t n_tokens, int32_t max_new,
+                                   const int32_t * stop_ids, int32_t n_stop, int32_t * out_ids, int32_t * n_out,
+                                   int32_t * stopped, int32_t * total_tokens, float * margins) {
+    if (!d || !x || !n_out || !stopped || !total_tokens || (max_new > 0 && !out_ids)) {
+        return fail(QA_ERR_INVALID, "qwenasr_text_generate_cached_backend: backend or out is null");
+    }
+    *n_out = 0;
+    *stopped = 0;
+    *total_tokens = n_tokens;
+    if (max_new < 0) return fail(QA_ERR_INVALID, "max_new_tokens must be non-negative");
+    if (n_tokens <= 0) return fail(QA_ERR_INVALID, "invalid backend cached text generation input");
+    if (n_tokens + max_new > d->max_seq) return fail(QA_ERR_CAPACITY, "backend text generation exceeds KV-cache capacity");
+    if (max_new == 0) return QA_OK;
+    if (!d->embd) return fail(QA_ERR_INVALID, "decoder has no token embedding");
+    int rc = ensure_rows(d, n_tokens);
+    if (rc != QA_OK) return rc;
+    const int32_t V = d->cfg.vocab;
+    std::vector<float> host_logits;
+    QA_HIP(hipMemcpyAsync(d->x, x, sizeof(float) * n_tokens * d->cfg.hidden, hipMemcpyHostToDevice, d->stream));
+    rc = forward_device(d, n_tokens, 0, true);
+    if (rc != QA_OK) return rc;
+    for (int32_t step = 0; step < max_new; ++step) {
+        QA_HIP(hipMemcpyAsync(d->h_ids, d->d_ids, sizeof(int32_t), hipMemcpyDeviceToHost, d->stream));
+        if (margins) {
+            host_logits.resize(static_cast<size_t>(V));
+            QA_HIP(hipMemcpyAsync(host_logits.data(), d->logits, sizeof(float) * V, hipMemcpyDeviceToHost, d->stream));
+        }
+        QA_HIP(hipStreamSynchronize(d->stream));
+        const int32_t id = d->h_ids[0];
+        if (id < 0 || id >= V) return fail(QA_ERR_RANGE, "generated token id is out of range");
+        if (margins) margins[step] = top2_margin(host_logits, id);
+        out_ids[(*n_out)++] = id;
+        *total_tokens = n_tokens + *n_out;
+        bool stop = false;
+        for (int32_t k = 0; k < n_stop; ++k) stop = stop || stop_ids[k] == id;
+        if (stop) {
+            *stopped = 1;
+            break;
+        }
+        if (step + 1 >= max_new) break;
+        rc = embed_rows_launch(d->embd, V, d->cfg.hidden, d->d_ids, 1, d->x, d->stream);
+        if (rc == QA_OK) rc = forward_device(d, 1, d->cur_len[0], true);
+        if (rc != QA_OK) return rc;
+    }
+    QA_HIP(hipStreamSynchronize(d->stream));
+    return QA_OK;
+}
+
+extern "C" int qa_decoder_decode_streams(qa_decoder * d, const int32_t * first_ids, int32_t n_steps, int32_t * out_ids) {
+    if (!d || !first_ids || (n_steps > 0 && !out_ids) || n_steps < 0) {
+        return fail(QA_ERR_INVALID, "qa_decoder_decode_streams: invalid arguments");
+    }
+    const int32_t S = d->n_streams;
+    for (int32_t s = 0; s < S; ++s) {
+        if (d->cur_len[s] + n_steps > d->max_seq) {
+            return fail(QA_ERR_CAPACITY, "decode steps exceed the KV-cache capacity of a stream");
+        }
+        if (first_ids[s] < 0 || first_ids[s] >= d->cfg.vocab) return fail(QA_ERR_RANGE, "first id out of range");
+    }
+    if (n_steps == 0) return QA_OK;
+    if (static_cast<int64_t>(n_steps) * S > 4096LL * S) return fail(QA_ERR_INVALID, "too many steps");
+    int rc = ensure_rows(d, S);
+    if (rc != QA_OK) return rc;
+    QA_HIP(hipMemcpyAsync(d->d_ids, first_ids, sizeof(int32_t) * S, hipMemcpyHostToDevice, d->stream));
+    for (int32_t k = 0; k < n_steps; ++k) {
+        rc = embed_rows_launch(d->embd, d->cfg.vocab, d->cfg.hidden, d->d_ids, S, d->x, d->stream);
+        for (int32_t l = 0; l < d->cfg.n_layers && rc == QA_OK; ++l) rc = run_layer(d, l, S, kDecode, 0);
+        if (rc == QA_OK) rc = logits_and_pick(d, 0, S, true);
+        if (rc == QA_OK) rc = advance_lens_launch(d->d_lens, S, 1, d->stream);
+        if (rc != QA_OK) return rc;
+        for (int32_t s = 0; s < S; ++s) d->cur_len[s] += 1;
+        QA_HIP(hipMemcpyAsync(d->h_ids + static_cast<size_t>(k) * S, d->d_ids, sizeof(int32_t) * S,
+                              hipMemcpyDeviceToHost, d->stream));
+    }
+    QA_HIP(hipStreamSynchronize(d->stream));
+    std::memcpy(out_ids, d->h_ids, sizeof(int32_t) * static_cast<size_t>(n_steps) * S);
+    return QA_OK;
+}
+
+extern "C" int qa_decoder_fill_cache(qa_decoder * d, int32_t stream, const float * k, const float * v, int32_t len) {
+    if (!d || !k || !v || stream < 0 || stream >= d->n_streams || len < 0 || len > d->max_seq) {
+        return fail(QA_ERR_INVALID, "qa_decoder_fill_cache: invalid arguments");
+    }
+    const size_t per_head = static_cast<size_t>(len) * kHeadDim;
+    const size_t per_layer = per_head * d->cfg.n_kv_heads;
+    if (per_layer * sizeof(float) > d->staging_bytes) {
+        if (d->staging) (void)hipFree(d->staging);
+        d->staging = nullptr;
+        d->staging_bytes = 0;
+        if (hipMalloc(reinterpret_cast<void **>(&d->staging), per_layer * sizeof(float)) != hipSuccess) {
+            return fail(QA_ERR_ALLOC, "staging allocation failed");
+        }
+        d->staging_bytes = per_layer * sizeof(float);
+    }
+    const size_t esz = qa_kv_elem_bytes(d->cache_type);
+    for (int32_t l = 0; l < d->cfg.n_layers; ++l) {
+        for (int kv = 0; kv < 2; ++kv) {
+            const float * src = (kv == 0 ? k : v) + per_layer * l;
+            QA_HIP(hipMemcpyAsync(d->staging, src, per_layer * sizeof(float), hipMemcpyHostToDevice, d->stream));
+            for (int32_t h = 0; h < d->cfg.n_kv_heads; ++h) {
+                char * dst = static_cast<char *>(d->cache) +
+                    esz * cache_row_offset(l, kv, stream, h, 0, d->n_streams, d->cfg.n_kv_heads, d->max_seq);
+                const int rc = cast_rows_launch(d->staging + per_head * h, dst, d->cache_type,
+                                                static_cast<int64_t>(per_head), d->stream);
+                if (rc != QA_OK) return rc;
+            }
+            QA_HIP(hipStreamSynchronize(d->stream));
+        }
+    }
+    return qa_decoder_set_cur_len(d, stream, len);
+}
+
+extern "C" int qa_decoder_layer_forward(qa_decoder * d, int32_t layer, const float * x, int32_t n_tokens, int32_t n_past,
+                                        float * y) {
+    if (!d || !x || !y || layer < 0 || layer >= d->cfg.n_layers) return fail(QA_ERR_INVALID, "qa_decoder_layer_forward");
+    int rc = check_forward(d, n_tokens, n_past);
+    if (rc != QA_OK) return rc;
+    rc = ensure_rows(d, n_tokens);
+    if (rc != QA_OK) return rc;
+    QA_HIP(hipMemcpyAsync(d->x, x, sizeof(float) * n_tokens * d->cfg.hidden, hipMemcpyHostToDevice, d->stream));
+    rc = set_values_launch(d->d_lens, 1, n_past, d->stream);
+    d->cur_len[0] = n_past;
+    if (rc == QA_OK) rc = run_layer(d, layer, n_tokens, n_tokens == 1 ? kDecode : kPrefill, n_past);
+    if (rc == QA_OK) rc = set_values_launch(d->d_lens, 1, n_past + n_tokens, d->stream);
+    if (rc != QA_OK) return rc;
+    d->cur_len[0] = n_past + n_tokens;
+    QA_HIP(hipMemcpyAsync(y, d->x, sizeof(float) * n_tokens * d->cfg.hidden, hipMemcpyDeviceToHost, d->stream));
+    QA_HIP(hipStreamSynchronize(d->stream));
+    return QA_OK;
+}
+
+extern "C" int qa_decoder_layer_forward_nocache(qa_decoder * d, int32_t layer, const float * x, int32_t n_tokens,
+                                                float * y) {
+    if (!d || !x || !y || layer < 0 || layer >= d->cfg.n_layers || n_tokens <= 0) {
+        return fail(QA_ERR_INVALID, "invalid decoder input for text layer backend");
+    }
+    int rc = ensure_rows(d, n_tokens);
+    if (rc != QA_OK) return rc;
+    QA_HIP(hipMemcpyAsync(d->x, x, sizeof(float) * n_tokens * d->cfg.hidden, hipMemcpyHostToDevice, d->stream));
+    rc = run_layer(d, layer, n_tokens, kNoCache, 0);
+    if (rc != QA_OK) return rc;
+    QA_HIP(hipMemcpyAsync(y, d->x, sizeof(float) * n_tokens * d->cfg.hidden, hipMemcpyDeviceToHost, d->stream));
+    QA_HIP(hipStreamSynchronize(d->stream));
+    return QA_OK;
+}
+
+extern "C" int qa_decoder_prefill_nocache(qa_decoder * d, const float * x, int32_t n_tokens, float * logits) {
+    if (!d || !x || !logits || n_tokens <= 0) return fail(QA_ERR_INVALID, "invalid decoder input for text prefill backend");
+    int rc = ensure_rows(d, n_tokens);
+    if (rc != QA_OK) return rc;
+    QA_HIP(hipMemcpyAsync(d->x, x, sizeof(float) * n_tokens * d->cfg.hidden, hipMemcpyHostToDevice, d->stream));
+    for (int32_t l = 0; l < d->cfg.n_layers && rc == QA_OK; ++l) rc = run_layer(d, l, n_tokens, kNoCache, 0);
+    if (rc == QA_OK) rc = logits_and_pick(d, n_tokens - 1, 1, false);
+    if (rc != QA_OK) return rc;
+    QA_HIP(hipMemcpyAsync(logits, d->logits, sizeof(float) * d->cfg.vocab, hipMemcpyDeviceToHost, d->stream));
+    QA_HIP(hipStreamSynchronize(d->stream));
+    return QA_OK;
+}
+
+extern "C" int qa_decoder_profile_enable(qa_decoder * d, int32_t enable) {
+    if (!d) return fail(QA_ERR_INVALID, "qa_decoder_profile_enable");
+    d->prof = enable != 0;
+    return QA_OK;
+}
+
+extern "C" int qa_decoder_profile_reset(qa_decoder * d) {
+    if (!d) return fail(QA_ERR_INVALID, "qa_decoder_profile_reset");
+    QA_HIP(hipStreamSynchronize(d->stream));
+    d->n_recs = 0;
+    return QA_OK;
+}
+
+extern "C" int qa_decoder_profile_read(qa_decoder * d, const char * family, double * total_ms, int64_t * launches) {
+    if (!d || !family || !total_ms || !launches) return fail(QA_ERR_INVALID, "qa_decoder_profile_read");
+    int fam = -1;
+    for (int i = 0; i < kFamCount; ++i) {
+        if (std::strcmp(kFamNames[i], family) == 0) fam = i;
+    }
+    if (fam < 0) return fail(QA_ERR_INVALID, std::string("unknown kernel family: ") + family);
+    QA_HIP(hipStreamSynchronize(d->stream));
+    double total = 0.0;
+    int64_t n = 0;
+    for (size_t i = 0; i < d->n_recs; ++i) {
+        if (d->recs[i].fam != fam) continue;
+        float ms = 0.0f;
+        QA_HIP(hipEventElapsedTime(&ms, d->recs[i].a, d->recs[i].b));
+        total += ms;
+        ++n;
+    }
+    *total_ms = total;
+    *launches = n;
+    return QA_OK;
+}

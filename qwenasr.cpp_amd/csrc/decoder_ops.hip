@@ -1,0 +1,423 @@
+// The rest of a Qwen3 decoder step on gfx950: f32 GEMV with fused pre-RMSNorm / residual / SwiGLU
+// epilogues, row RMSNorm, SwiGLU, residual add, greedy argmax, embedding gather, length bookkeeping.
+//
+// These replace the GGML ops around the KV-cache path in text-decoder.cpp:365-373 and 465-493
+// (linear_ggml with PREC_F32, rms_norm * w, silu * up, add, logits view) and the host argmax of
+// 2266-2274.  Weights stay f32 (the reference requires f32 tensors, require_f32_tensor 29-42), so a
+// decode step streams every weight byte once: the GEMV is HBM-bound and is written for that --
+// each wave keeps its input row in registers and walks whole weight rows with 16-byte loads.
+#include "ops.hpp"
+
+#include <algorithm>
+#include <cmath>
+
+namespace qa {
+namespace {
+
+enum { kEpiStore = 0, kEpiAccum = 1, kEpiSwiglu = 2 };
+
+struct GemvParams {
+    const float * W;        // [rows_w][in_dim]; for SwiGLU rows_w = 2 * out_dim (gate rows, then up rows)
+    const float * x;        // [in_dim]
+    float * y;              // [out_dim]
+    const float * norm_w;   // pre-RMSNorm weight (PRENORM only)
+    int32_t out_dim, in_dim;
+    float eps;
+};
+
+__device__ inline double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ inline float wave_sum_f(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ inline float dot4(const f4 a, const f4 b, float acc) {
+    acc = fmaf(a.x, b.x, acc);
+    acc = fmaf(a.y, b.y, acc);
+    acc = fmaf(a.z, b.z, acc);
+    acc = fmaf(a.w, b.w, acc);
+    return acc;
+}
+
+// IN4 = in_dim / 256 (each lane holds 4 * IN4 input elements), NR rows per wave iteration.
+template <int IN4, int NR, int EPI, bool PRENORM>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x >> 6;
+    f4 xv[IN4];
+#pragma unroll
+    for (int k = 0; k < IN4; ++k) xv[k] = *reinterpret_cast<const f4 *>(p.x + k * 256 + lane * 4);
+    if (PRENORM) {
+        // rms_norm_row (text-decoder.cpp:542-557): squares in double, float scale, (x * scale) * w
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < IN4; ++k) {
+            ss += static_cast<double>(xv[k].x) * xv[k].x + static_cast<double>(xv[k].y) * xv[k].y +
+                  static_cast<double>(xv[k].z) * xv[k].z + static_cast<double>(xv[k].w) * xv[k].w;
+        }
+        ss = wave_sum_d(ss);
+        const float scale = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(p.in_dim)) + p.eps);
+#pragma unroll
+        for (int k = 0; k < IN4; ++k) {
+            const f4 w = *reinterpret_cast<const f4 *>(p.norm_w + k * 256 + lane * 4);
+            xv[k].x = xv[k].x * scale * w.x;
+            xv[k].y = xv[k].y * scale * w.y;
+            xv[k].z = xv[k].z * scale * w.z;
+            xv[k].w = xv[k].w * scale * w.w;
+        }
+    }
+    const int gw = blockIdx.x * 4 + wave;
+    const int nw = gridDim.x * 4;
+    const int64_t in = p.in_dim;
+    for (int o0 = gw * NR; o0 < p.out_dim; o0 += nw * NR) {
+        float acc[NR];
+        float accu[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) { acc[r] = 0.0f; accu[r] = 0.0f; }
+        f4 wv[NR][IN4];
+        f4 wu[NR][IN4];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int o = min(o0 + r, p.out_dim - 1);
+            const float * wr = p.W + o * in + lane * 4;
+#pragma unroll
+            for (int k = 0; k < IN4; ++k) {
+                wv[r][k] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(wr + k * 256));
+            }
+            if constexpr (EPI == kEpiSwiglu) {
+                const float * wur = p.W + (o + p.out_dim) * in + lane * 4;
+#pragma unroll
+                for (int k = 0; k < IN4; ++k) {
+                    wu[r][k] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(wur + k * 256));
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+#pragma unroll
+            for (int k = 0; k < IN4; ++k) {
+                acc[r] = dot4(wv[r][k], xv[k], acc[r]);
+                if constexpr (EPI == kEpiSwiglu) accu[r] = dot4(wu[r][k], xv[k], accu[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const float a = wave_sum_f(acc[r]);
+            float u = 0.0f;
+            if constexpr (EPI == kEpiSwiglu) u = wave_sum_f(accu[r]);
+            const int o = o0 + r;
+            if (lane == 0 && o < p.out_dim) {
+                if constexpr (EPI == kEpiStore) p.y[o] = a;
+                else if constexpr (EPI == kEpiAccum) p.y[o] += a;
+                else p.y[o] = (a / (1.0f + expf(-a))) * u;   // silu(gate) * up (text-decoder.cpp:602)
+            }
+        }
+    }
+}
+
+template <int IN4, int NR, int EPI, bool PRENORM>
+int launch_gemv_t(const GemvParams & p, hipStream_t stream) {
+    const int64_t waves = (static_cast<int64_t>(p.out_dim) + NR - 1) / NR;
+    int64_t blocks = (waves + 3) / 4;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL((gemv_kernel<IN4, NR, EPI, PRENORM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       stream, p);
+    QA_LAUNCH_CHECK("gemv_kernel");
+    return QA_OK;
+}
+
+template <int EPI, bool PRENORM>
+int launch_gemv_in(const GemvParams & p, hipStream_t stream) {
+    switch (p.in_dim) {
+        case 1024: return launch_gemv_t<4, EPI == kEpiSwiglu ? 2 : 4, EPI, PRENORM>(p, stream);
+        case 2048: return launch_gemv_t<8, EPI == kEpiSwiglu ? 2 : 4, EPI, PRENORM>(p, stream);
+        case 3072: return launch_gemv_t<12, EPI == kEpiSwiglu ? 1 : 2, EPI, PRENORM>(p, stream);
+        case 4096: return launch_gemv_t<16, EPI == kEpiSwiglu ? 1 : 2, EPI, PRENORM>(p, stream);
+        case 6144: return launch_gemv_t<24, 1, EPI, PRENORM>(p, stream);
+        default: return fail(QA_ERR_INVALID, "gemv: in_dim must be one of 1024, 2048, 3072, 4096, 6144");
+    }
+}
+
+// ---------------------------------------------------------------- row RMSNorm (T > 1 paths)
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float * x, const float * w, int dim, float eps,
+                                                           float * y) {
+#pragma clang fp contract(off)
+    const int r = blockIdx.x;
+    const float * xr = x + static_cast<int64_t>(r) * dim;
+    float * yr = y + static_cast<int64_t>(r) * dim;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < dim; i += 256) ss += static_cast<double>(xr[i]) * xr[i];
+    ss = wave_sum_d(ss);
+    __shared__ double part[4];
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const double tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float scale = 1.0f / sqrtf(static_cast<float>(tot / static_cast<double>(dim)) + eps);
+    for (int i = threadIdx.x; i < dim; i += 256) yr[i] = xr[i] * scale * w[i];
+}
+
+__global__ void swiglu_rows_kernel(const float * gu, int rows, int dim, float * a) {
+#pragma clang fp contract(off)
+    const int64_t n = static_cast<int64_t>(rows) * dim;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t r = i / dim;
+        const int64_t c = i - r * dim;
+        const float g = gu[r * 2 * dim + c];
+        const float u = gu[r * 2 * dim + dim + c];
+        a[i] = (g / (1.0f + expf(-g))) * u;
+    }
+}
+
+__global__ void add_inplace_kernel(float * y, const float * x, size_t n) {
+    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        y[i] += x[i];
+    }
+}
+
+__global__ void embed_rows_kernel(const float * table, int n_rows, int dim, const int32_t * ids, float * out) {
+    const int r = blockIdx.x;
+    const int id = ids[r];
+    float * o = out + static_cast<int64_t>(r) * dim;
+    if (id < 0 || id >= n_rows) {
+        for (int i = threadIdx.x; i < dim; i += blockDim.x) o[i] = 0.0f;
+        return;
+    }
+    const float * t = table + static_cast<int64_t>(id) * dim;
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) o[i] = t[i];
+}
+
+__global__ void advance_lens_kernel(int32_t * lens, int n, int delta) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) lens[i] += delta;
+}
+
+// ---------------------------------------------------------------- argmax
+// Reference rule (text-decoder.cpp:2266-2274): best = -inf, take i when logits[i] > best, so the
+// lowest index among equal maxima wins, NaN and -inf never win, and -1 means nothing was taken.
+struct Cand {
+    float v;
+    int32_t i;
+};
+
+__device__ inline Cand better(Cand a, Cand b) {
+    if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+    return a;
+}
+
+constexpr int kArgmaxBlocks = 64;
+constexpr int32_t kNoIndex = 0x7fffffff;
+
+__global__ __launch_bounds__(256) void argmax_kernel(const float * logits, int vocab, Cand * partial,
+                                                     uint32_t * counters, int32_t * ids) {
+    const int row = blockIdx.y;
+    const int chunk = (vocab + kArgmaxBlocks - 1) / kArgmaxBlocks;
+    const int lo = blockIdx.x * chunk;
+    const int hi = min(vocab, lo + chunk);
+    const float * lr = logits + static_cast<int64_t>(row) * vocab;
+    Cand c{-INFINITY, kNoIndex};
+    for (int i = lo + static_cast<int>(threadIdx.x); i < hi; i += 256) {
+        const float v = lr[i];
+        if (v > c.v) { c.v = v; c.i = i; }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        Cand o;
+        o.v = __shfl_xor(c.v, off, kWave);
+        o.i = __shfl_xor(c.i, off, kWave);
+        c = better(c, o);
+    }
+    __shared__ Cand wc[4];
+    if ((threadIdx.x & 63) == 0) wc[threadIdx.x >> 6] = c;
+    __syncthreads();
+    __shared__ int is_last;
+    if (threadIdx.x == 0) {
+        Cand b = better(better(wc[0], wc[1]), better(wc[2], wc[3]));
+        partial[row * kArgmaxBlocks + blockIdx.x] = b;
+        __threadfence();
+        const uint32_t old = atomicAdd(counters + row, 1u);
+        is_last = old == kArgmaxBlocks - 1;
+        if (is_last) atomicExch(counters + row, 0u);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    if (threadIdx.x == 0) {
+        Cand b{-INFINITY, kNoIndex};
+        for (int k = 0; k < kArgmaxBlocks; ++k) {
+            Cand o;
+            o.v = __builtin_nontemporal_load(&partial[row * kArgmaxBlocks + k].v);
+            o.i = __builtin_nontemporal_load(&partial[row * kArgmaxBlocks + k].i);
+            b = better(b, o);
+        }
+        ids[row] = b.i == kNoIndex ? -1 : b.i;
+    }
+}
+
+}  // namespace
+
+int gemv_launch(int epi, bool prenorm, const float * W, int32_t out_dim, int32_t in_dim, const float * x,
+                float * y, const float * norm_w, float eps, hipStream_t stream) {
+    GemvParams p{W, x, y, norm_w, out_dim, in_dim, eps};
+    if (!W || !x || !y || out_dim <= 0 || (prenorm && !norm_w)) return fail(QA_ERR_INVALID, "gemv: invalid arguments");
+    if (epi == kEpiStore) return prenorm ? launch_gemv_in<kEpiStore, true>(p, stream) : launch_gemv_in<kEpiStore, false>(p, stream);
+    if (epi == kEpiAccum) return prenorm ? launch_gemv_in<kEpiAccum, true>(p, stream) : launch_gemv_in<kEpiAccum, false>(p, stream);
+    return prenorm ? launch_gemv_in<kEpiSwiglu, true>(p, stream) : launch_gemv_in<kEpiSwiglu, false>(p, stream);
+}
+
+size_t argmax_workspace_bytes(int32_t rows) {
+    return (sizeof(Cand) * kArgmaxBlocks + sizeof(uint32_t)) * static_cast<size_t>(rows) + 256;
+}
+
+int argmax_launch(const float * logits, int32_t rows, int32_t vocab, int32_t * ids, void * workspace,
+                  hipStream_t stream) {
+    Cand * partial = static_cast<Cand *>(workspace);
+    uint32_t * counters = reinterpret_cast<uint32_t *>(partial + static_cast<size_t>(rows) * kArgmaxBlocks);
+    hipLaunchKernelGGL(argmax_kernel, dim3(kArgmaxBlocks, static_cast<unsigned>(rows)), dim3(256), 0, stream,
+                       logits, vocab, partial, counters, ids);
+    QA_LAUNCH_CHECK("argmax_kernel");
+    return QA_OK;
+}
+
+int rmsnorm_rows_launch(const float * x, const float * w, int32_t rows, int32_t dim, float eps, float * y,
+                        hipStream_t stream) {
+    if (rows <= 0) return QA_OK;
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, x, w, dim,
+                       eps, y);
+    QA_LAUNCH_CHECK("rmsnorm_rows_kernel");
+    return QA_OK;
+}
+
+int swiglu_rows_launch(const float * gu, int32_t rows, int32_t dim, float * a, hipStream_t stream) {
+    const int64_t n = static_cast<int64_t>(rows) * dim;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
+    if (blocks <= 0) return QA_OK;
+    hipLaunchKernelGGL(swiglu_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, gu, rows,
+                       dim, a);
+    QA_LAUNCH_CHECK("swiglu_rows_kernel");
+    return QA_OK;
+}
+
+int embed_rows_launch(const float * table, int32_t n_rows, int32_t dim, const int32_t * ids, int32_t rows,
+                      float * out, hipStream_t stream) {
+    if (rows <= 0) return QA_OK;
+    hipLaunchKernelGGL(embed_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, table, n_rows,
+                       dim, ids, out);
+    QA_LAUNCH_CHECK("embed_rows_kernel");
+    return QA_OK;
+}
+
+int advance_lens_launch(int32_t * lens, int32_t n, int32_t delta, hipStream_t stream) {
+    if (n <= 0) return QA_OK;
+    hipLaunchKernelGGL(advance_lens_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
+                       lens, n, delta);
+    QA_LAUNCH_CHECK("advance_lens_kernel");
+    return QA_OK;
+}
+
+}  // namespace qa
+
+extern "C" int qa_gemv(const float * W, int32_t out_dim, int32_t in_dim, const float * x, int32_t rows, float * y,
+                       int32_t accumulate, void * stream) {
+    using namespace qa;
+    for (int32_t r = 0; r < rows; ++r) {
+        const int rc = gemv_launch(accumulate ? kEpiAccum : kEpiStore, false, W, out_dim, in_dim,
+                                   x + static_cast<int64_t>(r) * in_dim, y + static_cast<int64_t>(r) * out_dim,
+                                   nullptr, 0.0f, as_stream(stream));
+        if (rc != QA_OK) return rc;
+    }
+    return QA_OK;
+}
+
+extern "C" size_t qa_argmax_workspace_bytes(int32_t rows) {
+    return rows > 0 ? qa::argmax_workspace_bytes(rows) : 0;
+}
+
+extern "C" int qa_argmax_rows(const float * logits, int32_t rows, int32_t vocab, int32_t * ids, void * workspace,
+                              size_t workspace_bytes, void * stream) {
+    if (!logits || !ids || !workspace || rows <= 0 || vocab <= 0 ||
+        workspace_bytes < qa::argmax_workspace_bytes(rows)) {
+        return qa::fail(QA_ERR_INVALID, "qa_argmax_rows: invalid arguments");
+    }
+    return qa::argmax_launch(logits, rows, vocab, ids, workspace, qa::as_stream(stream));
+}
+
+extern "C" int qa_rmsnorm_rows(const float * x, const float * w, int32_t rows, int32_t dim, float eps, float * y,
+                               void * stream) {
+    if (!x || !w || !y || rows < 0 || dim <= 0) return qa::fail(QA_ERR_INVALID, "qa_rmsnorm_rows: invalid arguments");
+    return qa::rmsnorm_rows_launch(x, w, rows, dim, eps, y, qa::as_stream(stream));
+}
+
+extern "C" int qa_swiglu_rows(const float * gu, int32_t rows, int32_t dim, float * a, void * stream) {
+    if (!gu || !a || rows < 0 || dim <= 0) return qa::fail(QA_ERR_INVALID, "qa_swiglu_rows: invalid arguments");
+    return qa::swiglu_rows_launch(gu, rows, dim, a, qa::as_stream(stream));
+}
+
+extern "C" int qa_add_inplace(float * y, const float * x, size_t n, void * stream) {
+    if (!y || !x) return qa::fail(QA_ERR_INVALID, "qa_add_inplace: null pointer");
+    if (n == 0) return QA_OK;
+    const size_t blocks = std::min<size_t>((n + 255) / 256, 8192);
+    hipLaunchKernelGGL(qa::add_inplace_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       qa::as_stream(stream), y, x, n);
+    QA_LAUNCH_CHECK("add_inplace_kernel");
+    return QA_OK;
+}
+
+extern "C" int qa_embed_rows(const float * table, int32_t n_rows, int32_t dim, const int32_t * ids, int32_t rows,
+                             float * out, void * stream) {
+    if (!table || !ids || !out || dim <= 0) return qa::fail(QA_ERR_INVALID, "qa_embed_rows: invalid arguments");
+    return qa::embed_rows_launch(table, n_rows, dim, ids, rows, out, qa::as_stream(stream));
+}
+
+extern "C" int qa_advance_lens(int32_t * lens, int32_t n, int32_t delta, void * stream) {
+    if (!lens) return qa::fail(QA_ERR_INVALID, "qa_advance_lens: null pointer");
+    return qa::advance_lens_launch(lens, n, delta, qa::as_stream(stream));
+}
+
+namespace qa {
+namespace {
+
+__global__ void set_values_kernel(int32_t * dst, int n, int32_t value) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = value;
+}
+
+// f32 rows -> cache dtype (f16 rounds to nearest even, like ggml_cpy).
+__global__ void cast_rows_kernel(const float * src, void * dst, int f16, int64_t n) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        if (f16) static_cast<_Float16 *>(dst)[i] = static_cast<_Float16>(src[i]);
+        else static_cast<float *>(dst)[i] = src[i];
+    }
+}
+
+}  // namespace
+
+int set_values_launch(int32_t * dst, int32_t n, int32_t value, hipStream_t stream) {
+    if (n <= 0) return QA_OK;
+    hipLaunchKernelGGL(set_values_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, dst,
+                       n, value);
+    QA_LAUNCH_CHECK("set_values_kernel");
+    return QA_OK;
+}
+
+int cast_rows_launch(const float * src, void * dst, int32_t cache_type, int64_t n, hipStream_t stream) {
+    if (n <= 0) return QA_OK;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 16384);
+    hipLaunchKernelGGL(cast_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, src, dst,
+                       cache_type == QA_CACHE_F16 ? 1 : 0, n);
+    QA_LAUNCH_CHECK("cast_rows_kernel");
+    return QA_OK;
+}
+
+}  // namespace qa

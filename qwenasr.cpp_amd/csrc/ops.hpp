@@ -1,0 +1,37 @@
+// Internal launch functions shared by the runtime (not part of the C ABI).
+#pragma once
+
+#include "common.hpp"
+
+namespace qa {
+
+enum { kEpiStoreOp = 0, kEpiAccumOp = 1, kEpiSwigluOp = 2 };
+
+int gemv_launch(int epi, bool prenorm, const float * W, int32_t out_dim, int32_t in_dim, const float * x, float * y,
+                const float * norm_w, float eps, hipStream_t stream);
+size_t argmax_workspace_bytes(int32_t rows);
+int argmax_launch(const float * logits, int32_t rows, int32_t vocab, int32_t * ids, void * workspace,
+                  hipStream_t stream);
+int rmsnorm_rows_launch(const float * x, const float * w, int32_t rows, int32_t dim, float eps, float * y,
+                        hipStream_t stream);
+int swiglu_rows_launch(const float * gu, int32_t rows, int32_t dim, float * a, hipStream_t stream);
+int embed_rows_launch(const float * table, int32_t n_rows, int32_t dim, const int32_t * ids, int32_t rows,
+                      float * out, hipStream_t stream);
+int advance_lens_launch(int32_t * lens, int32_t n, int32_t delta, hipStream_t stream);
+int set_values_launch(int32_t * dst, int32_t n, int32_t value, hipStream_t stream);
+int cast_rows_launch(const float * src, void * dst, int32_t cache_type, int64_t n, hipStream_t stream);
+
+int decode_attn_launch(const float * q, int32_t q_stride, const void * cache, const qa_kv_layout & layout,
+                       int32_t layer, const int32_t * lens, int32_t lens_add, int32_t n_streams, int32_t max_len,
+                       int32_t n_heads, float scale, float * out, void * workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+size_t decode_attn_workspace(int32_t n_streams, int32_t n_heads, int32_t max_len);
+
+int prefill_attn_launch(const float * q, int32_t q_stride, const void * cache, const qa_kv_layout & layout,
+                        int32_t layer, int32_t stream_idx, int32_t n_past, int32_t n_tokens, int32_t n_heads,
+                        float scale, float * out, void * workspace, size_t workspace_bytes, hipStream_t stream);
+int causal_f32_launch(const float * q, int32_t q_stride, const float * k, const float * v, int64_t row_stride,
+                      int32_t n_tokens, int32_t n_heads, int32_t n_kv_heads, float scale, float * out,
+                      hipStream_t stream);
+
+}  // namespace qa

@@ -1,0 +1,153 @@
+"""Decoder-level parity: configs 0-4 on the HIP path against the oracle's golden fixtures, greedy
+token ids identical, bookkeeping (cur_len, device lengths) bit-exact, reference error behaviour."""
+import hashlib
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def digest(*arrays) -> str:
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()[:16]
+
+
+def golden(index):
+    with open(os.path.join(GOLDEN, f"cfg{index}.json")) as f:
+        return json.load(f)
+
+
+def close(got, ref, atol=2e-3, rtol_l2=1e-3):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    err = np.abs(got - ref).max()
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert err <= atol and rel <= rtol_l2, (err, rel)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu(qa):
+    assert qa.device_count() > 0, "no HIP device: GPU tests need the MI355X"
+
+
+def test_cfg0_single_layer_decode(qa):
+    from qwenasr_amd import configs
+
+    g = golden(0)
+    model = qa.Model(configs.CONFIGS[0].size, n_layers=1)
+    x, k, v = configs.cfg0_inputs(model.cfg.hidden)
+    assert digest(x, k, v, model.tensor("text.blk.0.attn_q.weight")) == g["input_digest"]
+    with qa.Decoder(model, 1, 157, qa.QA_CACHE_F32) as dec:
+        dec.fill_cache(0, k, v, 156)
+        assert dec.cur_len(0) == 156 and dec.device_lens().tolist() == [156]
+        y = dec.layer_forward(0, x, 156)
+        close(y[0], g["y"], atol=1e-4, rtol_l2=1e-5)
+        assert dec.cur_len(0) == g["cur_len"] == 157 and dec.device_lens().tolist() == [157]
+        ptr, lay = dec.cache()
+        n = lay.n_layers * 2 * lay.n_streams * lay.n_kv_heads * lay.max_seq * lay.head_dim
+        cache = np.empty(n, np.float32)
+        qa.check(qa.lib.qa_copy_to_host(cache.ctypes.data, ptr, n * 4))
+        cache = cache.reshape(1, 2, 1, 8, 157, 128)
+        close(cache[0, 0, 0, :, 156], g["k_row"], atol=1e-4, rtol_l2=1e-5)
+        close(cache[0, 1, 0, :, 156], g["v_row"], atol=1e-4, rtol_l2=1e-5)
+        np.testing.assert_array_equal(cache[0, 0, 0, :, :156], k[0].astype(np.float32))   # prefix untouched
+
+
+@pytest.mark.parametrize("f16", [True, False])
+def test_small_model_greedy_matches_oracle(qa, orc, f16):
+    """0.6B shapes, 3 layers: greedy ids, stop handling and bookkeeping against an in-test oracle run."""
+    model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=3)
+    om = orc.OracleModel.from_product_model(model)
+    x = qa.prompt_input(model, 40, 9)
+    N = 24
+    ref = om.generate(x, N, qa.STOP_IDS, om.cache(49 + N, f16))
+    with qa.Decoder(model, 1, 49 + N, qa.QA_CACHE_F16 if f16 else qa.QA_CACHE_F32) as dec:
+        out = dec.generate(x, N, margins=True)
+        assert out["ids"] == ref["ids"], (out["margins"], ref["margins"])
+        assert out["total_tokens"] == ref["total_tokens"] and out["stopped"] == ref["stopped"]
+        assert dec.cur_len(0) == ref["cur_len"] == 49 + N - 1
+        assert dec.device_lens().tolist() == [ref["cur_len"]]
+        # stop on the 5th generated id: the loop ends right after emitting it (text-decoder.cpp:2282-2292)
+        stop = dec.generate(x, N, stop_ids=[ref["ids"][4]])
+        first = ref["ids"].index(ref["ids"][4])
+        assert stop["stopped"] and stop["ids"] == ref["ids"][:first + 1]
+        assert dec.cur_len(0) == 49 + first
+        # capacity and argument errors are reported before any device work (text-decoder.cpp:2225-2233)
+        with pytest.raises(qa.QaError) as e:
+            dec.generate(x, N + 1)
+        assert e.value.code == qa.QA_ERR_CAPACITY
+        with pytest.raises(qa.QaError) as e:
+            dec.forward(x[:2], 49 + N - 1)
+        assert e.value.code == qa.QA_ERR_CAPACITY
+        # a cached forward of the prompt matches the oracle's logits
+        logits = dec.forward(x, 0)
+        ref_logits = om.forward_cached(x, 0, om.cache(49 + N, f16))
+        close(logits, ref_logits, atol=1e-3, rtol_l2=1e-4)
+
+
+@pytest.mark.parametrize("index", [1, 2, 3])
+def test_config_greedy_matches_golden(qa, index):
+    from qwenasr_amd import configs
+
+    g = golden(index)
+    w = configs.CONFIGS[index]
+    model = qa.Model(w.size, n_layers=w.n_layers)
+    x = qa.prompt_input(model, w.audio_tokens, w.prompt_tokens)
+    assert digest(x, model.tensor("text.blk.0.attn_q.weight")) == g["input_digest"]
+    print(f"config {index}: prompt {w.prompt}, {w.new_tokens} tokens", flush=True)
+    with qa.Decoder(model, 1, w.max_seq, w.cache_type) as dec:
+        out = dec.generate(x, w.new_tokens, margins=True)
+        first_diff = next((i for i, (a, b) in enumerate(zip(out["ids"], g["ids"])) if a != b), None)
+        assert out["ids"] == g["ids"], (first_diff, g["margins"][first_diff] if first_diff is not None else None)
+        assert out["stopped"] == g["stopped"] and out["total_tokens"] == g["total_tokens"]
+        assert dec.cur_len(0) == g["cur_len"] and dec.device_lens().tolist() == [g["cur_len"]]
+
+
+def test_config4_ragged_streams_match_golden(qa):
+    from qwenasr_amd import configs
+
+    g = golden(4)
+    w = configs.CONFIGS[4]
+    lens = configs.cfg4_lengths(w.streams)
+    first = configs.cfg4_first_ids(w.streams)
+    assert lens.tolist() == g["lengths"] and first.tolist() == g["first_ids"]
+    model = qa.Model(w.size, n_layers=w.n_layers)
+    with qa.Decoder(model, w.streams, w.max_seq, w.cache_type) as dec:
+        for s in range(w.streams):
+            k, v = configs.cfg4_stream_kv(s, int(lens[s]))
+            dec.fill_cache(s, k, v, int(lens[s]))
+            del k, v
+        print("config 4 caches filled", flush=True)
+        ids = dec.decode_streams(first, w.steps)
+        assert ids.shape == (w.steps, w.streams)
+        for s, ref in g["streams"].items():
+            assert ids[:, int(s)].tolist() == ref["ids"], s
+        assert dec.device_lens().tolist() == (lens + w.steps).tolist()
+        assert [dec.cur_len(s) for s in range(w.streams)] == (lens + w.steps).tolist()
+
+
+def test_drop_in_tool_generate(qa, orc):
+    """The text-decoder.h drop-in through the synthetic driver, key=value contract, ids vs the oracle."""
+    tool = os.path.join(ROOT, "qwenasr.cpp_amd", "qwen-asr-text-layer")
+    r = subprocess.run([tool, "--size", "0.6b", "--layers", "2", "--audio-tokens", "20", "--prompt-tokens", "5",
+                        "--generate", "6", "--kv-cache-type", "f16", "--device", "gpu"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    kv = dict(line.split("=", 1) for line in r.stdout.strip().splitlines())
+    model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=2)
+    om = orc.OracleModel.from_product_model(model)
+    ref = om.generate(qa.prompt_input(model, 20, 5), 6, qa.STOP_IDS, om.cache(31, True))
+    assert kv["generated_ids"] == ",".join(map(str, ref["ids"]))
+    assert int(kv["prompt_tokens"]) == 25 and int(kv["total_tokens"]) == ref["total_tokens"]
+    assert kv["stopped"] == ("true" if ref["stopped"] else "false")
+    r = subprocess.run([tool, "--size", "0.6b", "--layers", "1", "--device", "cpu", "--generate", "2"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 1 and "not available" in r.stderr

@@ -1,16 +1,21 @@
 """Decode benchmark of the MI355X Qwen3-ASR text decoder (BASELINE metric, one GPU).
 
-    python bench.py [--gpus 1] [--steps 64] [--warmup 8] [--config 3] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--config 3] [--no-cpu-baseline]
 
 Workload (config 3): Qwen3-ASR-1.7B decoder, seeded N(0, 0.02) f32 weights, f16 KV cache, prefill of
-3913 positions (3900 audio rows N(0, 1) + 13 random prompt ids), then greedy decode at ~4k context.
-A step is one decode token: embedding gather, 28 layers (fused K/V append, split-K attention, f32
-GEMVs), LM head and device argmax.  value = decode tokens/s over exactly --steps steps, inputs and
-weights resident in HBM, bracketed by device synchronisation.
+3913 positions (3900 audio rows + 13 random prompt ids), then greedy decode at ~4k context.
+A step is one decode token: embedding gather, 28 layers (q|k|v GEMV, fused K/V append + split-K
+attention, o / gate-up / down GEMVs), LM head and device argmax.  value = decode tokens/s over exactly
+--steps steps, weights and cache resident in HBM, bracketed by device synchronisation.
 
-Also reported: the decode attention's achieved HBM bandwidth (algorithmic bytes 4096 * L + 16384 per
-layer call, timed with HIP events on the decoder stream), prefill time, and the CPU oracle's decode
-rate on a bounded sample (cpu_baseline, kind "port").
+roofline: the decode-step attention of one layer (fused K/V append + split-K attention: the scores
+and values kernels).  Its average duration per layer is measured with HIP events on the decoder's
+stream around a back-to-back loop at the benchmark's context, rotating through all 28 layer caches
+so the 256 MB MALL cannot serve them (470 MB of KV per token).  Algorithmic bytes per launch =
+4096 * L + 16384 (K and V rows of L positions in f16, plus q in and o out in f32).
+
+cpu_baseline: the CPU oracle (oracle/qa_oracle.c, a restatement of the reference's graph
+semantics, OpenMP) decoding a bounded number of tokens of the same model at the same context.
 """
 from __future__ import annotations
 
@@ -31,17 +36,21 @@ def log(msg: str):
     print(msg, file=sys.stderr, flush=True)
 
 
+def host_cores() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return min(n, 16)   # the GPU box grants 16 host cores per GPU
+
+
 def cpu_baseline(model, length: int, steps: int):
     """Oracle decode steps of the same model at the same context (cache rows N(0, 1), f16)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import qa_oracle as orc
     import qwenasr_amd as qa
 
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count() or 1
-    cores = min(cores, 16)
+    cores = host_cores()
     orc.set_threads(cores)
     om = orc.OracleModel.from_product_model(model)
     c = model.cfg
@@ -56,23 +65,73 @@ def cpu_baseline(model, length: int, steps: int):
     om.decode_steps(cache, 1234, steps)
     dt = time.perf_counter() - t0
     return dict(value=round(steps / dt, 4), unit="tok/s", cores=cores, kind="port",
-                sample=f"{steps} oracle decode steps of the 1.7B decoder at context {length + 1}..{length + steps + 1}, "
-                       f"f16 cache, {dt:.1f} s")
+                sample=f"{steps} decode steps of the 1.7B decoder by the CPU oracle (C, OpenMP, {cores} threads) at "
+                       f"context {length + 1}..{length + steps + 1}, f16 cache, {dt:.1f} s")
+
+
+def attention_roofline(qa, dec, reps: int):
+    """Average duration of one layer's decode-step attention (fused append + split-K attention: the
+    scores and values kernels), back to back on the decoder stream, HIP events from the C ABI."""
+    import ctypes as C
+
+    import numpy as np
+
+    lay = qa.KvLayout()
+    cache = qa.lib.qa_decoder_cache(dec.handle, C.byref(lay))
+    s_ptr = qa.lib.qa_decoder_stream(dec.handle)
+    cfg = dec.cfg
+    q_dim, kv_dim = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    ctx = dec.cur_len(0)                       # the kernels append at row ctx and attend ctx + 1 rows
+    assert ctx + 1 <= lay.max_seq
+    qkv = qa.DeviceArray.from_numpy(np.random.default_rng(5).standard_normal((1, q_dim + 2 * kv_dim)).astype(np.float32))
+    ones = qa.DeviceArray.from_numpy(np.ones(cfg.head_dim, np.float32))
+    n_past = qa.DeviceArray.from_numpy(np.array([ctx], np.int32))
+    out = qa.DeviceArray((1, q_dim))
+    ws_bytes = qa.lib.qa_decode_attn_workspace_bytes(lay.n_streams, cfg.n_heads, lay.max_seq)
+    ws = qa.DeviceArray(ws_bytes, np.uint8)
+    qa.synchronize()
+    scale = 1.0 / (cfg.head_dim ** 0.5)
+
+    def launch(layer):
+        qa.check(qa.lib.qa_decode_step_attn(qkv.ptr, ones.ptr, ones.ptr, C.c_void_p(cache), C.byref(lay), layer,
+                                            n_past.ptr, 1, ctx + 1, cfg.n_heads, cfg.rope_theta, cfg.rms_norm_eps,
+                                            scale, out.ptr, ws.ptr, ws_bytes, C.c_void_p(s_ptr)))
+
+    for layer in range(lay.n_layers):          # warm
+        launch(layer)
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    qa.check(qa.lib.qa_event_create(C.byref(e0)))
+    qa.check(qa.lib.qa_event_create(C.byref(e1)))
+    qa.check(qa.lib.qa_event_record(e0, C.c_void_p(s_ptr)))
+    for _ in range(reps):
+        for layer in range(lay.n_layers):
+            launch(layer)
+    qa.check(qa.lib.qa_event_record(e1, C.c_void_p(s_ptr)))
+    ms = C.c_float()
+    qa.check(qa.lib.qa_event_elapsed_ms(e0, e1, C.byref(ms)))
+    qa.lib.qa_event_destroy(e0)
+    qa.lib.qa_event_destroy(e1)
+    n = reps * lay.n_layers
+    us = ms.value * 1e3 / n
+    L = ctx + 1
+    bytes_per_launch = 4096 * L + 16384
+    return us, L, bytes_per_launch, n
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--config", type=int, default=3, choices=[2, 3])
-    ap.add_argument("--profile-steps", type=int, default=16)
-    ap.add_argument("--cpu-steps", type=int, default=8)
+    ap.add_argument("--roofline-reps", type=int, default=20)
+    ap.add_argument("--profile-steps", type=int, default=8)
+    ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the KV-cache path shards by "
-              "KV head or by stream, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the KV-cache path would shard by "
+              "KV head or by stream); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
@@ -104,23 +163,27 @@ def main():
     ids = dec.decode_streams(np.array([last], np.int32), args.steps)
     qa.check(qa.lib.qa_device_synchronize())
     dt = time.perf_counter() - t0
-    log(f"timed {args.steps} decode steps at context {ctx0}..{ctx0 + args.steps}: {dt * 1e3:.1f} ms")
+    log(f"timed {args.steps} decode steps at context {ctx0}..{ctx0 + args.steps}: {dt * 1e3:.1f} ms "
+        f"({dt * 1e3 / args.steps:.3f} ms/token)")
 
-    # attention roofline: HIP events around every decode-attention call on the decoder stream
+    # per-step device time by kernel family (HIP events around each family; events add gaps, so these
+    # are upper bounds used only for the breakdown)
     dec.profile(True)
     dec.profile_reset()
-    ctx1 = dec.cur_len(0)
     dec.decode_streams(np.array([int(ids[-1, 0])], np.int32), args.profile_steps)
-    fam = {f: dec.profile_read(f) for f in ("decode_attn", "kv_append", "projections", "logits")}
+    fam = {f: dec.profile_read(f) for f in ("decode_attn", "projections", "logits")}
     dec.profile(False)
-    attn_ms, attn_n = fam["decode_attn"]
-    attn_us = attn_ms * 1e3 / attn_n
-    L_avg = ctx1 + 1 + (args.profile_steps - 1) / 2.0
-    attn_bytes = 4096.0 * L_avg + 16384.0
-    achieved = attn_bytes / (attn_us * 1e-6) / 1e9
-    log("per-step device time by family (ms): " +
+    log("per-step device time by family, event-bracketed (ms): " +
         ", ".join(f"{k} {v[0] / args.profile_steps:.3f}" for k, v in fam.items()))
 
+    attn_us, L, attn_bytes, n_launch = attention_roofline(qa, dec, args.roofline_reps)
+    achieved = attn_bytes / (attn_us * 1e-6) / 1e9
+    log(f"decode-step attention: {attn_us:.2f} us per launch over {n_launch} launches at L={L}: "
+        f"{achieved:.0f} GB/s")
+
+    weight_bytes = int(4 * sum(model.tensor(n).size for n in (
+        [f"text.blk.{l}.{t}.weight" for l in range(model.cfg.n_layers) for t in
+         ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")] + ["text.output.weight"])))
     result = {
         "metric": METRIC,
         "value": round(args.steps / dt, 3),
@@ -133,19 +196,20 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) audio rows, random prompt ids)",
+        "data": "synthetic (seeded N(0,0.02) f32 weights, N(0,1) audio rows, random prompt ids)",
         "config": {"workload": f"config {args.config}: {w.size.name} decoder, prefill {w.prompt} positions, greedy "
-                               f"decode at context {ctx0}..{ctx0 + args.steps}, f16 KV cache, f32 weights, batch 1",
+                               f"decode of {args.steps} tokens at context {ctx0}..{ctx0 + args.steps}, f16 KV cache, "
+                               f"f32 weights, batch 1",
                    "kv_cache": "f16", "prompt_positions": w.prompt},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode attention (decode_scores_kernel + decode_values_kernel) per layer call",
-                     "bytes_per_launch": round(attn_bytes), "avg_launch_us": round(attn_us, 3)},
+                     "kernel": "decode attention of one layer: decode_scores_kernel (fused K/V append) + "
+                               "decode_values_kernel, launched back to back",
+                     "bytes_per_launch": attn_bytes, "attended_positions": L, "avg_launch_us": round(attn_us, 3)},
         "attn_us_per_layer": round(attn_us, 3),
         "prefill_ms": round(prefill_ms, 2),
-        "weight_bytes_per_token": int(4 * sum(model.tensor(n).size for n in (
-            [f"text.blk.{l}.{t}.weight" for l in range(model.cfg.n_layers) for t in
-             ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")] + ["text.output.weight"]))),
+        "weight_bytes_per_token": weight_bytes,
+        "weight_stream_gbs": round(weight_bytes / (dt / args.steps) / 1e9, 1),
     }
     dec.close()
     if not args.no_cpu_baseline:

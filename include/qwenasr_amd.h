@@ -50,6 +50,19 @@ int qa_copy_to_host(void * host_dst, const void * dev_src, size_t bytes);
 /* Waits for all work on device 0 (hipDeviceSynchronize). */
 int qa_device_synchronize(void);
 
+/* Device memory, copies and timing on device 0, so hosts (tests, benchmarks, FFI callers) need no
+ * second HIP runtime of their own.  stream NULL is the default stream. */
+int qa_device_malloc(void ** out, size_t bytes);
+int qa_device_free(void * dev_ptr);
+int qa_copy_to_device(void * dev_dst, const void * host_src, size_t bytes);
+int qa_memset_device(void * dev_dst, int value, size_t bytes);
+int qa_event_create(void ** event);
+int qa_event_destroy(void * event);
+int qa_event_record(void * event, void * stream);
+/* Waits for `stop`, then ms = time between the two recorded events. */
+int qa_event_elapsed_ms(void * start, void * stop, float * ms);
+int qa_stream_synchronize(void * stream);
+
 /* ---------------------------------------------------------------- KV cache layout (rows a1, a2)
  * One allocation holds K and V for every layer and stream.  Element (layer, kv, stream, head, pos, i)
  * with kv = 0 for K and 1 for V lives at element index
@@ -106,21 +119,38 @@ int qa_kv_append(const float * qkv, const float * q_norm_w, const float * k_norm
                  const int32_t * n_past, int32_t n_streams, int32_t n_tokens, int32_t n_heads,
                  float rope_theta, float eps, void * stream);
 
-/* Split-K GQA decode attention over the cache (row a6), one query token per stream.
+/* Split-K GQA decode attention over the cache (row a6), one query token per stream (two launches:
+ * scores + chunk statistics, then normalised PV + merge).
  * q       : [n_streams][q_dim] f32 (post norm + RoPE), out: [n_streams][q_dim] f32.
  * lens    : device int32[n_streams]; stream s attends positions [0, lens[s]).  Every lens[s] must be
  *           in [1, max_len] and max_len <= layout->max_seq.
  * Q head h reads KV head h / (n_heads / n_kv_heads) (text-decoder.cpp:725, 1035).
  * Arithmetic is that of the reference's GGML graph (text-decoder.cpp:454-461) for the cache dtype:
- *   f16 cache: s_j = f32dot(f16(q), K_j); p = softmax(s * scale) with the sum in double; p -> f16;
- *              o = f32dot(p, V).   f32 cache: no f16 rounding of q or p.
- * workspace: device scratch of qa_decode_attn_workspace_bytes() bytes.  Its counters must be zero
- * before the first call (qa_workspace_clear); every call leaves them zero again.                */
-size_t qa_decode_attn_workspace_bytes(int32_t n_streams, int32_t n_heads, int32_t max_len);
+ *   f16 cache: s_j = f32dot(f16(q), K_j) * scale; p = expf(s - max) * (float)(1 / sum), the sum in
+ *              double; p -> f16; o = f32dot(p, V).   f32 cache: no f16 rounding of q or p.
+ * workspace: device scratch of qa_decode_attn_workspace_bytes(layout->n_streams, n_heads,
+ * layout->max_seq) bytes, i.e. sized by the cache CAPACITY so its internal offsets never move.  Its
+ * counters must be zero before the first call (qa_workspace_clear); every call leaves them zero
+ * again, so one workspace serves any sequence of calls on that cache.  Calls that share a
+ * workspace must be stream-ordered.                                                             */
+size_t qa_decode_attn_workspace_bytes(int32_t n_streams, int32_t n_heads, int32_t max_seq);
 int qa_workspace_clear(void * workspace, size_t bytes, void * stream);
 int qa_decode_attn(const float * q, const void * cache, const qa_kv_layout * layout, int32_t layer,
                    const int32_t * lens, int32_t n_streams, int32_t max_len, int32_t n_heads,
                    float scale, float * out, void * workspace, size_t workspace_bytes, void * stream);
+
+/* One decode step of a layer's KV-cache path with the append fused in (rows a5 + a6): for each stream s,
+ * the token at position n_past[s] is appended and attended.  qkv: [n_streams][q_dim + 2 * kv_dim]
+ * raw projection rows (q | k | v).  The kernel applies q_norm/k_norm RMSNorm and NEOX RoPE exactly
+ * as qa_kv_append does (same bits), writes the new K and V rows into the cache at n_past[s], and
+ * computes what qa_decode_attn computes over positions [0, n_past[s] + 1).  n_past[s] + 1 must be
+ * in [1, max_len], max_len <= layout->max_seq.  n_past itself is not advanced (qa_advance_lens).
+ * out: [n_streams][q_dim].  Workspace as for qa_decode_attn.  Equals qa_kv_append followed by
+ * qa_decode_attn on lens = n_past + 1 (text-decoder.cpp:410-463 at T = 1).                      */
+int qa_decode_step_attn(const float * qkv, const float * q_norm_w, const float * k_norm_w, void * cache,
+                        const qa_kv_layout * layout, int32_t layer, const int32_t * n_past, int32_t n_streams,
+                        int32_t max_len, int32_t n_heads, float rope_theta, float eps, float scale, float * out,
+                        void * workspace, size_t workspace_bytes, void * stream);
 
 /* Causal prefill attention over the cache (row a7): the n_tokens queries of stream `stream_idx` at
  * positions n_past .. n_past + n_tokens - 1, query t attending keys [0, n_past + t].  Same

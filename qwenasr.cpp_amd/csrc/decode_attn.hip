@@ -1,32 +1,60 @@
-// Split-K GQA decode attention over the KV cache, gfx950.
+// Split-K GQA decode attention over the KV cache (flash-decoding), gfx950.
 //
 // Replaces the decode half of backend_text_layer_forward_cached_ggml (text-decoder.cpp:435-463):
 //   scores = mul_mat(K[0,L), q); soft_max_ext(scores, mask, 1/sqrt(d)); out = mul_mat(cont(V^T), p)
 // including the transposed copy of V that the reference materialises on every call (459): V is read
-// row-wise here, so each K and V byte of the prefix is read from HBM exactly once.
+// row-wise here, so each K and V byte of the attended prefix is read from HBM exactly once.
 //
-// The reference's arithmetic with an f16 cache rounds q to f16 before QK^T and the *normalised*
-// probabilities to f16 before PV (GGML mul_mat converts src1 to src0's dot type).  Normalised p needs
-// the global max and sum before any PV, so the work is split in two launches:
-//   K pass  grid (split, kv_head, stream): scores of both query heads of the group for 64 positions,
-//           written to the workspace with that split's max and sum(exp(x - max)) (sum in double).
-//   V pass  same grid: global max/sum from the split stats, p = f16(expf(x - max) * (1/sum)),
-//           partial o for the split, then the last workgroup of each (stream, kv_head) adds the
-//           partials in split order and writes o.  Its counter is reset by that same workgroup, so no
-//           memset is ever needed between calls (the launch sequence is graph-capturable).
-// Memory layout inside a split: 16 lanes cover one 128-wide row (8 elements = 16 B of f16 per lane),
-// so one wave load fetches 4 consecutive rows = 1 KB; both query heads of the GQA group use every
-// loaded K/V element from registers, which is where the reference's broadcast of KV head h/2 lives.
+// Arithmetic = the reference's GGML graph for the cache dtype (f32 precision):
+//   s_j = f32dot(q, K_j) * scale, q rounded to f16 first when K is f16 (GGML's mul_mat converts src1
+//   to the f16 dot type of src0); max over j; sum of expf(s_j - max) in double;
+//   p_j = expf(s_j - max) * (float)(1 / sum), rounded to f16 when V is f16 (same conversion rule);
+//   o = f32 sum of p_j V_j.
+// The f16 rounding of the NORMALISED p needs the global max and sum before any PV, so the work is two
+// launches over the same (chunk, KV head, stream) grid:
+//   scores kernel  K rows of the chunk -> scores of both query heads of the GQA group (workspace) and
+//                  the chunk's max m_c and double sum_j expf(s_j - m_c);
+//   values kernel  global max M and sum S = sum_c sum_c * exp(m_c - M) from the chunk statistics,
+//                  p_j, the chunk's partial o, and the merge: the last workgroup of each
+//                  (stream, KV head) adds the partials in chunk order.
+// Dropping the p rounding would allow a single-pass launch, but it moves logits by up to ~1e-3 and
+// flips greedy near-ties against the reference semantics; identical greedy ids are the contract.
+//
+// Work decomposition.  One workgroup (4 waves) owns CHUNK consecutive positions of one KV head of one
+// stream and serves both query heads of the group (Q head h reads KV head h / 2,
+// text-decoder.cpp:725, 1035), so every K/V byte loaded feeds two dot products from registers.
+// 16 lanes cover one 128-wide row (8 elements per lane, one 16-byte load for f16); one wave load
+// instruction fetches 4 consecutive rows (1 KB of f16).  A workgroup issues every load of its chunk
+// before the first arithmetic, so the whole chunk is in flight at once.
+// blockIdx.x = chunk * n_kv + kv_head: consecutive workgroups (round-robin over the 8 XCDs) walk the
+// KV heads of one chunk.
+//
+// Merge without fences.  The partial o of a chunk is published with agent-scope atomic stores and
+// read back by the merging workgroup with agent-scope atomic loads (both coherent across XCDs by
+// themselves), ordered by a vmcnt wait before the counter increment.  A release/acquire fence would
+// order plain stores instead, at the price of writing back and invalidating the whole L2 of the XCD
+// in every workgroup, which costs more than the attention itself.  The counter is reset by the
+// merging workgroup, so the workspace never needs clearing between calls.
+//
+// Fused mode (the decode step of the runtime): the scores kernel takes the raw q|k|v projection row
+// and does the append itself.  Every workgroup normalises and rotates its two query heads (the same
+// function, hence the same bits, as the append kernel); the workgroup that owns the new position
+// normalises and rotates k, casts k and v to the cache dtype and writes both rows into the cache, and
+// uses the new K row from LDS.  The values kernel then reads the new V row from the cache: the
+// reference's append-then-attend order (the cpy nodes precede attention, text-decoder.cpp:432-433)
+// without a separate append launch.
 #include "ops.hpp"
+#include "prep.hpp"
 
 #include <cmath>
+#include <cstdlib>
 
 namespace qa {
 namespace {
 
-constexpr int kSplit = 64;          // positions per workgroup
-constexpr int kThreads = 256;       // 4 waves, 16 positions each
-constexpr int kRep = 2;             // query heads per KV head (Qwen3-ASR: 16 / 8)
+constexpr int kThreads = 256;   // 4 waves
+constexpr int kRep = 2;         // query heads per KV head (Qwen3-ASR: 16 / 8)
+constexpr int kMinChunk = 32;   // the workspace is laid out for the smallest chunk size
 
 struct SplitStat {
     float m;
@@ -35,18 +63,21 @@ struct SplitStat {
 };
 
 struct DecodeParams {
-    const float * q;          // [S][q_stride]
-    const void * cache;
-    float * out;              // [S][q_stride]
-    const int32_t * lens;     // attended length = lens[s] + lens_add
-    float * scores;           // [S][H][score_stride]
-    SplitStat * stats;        // [S][H][max_splits]
-    float * partial;          // [S][max_splits][H][128]
-    uint32_t * counters;      // [S][n_kv]
+    const float * q;          // [S][q_stride] prepared q; fused mode: raw q|k|v rows [S][q_stride]
+    void * cache;
+    float * out;              // [S][out_stride]
+    const int32_t * lens;     // attended length = lens[s] + lens_add, clamped to [0, max_len]
+    float * scores;           // [S_cap][n_heads][score_stride]
+    SplitStat * stats;        // [S_cap][n_heads][max_chunks]
+    float * partial;          // [S_cap][n_kv][max_chunks][2][128]
+    uint32_t * counters;      // [S_cap][n_kv]
+    const float * q_norm_w;   // fused mode only
+    const float * k_norm_w;
+    float eps;
     int32_t lens_add;
-    int32_t q_stride;
+    int32_t q_stride, out_stride;
     int32_t n_heads, n_kv_heads, n_streams, max_seq, layer;
-    int32_t max_len, max_splits, score_stride;
+    int32_t max_len, max_chunks, score_stride;
     float scale;
 };
 
@@ -56,163 +87,271 @@ struct Workspace {
 
 inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
-Workspace workspace_layout(int32_t n_streams, int32_t n_heads, int32_t max_len) {
-    const size_t splits = (static_cast<size_t>(max_len) + kSplit - 1) / kSplit;
-    const size_t stride = splits * kSplit;
+// Sized from the cache capacity (streams x max_seq), never from a call's length, so the offsets of
+// the counters stay fixed for the lifetime of a workspace.
+Workspace workspace_layout(int32_t n_streams, int32_t n_kv, int32_t max_seq) {
+    const size_t chunks = (static_cast<size_t>(max_seq) + kMinChunk - 1) / kMinChunk;
+    const size_t units = static_cast<size_t>(n_streams) * n_kv;
     Workspace w{};
     w.scores = 0;
-    w.stats = align256(w.scores + sizeof(float) * n_streams * n_heads * stride);
-    w.partial = align256(w.stats + sizeof(SplitStat) * n_streams * n_heads * splits);
-    w.counters = align256(w.partial + sizeof(float) * n_streams * splits * n_heads * kHeadDim);
-    w.total = align256(w.counters + sizeof(uint32_t) * n_streams * (n_heads / kRep));
+    w.stats = align256(w.scores + sizeof(float) * units * kRep * chunks * kMinChunk);
+    w.partial = align256(w.stats + sizeof(SplitStat) * units * kRep * chunks);
+    w.counters = align256(w.partial + sizeof(float) * units * chunks * kRep * kHeadDim);
+    w.total = align256(w.counters + sizeof(uint32_t) * units);
     return w;
 }
 
+// 8 consecutive elements of a cache row: raw bits are loaded first (all loads in flight), converted
+// to f32 when used.
 template <typename CT>
-struct RowSlice;
+struct Slice;
 
-// 8 consecutive elements of a row as floats (16 B load for f16, 2 x 16 B for f32).
 template <>
-struct RowSlice<_Float16> {
-    static __device__ inline void load(const _Float16 * p, float (&v)[8]) {
-        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-        const h8 x = *reinterpret_cast<const h8 *>(p);
+struct Slice<_Float16> {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    h8 x;
+    __device__ inline void load(const _Float16 * p) { x = *reinterpret_cast<const h8 *>(p); }
+    __device__ inline void zero() {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = static_cast<float>(x[i]);
+        for (int i = 0; i < 8; ++i) x[i] = static_cast<_Float16>(0.0f);
     }
+    __device__ inline float get(int i) const { return static_cast<float>(x[i]); }
+    __device__ inline void set(int i, float v) { x[i] = static_cast<_Float16>(v); }
 };
 
 template <>
-struct RowSlice<float> {
-    static __device__ inline void load(const float * p, float (&v)[8]) {
-        const float4 a = *reinterpret_cast<const float4 *>(p);
-        const float4 b = *reinterpret_cast<const float4 *>(p + 4);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+struct Slice<float> {
+    float4 a, b;
+    __device__ inline void load(const float * p) {
+        a = *reinterpret_cast<const float4 *>(p);
+        b = *reinterpret_cast<const float4 *>(p + 4);
+    }
+    __device__ inline void zero() {
+        a = make_float4(0.f, 0.f, 0.f, 0.f);
+        b = a;
+    }
+    __device__ inline float get(int i) const {
+        switch (i) {
+            case 0: return a.x; case 1: return a.y; case 2: return a.z; case 3: return a.w;
+            case 4: return b.x; case 5: return b.y; case 6: return b.z; default: return b.w;
+        }
+    }
+    __device__ inline void set(int i, float v) {
+        switch (i) {
+            case 0: a.x = v; break; case 1: a.y = v; break; case 2: a.z = v; break; case 3: a.w = v; break;
+            case 4: b.x = v; break; case 5: b.y = v; break; case 6: b.z = v; break; default: b.w = v; break;
+        }
     }
 };
 
 __device__ inline float round_f16(float x) { return static_cast<float>(static_cast<_Float16>(x)); }
 
-__device__ inline float group16_sum(float v) {
+// Sum over the 16 lanes that hold one row (lane bits 0-3).
+__device__ inline float row_sum16(float v) {
 #pragma unroll
     for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
     return v;
 }
 
-template <typename CT, bool R16>
-__global__ __launch_bounds__(kThreads) void decode_scores_kernel(DecodeParams p) {
-    const int c = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
-    const int L = min(p.lens[s] + p.lens_add, p.max_len);   // never past the rows the launch was sized for
-    const int row0 = c * kSplit;
-    if (row0 >= L) return;
+__device__ inline void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ inline void publish(float * p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline int attended(const DecodeParams & p, int s) {
+    return min(max(p.lens[s] + p.lens_add, 0), p.max_len);
+}
+
+template <typename CT, bool R16, int CHUNK, bool FUSED>
+__global__ __launch_bounds__(kThreads) void decode_scores_kernel(DecodeParams p, RopeTable rope) {
+    constexpr int RPT = CHUNK / 16;   // rows per lane: 16 rows per workgroup pass
+    const int g = static_cast<int>(blockIdx.x) % p.n_kv_heads;
+    const int c = static_cast<int>(blockIdx.x) / p.n_kv_heads;
+    const int s = blockIdx.y;
+    const int L = attended(p, s);
+    if (c * CHUNK >= L) return;                      // uniform for the whole workgroup
+
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x >> 6;
-    const int sub = lane >> 4;
-    const int part = lane & 15;
+    const int sub = lane >> 4;                        // row within the wave's 4-row group
+    const int part = lane & 15;                       // 8-element slice of the row
     const int h0 = g * kRep;
+    const int row0 = c * CHUNK + wave * (CHUNK / 4);  // each wave: CHUNK / 4 consecutive rows
+    const int pos_new = L - 1;                        // fused mode: the token being appended
+    const bool owner = FUSED && pos_new / CHUNK == c;
+
+    CT * kc = static_cast<CT *>(p.cache) +
+              cache_row_offset(p.layer, 0, s, g, 0, p.n_streams, p.n_kv_heads, p.max_seq);
+    const CT * kb = kc + part * 8;
+
+    Slice<CT> ks[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        const int j = row0 + k * 4 + sub;
+        if (j < L && !(FUSED && j == pos_new)) ks[k].load(kb + static_cast<int64_t>(j) * kHeadDim);
+        else ks[k].zero();
+    }
 
     float q0[8], q1[8];
-    {
+    if (FUSED) {
+        // waves 0/1: the two query heads; waves 2/3 of the owner: k (norm + RoPE) and v of the new row
+        __shared__ float s_q[kRep][kHeadDim];
+        __shared__ float s_k[kHeadDim];
+        const float * row = p.q + static_cast<int64_t>(s) * p.q_stride;
+        const int q_dim = p.n_heads * kHeadDim;
+        if (wave < 2) {
+            float a = row[(h0 + wave) * kHeadDim + lane];
+            float b = row[(h0 + wave) * kHeadDim + lane + 64];
+            norm_rope_pair(a, b, p.q_norm_w, p.eps, pos_new, rope, lane);
+            s_q[wave][lane] = a;
+            s_q[wave][lane + 64] = b;
+        } else if (owner) {
+            const bool is_k = wave == 2;
+            const float * src = row + q_dim + (is_k ? 0 : p.n_kv_heads * kHeadDim) + g * kHeadDim;
+            float a = src[lane];
+            float b = src[lane + 64];
+            if (is_k) norm_rope_pair(a, b, p.k_norm_w, p.eps, pos_new, rope, lane);
+            const CT ca = static_cast<CT>(a), cb = static_cast<CT>(b);
+            const int64_t v_delta = cache_row_offset(0, 1, 0, 0, 0, p.n_streams, p.n_kv_heads, p.max_seq);
+            CT * dst = kc + (is_k ? 0 : v_delta) + static_cast<int64_t>(pos_new) * kHeadDim;
+            dst[lane] = ca;
+            dst[lane + 64] = cb;
+            if (is_k) {
+                s_k[lane] = static_cast<float>(ca);
+                s_k[lane + 64] = static_cast<float>(cb);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            q0[i] = s_q[0][part * 8 + i];
+            q1[i] = s_q[1][part * 8 + i];
+        }
+        if (owner) {
+#pragma unroll
+            for (int k = 0; k < RPT; ++k) {
+                if (row0 + k * 4 + sub == pos_new) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) ks[k].set(i, s_k[part * 8 + i]);
+                }
+            }
+        }
+    } else {
         const float * qp = p.q + static_cast<int64_t>(s) * p.q_stride + h0 * kHeadDim + part * 8;
-        RowSlice<float>::load(qp, q0);
-        RowSlice<float>::load(qp + kHeadDim, q1);
-        if (R16) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) { q0[i] = round_f16(q0[i]); q1[i] = round_f16(q1[i]); }
-        }
+        const float4 a = *reinterpret_cast<const float4 *>(qp);
+        const float4 b = *reinterpret_cast<const float4 *>(qp + 4);
+        const float4 e = *reinterpret_cast<const float4 *>(qp + kHeadDim);
+        const float4 f = *reinterpret_cast<const float4 *>(qp + kHeadDim + 4);
+        q0[0] = a.x; q0[1] = a.y; q0[2] = a.z; q0[3] = a.w; q0[4] = b.x; q0[5] = b.y; q0[6] = b.z; q0[7] = b.w;
+        q1[0] = e.x; q1[1] = e.y; q1[2] = e.z; q1[3] = e.w; q1[4] = f.x; q1[5] = f.y; q1[6] = f.z; q1[7] = f.w;
     }
-    const CT * kbase = static_cast<const CT *>(p.cache) +
-        cache_row_offset(p.layer, 0, s, g, 0, p.n_streams, p.n_kv_heads, p.max_seq) + part * 8;
+    if (R16) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { q0[i] = round_f16(q0[i]); q1[i] = round_f16(q1[i]); }
+    }
 
-    float kv[4][8];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int j = row0 + wave * 16 + k * 4 + sub;
-        if (j < L) {
-            RowSlice<CT>::load(kbase + static_cast<int64_t>(j) * kHeadDim, kv[k]);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) kv[k][i] = 0.0f;
-        }
-    }
-    float x0[4], x1[4];
+    // scores of both heads; every lane of a 16-lane row group ends with the full row sum
+    float x0[RPT], x1[RPT];
     float m0 = -INFINITY, m1 = -INFINITY;
+    float * sc0 = p.scores + (static_cast<int64_t>(s) * p.n_heads + h0) * p.score_stride;
+    float * sc1 = sc0 + p.score_stride;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < RPT; ++k) {
         float a = 0.0f, b = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            a = fmaf(q0[i], kv[k][i], a);
-            b = fmaf(q1[i], kv[k][i], b);
+            const float kv = ks[k].get(i);
+            a = fmaf(q0[i], kv, a);
+            b = fmaf(q1[i], kv, b);
         }
-        a = group16_sum(a) * p.scale;
-        b = group16_sum(b) * p.scale;
-        const int j = row0 + wave * 16 + k * 4 + sub;
+        a = row_sum16(a) * p.scale;
+        b = row_sum16(b) * p.scale;
+        const int j = row0 + k * 4 + sub;
         const bool valid = j < L;
+        if (valid && part == 0) {
+            sc0[j] = a;
+            sc1[j] = b;
+        }
         x0[k] = valid ? a : -INFINITY;
         x1[k] = valid ? b : -INFINITY;
-        if (valid && part == 0) {
-            float * sp = p.scores + (static_cast<int64_t>(s) * p.n_heads + h0) * p.score_stride + j;
-            sp[0] = a;
-            sp[p.score_stride] = b;
-        }
         m0 = fmaxf(m0, x0[k]);
         m1 = fmaxf(m1, x1[k]);
     }
-    // max over the 4 row groups of the wave, then over the 4 waves
     m0 = fmaxf(m0, __shfl_xor(m0, 16, kWave)); m0 = fmaxf(m0, __shfl_xor(m0, 32, kWave));
     m1 = fmaxf(m1, __shfl_xor(m1, 16, kWave)); m1 = fmaxf(m1, __shfl_xor(m1, 32, kWave));
-    __shared__ float smax[2][4];
-    __shared__ double ssum[2][4];
-    if (lane == 0) { smax[0][wave] = m0; smax[1][wave] = m1; }
+    __shared__ float s_max[kRep][4];
+    __shared__ double s_sum[kRep][4];
+    if (lane == 0) { s_max[0][wave] = m0; s_max[1][wave] = m1; }
     __syncthreads();
-    m0 = fmaxf(fmaxf(smax[0][0], smax[0][1]), fmaxf(smax[0][2], smax[0][3]));
-    m1 = fmaxf(fmaxf(smax[1][0], smax[1][1]), fmaxf(smax[1][2], smax[1][3]));
+    m0 = fmaxf(fmaxf(s_max[0][0], s_max[0][1]), fmaxf(s_max[0][2], s_max[0][3]));
+    m1 = fmaxf(fmaxf(s_max[1][0], s_max[1][1]), fmaxf(s_max[1][2], s_max[1][3]));
 
     double e0 = 0.0, e1 = 0.0;
     if (part == 0) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < RPT; ++k) {
             if (x0[k] != -INFINITY) e0 += static_cast<double>(expf(x0[k] - m0));
             if (x1[k] != -INFINITY) e1 += static_cast<double>(expf(x1[k] - m1));
         }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        e0 += __shfl_xor(e0, off, kWave);
-        e1 += __shfl_xor(e1, off, kWave);
-    }
-    if (lane == 0) { ssum[0][wave] = e0; ssum[1][wave] = e1; }
+    e0 += __shfl_xor(e0, 16, kWave); e0 += __shfl_xor(e0, 32, kWave);
+    e1 += __shfl_xor(e1, 16, kWave); e1 += __shfl_xor(e1, 32, kWave);
+    if (lane == 0) { s_sum[0][wave] = e0; s_sum[1][wave] = e1; }
     __syncthreads();
-    if (threadIdx.x < 2) {
+    if (threadIdx.x < kRep) {
         const int h = threadIdx.x;
         SplitStat st;
         st.m = h == 0 ? m0 : m1;
         st.pad = 0.0f;
-        st.s = (ssum[h][0] + ssum[h][1]) + (ssum[h][2] + ssum[h][3]);
-        p.stats[(static_cast<int64_t>(s) * p.n_heads + h0 + h) * p.max_splits + c] = st;
+        st.s = (s_sum[h][0] + s_sum[h][1]) + (s_sum[h][2] + s_sum[h][3]);
+        p.stats[(static_cast<int64_t>(s) * p.n_heads + h0 + h) * p.max_chunks + c] = st;
     }
 }
 
-template <typename CT, bool R16>
+template <typename CT, bool R16, int CHUNK>
 __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p) {
-    const int c = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
-    const int L = min(p.lens[s] + p.lens_add, p.max_len);   // never past the rows the launch was sized for
-    const int n_splits = (L + kSplit - 1) / kSplit;
-    if (c >= n_splits) return;
-    const int row0 = c * kSplit;
+    constexpr int RPT = CHUNK / 16;
+    const int g = static_cast<int>(blockIdx.x) % p.n_kv_heads;
+    const int c = static_cast<int>(blockIdx.x) / p.n_kv_heads;
+    const int s = blockIdx.y;
+    const int L = attended(p, s);
+    const int n_chunks = (L + CHUNK - 1) / CHUNK;
+    if (c >= n_chunks) return;
+
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x >> 6;
     const int sub = lane >> 4;
     const int part = lane & 15;
     const int h0 = g * kRep;
+    const int row0 = c * CHUNK + wave * (CHUNK / 4);
 
-    // global max and sum of the two heads from the split statistics (every wave, redundantly)
-    const SplitStat * st0 = p.stats + (static_cast<int64_t>(s) * p.n_heads + h0) * p.max_splits;
-    const SplitStat * st1 = st0 + p.max_splits;
+    // V rows and the scores of the chunk in flight first
+    const CT * vb = static_cast<const CT *>(p.cache) +
+                    cache_row_offset(p.layer, 1, s, g, 0, p.n_streams, p.n_kv_heads, p.max_seq) + part * 8;
+    const float * sc0 = p.scores + (static_cast<int64_t>(s) * p.n_heads + h0) * p.score_stride;
+    const float * sc1 = sc0 + p.score_stride;
+    Slice<CT> vs[RPT];
+    float x0[RPT], x1[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        const int j = row0 + k * 4 + sub;
+        if (j < L) {
+            vs[k].load(vb + static_cast<int64_t>(j) * kHeadDim);
+            x0[k] = sc0[j];
+            x1[k] = sc1[j];
+        } else {
+            vs[k].zero();
+            x0[k] = -INFINITY;
+            x1[k] = -INFINITY;
+        }
+    }
+
+    // global max and sum of both heads from the chunk statistics (every wave, redundantly)
+    const SplitStat * st0 = p.stats + (static_cast<int64_t>(s) * p.n_heads + h0) * p.max_chunks;
+    const SplitStat * st1 = st0 + p.max_chunks;
     float M0 = -INFINITY, M1 = -INFINITY;
-    for (int i = lane; i < n_splits; i += kWave) {
+    for (int i = lane; i < n_chunks; i += kWave) {
         M0 = fmaxf(M0, st0[i].m);
         M1 = fmaxf(M1, st1[i].m);
     }
@@ -222,7 +361,7 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
         M1 = fmaxf(M1, __shfl_xor(M1, off, kWave));
     }
     double S0 = 0.0, S1 = 0.0;
-    for (int i = lane; i < n_splits; i += kWave) {
+    for (int i = lane; i < n_chunks; i += kWave) {
         S0 += st0[i].s * exp(static_cast<double>(st0[i].m) - static_cast<double>(M0));
         S1 += st1[i].s * exp(static_cast<double>(st1[i].m) - static_cast<double>(M1));
     }
@@ -234,80 +373,164 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
     const float r0 = static_cast<float>(1.0 / S0);
     const float r1 = static_cast<float>(1.0 / S1);
 
-    const CT * vbase = static_cast<const CT *>(p.cache) +
-        cache_row_offset(p.layer, 1, s, g, 0, p.n_streams, p.n_kv_heads, p.max_seq) + part * 8;
-    const float * sc0 = p.scores + (static_cast<int64_t>(s) * p.n_heads + h0) * p.score_stride;
-    const float * sc1 = sc0 + p.score_stride;
-
-    float vv[4][8];
-    float p0[4], p1[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int j = row0 + wave * 16 + k * 4 + sub;
-        if (j < L) {
-            RowSlice<CT>::load(vbase + static_cast<int64_t>(j) * kHeadDim, vv[k]);
-            float a = expf(sc0[j] - M0) * r0;
-            float b = expf(sc1[j] - M1) * r1;
-            if (R16) { a = round_f16(a); b = round_f16(b); }
-            p0[k] = a;
-            p1[k] = b;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) vv[k][i] = 0.0f;
-            p0[k] = 0.0f;
-            p1[k] = 0.0f;
-        }
-    }
     float a0[8], a1[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) { a0[i] = 0.0f; a1[i] = 0.0f; }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < RPT; ++k) {
+        float pa = x0[k] == -INFINITY ? 0.0f : expf(x0[k] - M0) * r0;
+        float pb = x1[k] == -INFINITY ? 0.0f : expf(x1[k] - M1) * r1;
+        if (R16) { pa = round_f16(pa); pb = round_f16(pb); }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            a0[i] = fmaf(p0[k], vv[k][i], a0[i]);
-            a1[i] = fmaf(p1[k], vv[k][i], a1[i]);
+            const float v = vs[k].get(i);
+            a0[i] = fmaf(pa, v, a0[i]);
+            a1[i] = fmaf(pb, v, a1[i]);
         }
     }
+    // reduce over the 4 row groups of the wave (lane bits 4-5), then over the 4 waves in LDS
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         a0[i] += __shfl_xor(a0[i], 16, kWave); a0[i] += __shfl_xor(a0[i], 32, kWave);
         a1[i] += __shfl_xor(a1[i], 16, kWave); a1[i] += __shfl_xor(a1[i], 32, kWave);
     }
-    __shared__ float red[4][kRep][kHeadDim];
+    __shared__ float s_o[4][kRep][kHeadDim];
     if (sub == 0) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            red[wave][0][part * 8 + i] = a0[i];
-            red[wave][1][part * 8 + i] = a1[i];
+            s_o[wave][0][part * 8 + i] = a0[i];
+            s_o[wave][1][part * 8 + i] = a1[i];
         }
     }
     __syncthreads();
-    const int hh = threadIdx.x >> 7;          // 0..1
+    const int hh = threadIdx.x >> 7;               // query head of the group this thread finishes
     const int d = threadIdx.x & (kHeadDim - 1);
-    const float sum = (red[0][hh][d] + red[1][hh][d]) + (red[2][hh][d] + red[3][hh][d]);
-    float * part_out = p.partial +
-        ((static_cast<int64_t>(s) * p.max_splits + c) * p.n_heads + h0 + hh) * kHeadDim;
-    part_out[d] = sum;
+    const float o = (s_o[0][hh][d] + s_o[1][hh][d]) + (s_o[2][hh][d] + s_o[3][hh][d]);
+    float * out = p.out + static_cast<int64_t>(s) * p.out_stride + (h0 + hh) * kHeadDim + d;
+    if (n_chunks == 1) {
+        *out = o;
+        return;
+    }
 
-    __threadfence();
+    const int64_t unit = static_cast<int64_t>(s) * p.n_kv_heads + g;
+    float * part_base = p.partial + unit * p.max_chunks * (kRep * kHeadDim);
+    publish(part_base + static_cast<int64_t>(c) * (kRep * kHeadDim) + threadIdx.x, o);
+    // every wave's stores have completed before any wave passes the barrier; then count
+    wait_vmem();
     __syncthreads();
-    __shared__ int is_last;
+    __shared__ int s_last;
     if (threadIdx.x == 0) {
-        uint32_t * ctr = p.counters + static_cast<int64_t>(s) * p.n_kv_heads + g;
-        const uint32_t old = atomicAdd(ctr, 1u);
-        is_last = old == static_cast<uint32_t>(n_splits - 1);
-        if (is_last) atomicExch(ctr, 0u);
+        uint32_t * ctr = p.counters + unit;
+        const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == static_cast<uint32_t>(n_chunks - 1);
+        if (s_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    const float * pp = p.partial +
-        (static_cast<int64_t>(s) * p.max_splits * p.n_heads + h0 + hh) * kHeadDim + d;
-    const int64_t step = static_cast<int64_t>(p.n_heads) * kHeadDim;
-    float acc = 0.0f;
-    for (int i = 0; i < n_splits; ++i) acc += __builtin_nontemporal_load(pp + i * step);
-    p.out[static_cast<int64_t>(s) * p.q_stride + (h0 + hh) * kHeadDim + d] = acc;
+    if (!s_last) return;
+
+    // Sum of the partials: thread t owns the float pair j = t % 128 of the 256-float state and the
+    // chunks c = t / 128, t / 128 + 2, ...; up to 32 8-byte loads per thread in flight at once.  The
+    // two chunk groups are then added in LDS.  Fixed order, so the result is deterministic.
+    const int pair = threadIdx.x & 127;
+    const int grp = threadIdx.x >> 7;
+    const uint64_t * pp = reinterpret_cast<const uint64_t *>(part_base) + pair;
+    constexpr int kStride = kRep * kHeadDim / 2;    // uint64 per chunk state
+    float acc_lo = 0.0f, acc_hi = 0.0f;
+    int i = grp;
+    for (; i + 2 * 31 < n_chunks; i += 2 * 32) {
+        uint64_t v[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) {
+            v[u] = __hip_atomic_load(pp + static_cast<int64_t>(i + 2 * u) * kStride, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int u = 0; u < 32; ++u) {
+            acc_lo += __uint_as_float(static_cast<uint32_t>(v[u]));
+            acc_hi += __uint_as_float(static_cast<uint32_t>(v[u] >> 32));
+        }
+    }
+    for (; i < n_chunks; i += 2) {
+        const uint64_t v = __hip_atomic_load(pp + static_cast<int64_t>(i) * kStride, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        acc_lo += __uint_as_float(static_cast<uint32_t>(v));
+        acc_hi += __uint_as_float(static_cast<uint32_t>(v >> 32));
+    }
+    __shared__ float s_acc[2][kRep * kHeadDim];
+    s_acc[grp][2 * pair] = acc_lo;
+    s_acc[grp][2 * pair + 1] = acc_hi;
+    __syncthreads();
+    *out = s_acc[0][threadIdx.x] + s_acc[1][threadIdx.x];
+}
+
+// Positions per workgroup.  Short single-stream prefixes want more, smaller chunks (more
+// workgroups in flight); many streams already fill the chip and favour fewer partial states.
+int pick_chunk(int32_t n_streams, int32_t n_kv, int32_t max_len) {
+    static const int forced = [] {
+        const char * e = std::getenv("QA_DECODE_CHUNK");
+        return e ? std::atoi(e) : 0;
+    }();
+    if (forced == 32 || forced == 64 || forced == 128) return forced;
+    const int64_t wg64 = static_cast<int64_t>(n_streams) * n_kv * ((max_len + 63) / 64);
+    if (wg64 < 1024) return 32;
+    if (wg64 < 8192) return 64;
+    return 128;
+}
+
+template <typename CT, bool R16, int CHUNK>
+void launch_pair(bool fused, dim3 grid, const DecodeParams & p, const RopeTable & rope, hipStream_t stream) {
+    if (fused) {
+        hipLaunchKernelGGL((decode_scores_kernel<CT, R16, CHUNK, true>), grid, dim3(kThreads), 0, stream, p, rope);
+    } else {
+        hipLaunchKernelGGL((decode_scores_kernel<CT, R16, CHUNK, false>), grid, dim3(kThreads), 0, stream, p, rope);
+    }
+    hipLaunchKernelGGL((decode_values_kernel<CT, R16, CHUNK>), grid, dim3(kThreads), 0, stream, p);
+}
+
+template <typename CT, bool R16>
+void launch_chunk(int chunk, bool fused, dim3 grid, const DecodeParams & p, const RopeTable & rope,
+                  hipStream_t stream) {
+    switch (chunk) {
+        case 32: launch_pair<CT, R16, 32>(fused, grid, p, rope, stream); break;
+        case 64: launch_pair<CT, R16, 64>(fused, grid, p, rope, stream); break;
+        default: launch_pair<CT, R16, 128>(fused, grid, p, rope, stream); break;
+    }
+}
+
+int launch_decode(DecodeParams p, bool fused, const RopeTable & rope, const qa_kv_layout & layout,
+                  int32_t n_streams, void * workspace, size_t workspace_bytes, hipStream_t stream) {
+    const int chunk = pick_chunk(n_streams, layout.n_kv_heads, p.max_len);
+    const Workspace w = workspace_layout(layout.n_streams, layout.n_kv_heads, layout.max_seq);
+    if (!workspace || workspace_bytes < w.total) {
+        return fail(QA_ERR_INVALID, "decode attention: workspace too small for the cache capacity");
+    }
+    char * base = static_cast<char *>(workspace);
+    p.scores = reinterpret_cast<float *>(base + w.scores);
+    p.stats = reinterpret_cast<SplitStat *>(base + w.stats);
+    p.partial = reinterpret_cast<float *>(base + w.partial);
+    p.counters = reinterpret_cast<uint32_t *>(base + w.counters);
+    p.n_kv_heads = layout.n_kv_heads;
+    p.n_streams = layout.n_streams;
+    p.max_seq = layout.max_seq;
+    p.max_chunks = (layout.max_seq + kMinChunk - 1) / kMinChunk;
+    p.score_stride = p.max_chunks * kMinChunk;
+    const int32_t grid_chunks = (p.max_len + chunk - 1) / chunk;
+    const dim3 grid(static_cast<unsigned>(grid_chunks * layout.n_kv_heads), static_cast<unsigned>(n_streams));
+    if (layout.cache_type == QA_CACHE_F16) launch_chunk<_Float16, true>(chunk, fused, grid, p, rope, stream);
+    else launch_chunk<float, false>(chunk, fused, grid, p, rope, stream);
+    QA_LAUNCH_CHECK("decode attention kernels");
+    return QA_OK;
+}
+
+int check_shape(const qa_kv_layout & layout, int32_t n_streams, int32_t max_len, int32_t n_heads, int32_t layer) {
+    if (layout.head_dim != kHeadDim || n_heads != kRep * layout.n_kv_heads) {
+        return fail(QA_ERR_INVALID, "decode attention: only head_dim 128 with 2 query heads per KV head");
+    }
+    if (n_streams <= 0 || n_streams > layout.n_streams || max_len <= 0 || max_len > layout.max_seq ||
+        layer < 0 || layer >= layout.n_layers) {
+        return fail(QA_ERR_INVALID, "decode attention: invalid streams, length or layer");
+    }
+    return QA_OK;
 }
 
 }  // namespace
@@ -316,63 +539,57 @@ int decode_attn_launch(const float * q, int32_t q_stride, const void * cache, co
                        int32_t layer, const int32_t * lens, int32_t lens_add, int32_t n_streams,
                        int32_t max_len, int32_t n_heads, float scale, float * out, void * workspace,
                        size_t workspace_bytes, hipStream_t stream) {
-    if (layout.head_dim != kHeadDim || n_heads != kRep * layout.n_kv_heads) {
-        return fail(QA_ERR_INVALID, "decode attention: only head_dim 128 with 2 query heads per KV head");
-    }
-    if (n_streams <= 0 || n_streams > layout.n_streams || max_len <= 0 || max_len > layout.max_seq ||
-        layer < 0 || layer >= layout.n_layers) {
-        return fail(QA_ERR_INVALID, "decode attention: invalid streams, length or layer");
-    }
-    const Workspace w = workspace_layout(n_streams, n_heads, max_len);
-    if (!workspace || workspace_bytes < w.total) {
-        return fail(QA_ERR_INVALID, "decode attention: workspace too small");
-    }
-    char * base = static_cast<char *>(workspace);
+    const int rc = check_shape(layout, n_streams, max_len, n_heads, layer);
+    if (rc != QA_OK) return rc;
     DecodeParams p{};
     p.q = q;
-    p.cache = cache;
+    p.cache = const_cast<void *>(cache);
     p.out = out;
     p.lens = lens;
     p.lens_add = lens_add;
-    p.scores = reinterpret_cast<float *>(base + w.scores);
-    p.stats = reinterpret_cast<SplitStat *>(base + w.stats);
-    p.partial = reinterpret_cast<float *>(base + w.partial);
-    p.counters = reinterpret_cast<uint32_t *>(base + w.counters);
     p.q_stride = q_stride;
+    p.out_stride = n_heads * kHeadDim;
     p.n_heads = n_heads;
-    p.n_kv_heads = layout.n_kv_heads;
-    p.n_streams = layout.n_streams;
-    p.max_seq = layout.max_seq;
     p.layer = layer;
     p.max_len = max_len;
-    p.max_splits = (max_len + kSplit - 1) / kSplit;
-    p.score_stride = p.max_splits * kSplit;
     p.scale = scale;
-    const dim3 grid(static_cast<unsigned>(p.max_splits), static_cast<unsigned>(layout.n_kv_heads),
-                    static_cast<unsigned>(n_streams));
-    if (layout.cache_type == QA_CACHE_F16) {
-        hipLaunchKernelGGL((decode_scores_kernel<_Float16, true>), grid, dim3(kThreads), 0, stream, p);
-        QA_LAUNCH_CHECK("decode_scores_kernel");
-        hipLaunchKernelGGL((decode_values_kernel<_Float16, true>), grid, dim3(kThreads), 0, stream, p);
-        QA_LAUNCH_CHECK("decode_values_kernel");
-    } else {
-        hipLaunchKernelGGL((decode_scores_kernel<float, false>), grid, dim3(kThreads), 0, stream, p);
-        QA_LAUNCH_CHECK("decode_scores_kernel");
-        hipLaunchKernelGGL((decode_values_kernel<float, false>), grid, dim3(kThreads), 0, stream, p);
-        QA_LAUNCH_CHECK("decode_values_kernel");
-    }
-    return QA_OK;
+    return launch_decode(p, false, RopeTable{}, layout, n_streams, workspace, workspace_bytes, stream);
 }
 
-size_t decode_attn_workspace(int32_t n_streams, int32_t n_heads, int32_t max_len) {
-    if (n_streams <= 0 || n_heads <= 0 || max_len <= 0) return 0;
-    return workspace_layout(n_streams, n_heads, max_len).total;
+int decode_step_attn_launch(const float * qkv, const float * q_norm_w, const float * k_norm_w, void * cache,
+                            const qa_kv_layout & layout, int32_t layer, const int32_t * n_past, int32_t n_streams,
+                            int32_t max_len, int32_t n_heads, float rope_theta, float eps, float scale, float * out,
+                            void * workspace, size_t workspace_bytes, hipStream_t stream) {
+    const int rc = check_shape(layout, n_streams, max_len, n_heads, layer);
+    if (rc != QA_OK) return rc;
+    DecodeParams p{};
+    p.q = qkv;
+    p.cache = cache;
+    p.out = out;
+    p.lens = n_past;
+    p.lens_add = 1;
+    p.q_norm_w = q_norm_w;
+    p.k_norm_w = k_norm_w;
+    p.eps = eps;
+    p.q_stride = (n_heads + 2 * layout.n_kv_heads) * kHeadDim;
+    p.out_stride = n_heads * kHeadDim;
+    p.n_heads = n_heads;
+    p.layer = layer;
+    p.max_len = max_len;
+    p.scale = scale;
+    return launch_decode(p, true, make_rope_table(rope_theta), layout, n_streams, workspace, workspace_bytes, stream);
+}
+
+size_t decode_attn_workspace(int32_t n_streams, int32_t n_kv_heads, int32_t max_seq) {
+    if (n_streams <= 0 || n_kv_heads <= 0 || max_seq <= 0) return 0;
+    return workspace_layout(n_streams, n_kv_heads, max_seq).total;
 }
 
 }  // namespace qa
 
-extern "C" size_t qa_decode_attn_workspace_bytes(int32_t n_streams, int32_t n_heads, int32_t max_len) {
-    return qa::decode_attn_workspace(n_streams, n_heads, max_len);
+extern "C" size_t qa_decode_attn_workspace_bytes(int32_t n_streams, int32_t n_heads, int32_t max_seq) {
+    if (n_heads <= 0 || n_heads % qa::kRep != 0) return 0;
+    return qa::decode_attn_workspace(n_streams, n_heads / qa::kRep, max_seq);
 }
 
 extern "C" int qa_decode_attn(const float * q, const void * cache, const qa_kv_layout * layout, int32_t layer,
@@ -383,4 +600,17 @@ extern "C" int qa_decode_attn(const float * q, const void * cache, const qa_kv_l
     if (!q || !cache || !lens || !out) return fail(QA_ERR_INVALID, "qa_decode_attn: null pointer");
     return decode_attn_launch(q, n_heads * kHeadDim, cache, *layout, layer, lens, 0, n_streams, max_len,
                               n_heads, scale, out, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int qa_decode_step_attn(const float * qkv, const float * q_norm_w, const float * k_norm_w, void * cache,
+                                   const qa_kv_layout * layout, int32_t layer, const int32_t * n_past,
+                                   int32_t n_streams, int32_t max_len, int32_t n_heads, float rope_theta, float eps,
+                                   float scale, float * out, void * workspace, size_t workspace_bytes, void * stream) {
+    using namespace qa;
+    if (qa_kv_layout_check(layout) != QA_OK) return QA_ERR_INVALID;
+    if (!qkv || !q_norm_w || !k_norm_w || !cache || !n_past || !out) {
+        return fail(QA_ERR_INVALID, "qa_decode_step_attn: null pointer");
+    }
+    return decode_step_attn_launch(qkv, q_norm_w, k_norm_w, cache, *layout, layer, n_past, n_streams, max_len, n_heads,
+                                   rope_theta, eps, scale, out, workspace, workspace_bytes, as_stream(stream));
 }

@@ -198,24 +198,23 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past)
         rc = causal_f32_launch(d->qkv, W3, d->qkv + QD, d->qkv + QD + KD, W3, rows, c.n_heads, c.n_kv_heads,
                                d->scale, d->attn, s);
         if (rc != QA_OK) return rc;
+    } else if (kind == kDecode) {
+        // append + attend in one launch: one token per stream at position d_lens[s]
+        Prof pr(d, kFamDecodeAttn);
+        rc = decode_step_attn_launch(d->qkv, L.q_norm, L.k_norm, d->cache, d->layout, l, d->d_lens, rows,
+                                     host_max_len(d, rows, 1), c.n_heads, c.rope_theta, c.rms_norm_eps, d->scale,
+                                     d->attn, d->attn_ws, d->attn_ws_bytes, s);
+        if (rc != QA_OK) return rc;
     } else {
         {
             Prof pr(d, kFamAppend);
-            rc = qa_kv_append(d->qkv, L.q_norm, L.k_norm, d->qrot, d->cache, &d->layout, l, d->d_lens,
-                              kind == kDecode ? rows : 1, kind == kDecode ? 1 : rows, c.n_heads, c.rope_theta,
-                              c.rms_norm_eps, s);
+            rc = qa_kv_append(d->qkv, L.q_norm, L.k_norm, d->qrot, d->cache, &d->layout, l, d->d_lens, 1, rows,
+                              c.n_heads, c.rope_theta, c.rms_norm_eps, s);
             if (rc != QA_OK) return rc;
         }
-        if (kind == kDecode) {
-            Prof pr(d, kFamDecodeAttn);
-            rc = decode_attn_launch(d->qrot, QD, d->cache, d->layout, l, d->d_lens, 1, rows,
-                                    host_max_len(d, rows, 1), c.n_heads, d->scale, d->attn, d->attn_ws,
-                                    d->attn_ws_bytes, s);
-        } else {
-            Prof pr(d, kFamPrefillAttn);
-            rc = prefill_attn_launch(d->qrot, QD, d->cache, d->layout, l, 0, n_past, rows, c.n_heads, d->scale,
-                                     d->attn, nullptr, 0, s);
-        }
+        Prof pr(d, kFamPrefillAttn);
+        rc = prefill_attn_launch(d->qrot, QD, d->cache, d->layout, l, 0, n_past, rows, c.n_heads, d->scale,
+                                 d->attn, nullptr, 0, s);
         if (rc != QA_OK) return rc;
     }
     Prof pr(d, kFamProj);
@@ -382,7 +381,7 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
     rc = rc ? rc : dmalloc_t(d->weight_allocs, static_cast<size_t>(n_streams), &d->d_lens);
     rc = rc ? rc : dmalloc_t(d->weight_allocs, static_cast<size_t>(n_streams), &d->d_ids);
     rc = rc ? rc : dmalloc_t(d->weight_allocs, static_cast<size_t>(n_streams) * cfg->vocab, &d->logits);
-    d->attn_ws_bytes = decode_attn_workspace(n_streams, cfg->n_heads, max_seq);
+    d->attn_ws_bytes = decode_attn_workspace(n_streams, cfg->n_kv_heads, max_seq);
     rc = rc ? rc : dmalloc(d->weight_allocs, d->attn_ws_bytes, &d->attn_ws);
     d->am_ws_bytes = argmax_workspace_bytes(n_streams);
     rc = rc ? rc : dmalloc(d->weight_allocs, d->am_ws_bytes, &d->am_ws);

@@ -8,6 +8,7 @@
 // (rms_norm_row 542-557, apply_rope_position 604-625): squares summed in double, float scale,
 // (x * scale) * w, angles in double from a host-computed inv_freq table, no FMA contraction.
 #include "ops.hpp"
+#include "prep.hpp"
 
 #include <cmath>
 
@@ -38,12 +39,6 @@ struct PrepParams {
     float eps;
 };
 
-__device__ inline double wave_sum_d(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
-}
-
 template <int MODE>
 __global__ __launch_bounds__(256) void qkv_prep_kernel(PrepParams p, RopeTable rope) {
 #pragma clang fp contract(off)
@@ -67,19 +62,8 @@ __global__ __launch_bounds__(256) void qkv_prep_kernel(PrepParams p, RopeTable r
 
     if (slot < p.n_heads + p.n_kv_heads) {
         const bool is_q = slot < p.n_heads;
-        const float * w = is_q ? p.q_norm_w : p.k_norm_w;
-        const double ss = wave_sum_d(static_cast<double>(a) * a + static_cast<double>(b) * b);
-        const double ms = ss / static_cast<double>(kHeadDim);
-        const float scale = 1.0f / sqrtf(static_cast<float>(ms) + p.eps);
-        a = a * scale * w[lane];
-        b = b * scale * w[lane + 64];
-
-        double sn, cs;
-        sincos(static_cast<double>(pos) * rope.inv_freq[lane], &sn, &cs);
-        const float c = static_cast<float>(cs);
-        const float s = static_cast<float>(sn);
-        const float ra = a * c - b * s;
-        const float rb = b * c + a * s;
+        norm_rope_pair(a, b, is_q ? p.q_norm_w : p.k_norm_w, p.eps, pos, rope, lane);
+        const float ra = a, rb = b;
 
         if (MODE == kPrepInPlace) {
             src[lane] = ra;

@@ -25,7 +25,11 @@ int decode_attn_launch(const float * q, int32_t q_stride, const void * cache, co
                        int32_t layer, const int32_t * lens, int32_t lens_add, int32_t n_streams, int32_t max_len,
                        int32_t n_heads, float scale, float * out, void * workspace, size_t workspace_bytes,
                        hipStream_t stream);
-size_t decode_attn_workspace(int32_t n_streams, int32_t n_heads, int32_t max_len);
+int decode_step_attn_launch(const float * qkv, const float * q_norm_w, const float * k_norm_w, void * cache,
+                            const qa_kv_layout & layout, int32_t layer, const int32_t * n_past, int32_t n_streams,
+                            int32_t max_len, int32_t n_heads, float rope_theta, float eps, float scale, float * out,
+                            void * workspace, size_t workspace_bytes, hipStream_t stream);
+size_t decode_attn_workspace(int32_t n_streams, int32_t n_kv_heads, int32_t max_seq);
 
 int prefill_attn_launch(const float * q, int32_t q_stride, const void * cache, const qa_kv_layout & layout,
                         int32_t layer, int32_t stream_idx, int32_t n_past, int32_t n_tokens, int32_t n_heads,

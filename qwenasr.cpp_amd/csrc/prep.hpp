@@ -1,0 +1,39 @@
+// Per-head RMSNorm + NEOX RoPE of one 128-wide head row, computed by one wavefront.
+//
+// Lane i holds elements i and i + 64, which is exactly one NEOX rotation pair, so the norm needs one
+// wave reduction and the rotation needs no data exchange.  The arithmetic follows the reference's
+// scalar statement (rms_norm_row, text-decoder.cpp:542-557; apply_rope_position, 604-625):
+// squares summed in double, scale = 1 / sqrtf(float(ms) + eps), (x * scale) * w, angle = pos * inv_freq
+// in double with inv_freq = exp(-ln(theta) * 2i / d) computed on the host in double, no FMA
+// contraction.  Every kernel that prepares q or k goes through this one function, so the fused decode
+// kernel and the separate append kernel produce identical bits.
+#pragma once
+
+#include "common.hpp"
+
+namespace qa {
+
+__device__ inline double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// a = x[lane], b = x[lane + 64] in, rotated pair out.
+__device__ inline void norm_rope_pair(float & a, float & b, const float * w, float eps, int pos,
+                                      const RopeTable & rope, int lane) {
+#pragma clang fp contract(off)
+    const double ss = wave_sum_d(static_cast<double>(a) * a + static_cast<double>(b) * b);
+    const double ms = ss / static_cast<double>(kHeadDim);
+    const float scale = 1.0f / sqrtf(static_cast<float>(ms) + eps);
+    const float na = a * scale * w[lane];
+    const float nb = b * scale * w[lane + 64];
+    double sn, cs;
+    sincos(static_cast<double>(pos) * rope.inv_freq[lane], &sn, &cs);
+    const float c = static_cast<float>(cs);
+    const float s = static_cast<float>(sn);
+    a = na * c - nb * s;
+    b = nb * c + na * s;
+}
+
+}  // namespace qa

@@ -66,6 +66,66 @@ extern "C" int qa_device_synchronize(void) {
     return QA_OK;
 }
 
+// ------------------------------------------------------------------------------------------ memory, events
+extern "C" int qa_device_malloc(void ** out, size_t bytes) {
+    if (!out) return fail(QA_ERR_INVALID, "qa_device_malloc: null output");
+    *out = nullptr;
+    if (qa_device_count() <= 0) return fail(QA_ERR_NO_DEVICE, "qa_device_malloc: no HIP device");
+    if (hipMalloc(out, bytes ? bytes : 1) != hipSuccess) {
+        *out = nullptr;
+        return fail(QA_ERR_ALLOC, "qa_device_malloc: device allocation failed");
+    }
+    return QA_OK;
+}
+
+extern "C" int qa_device_free(void * p) {
+    if (p) QA_HIP(hipFree(p));
+    return QA_OK;
+}
+
+extern "C" int qa_copy_to_device(void * dev_dst, const void * host_src, size_t bytes) {
+    if (!dev_dst || !host_src) return fail(QA_ERR_INVALID, "qa_copy_to_device: null pointer");
+    QA_HIP(hipMemcpy(dev_dst, host_src, bytes, hipMemcpyHostToDevice));
+    return QA_OK;
+}
+
+extern "C" int qa_memset_device(void * dev_dst, int value, size_t bytes) {
+    if (!dev_dst) return fail(QA_ERR_INVALID, "qa_memset_device: null pointer");
+    QA_HIP(hipMemset(dev_dst, value, bytes));
+    return QA_OK;
+}
+
+extern "C" int qa_event_create(void ** out) {
+    if (!out) return fail(QA_ERR_INVALID, "qa_event_create: null output");
+    hipEvent_t e = nullptr;
+    QA_HIP(hipEventCreate(&e));
+    *out = e;
+    return QA_OK;
+}
+
+extern "C" int qa_event_destroy(void * ev) {
+    if (ev) QA_HIP(hipEventDestroy(static_cast<hipEvent_t>(ev)));
+    return QA_OK;
+}
+
+extern "C" int qa_event_record(void * ev, void * stream) {
+    if (!ev) return fail(QA_ERR_INVALID, "qa_event_record: null event");
+    QA_HIP(hipEventRecord(static_cast<hipEvent_t>(ev), as_stream(stream)));
+    return QA_OK;
+}
+
+extern "C" int qa_event_elapsed_ms(void * start, void * stop, float * ms) {
+    if (!start || !stop || !ms) return fail(QA_ERR_INVALID, "qa_event_elapsed_ms: null argument");
+    QA_HIP(hipEventSynchronize(static_cast<hipEvent_t>(stop)));
+    QA_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)));
+    return QA_OK;
+}
+
+extern "C" int qa_stream_synchronize(void * stream) {
+    QA_HIP(hipStreamSynchronize(as_stream(stream)));
+    return QA_OK;
+}
+
 // ------------------------------------------------------------------------------------------ layout
 extern "C" int qa_kv_layout_check(const qa_kv_layout * l) {
     if (!l) return fail(QA_ERR_INVALID, "null KV layout");

@@ -73,6 +73,15 @@ SIGNATURES = {
     "qa_device_arch": (C.c_int, C.c_char_p, sz),
     "qa_copy_to_host": (C.c_int, vp, vp, sz),
     "qa_device_synchronize": (C.c_int,),
+    "qa_device_malloc": (C.c_int, C.POINTER(vp), sz),
+    "qa_device_free": (C.c_int, vp),
+    "qa_copy_to_device": (C.c_int, vp, vp, sz),
+    "qa_memset_device": (C.c_int, vp, C.c_int, sz),
+    "qa_event_create": (C.c_int, C.POINTER(vp)),
+    "qa_event_destroy": (C.c_int, vp),
+    "qa_event_record": (C.c_int, vp, vp),
+    "qa_event_elapsed_ms": (C.c_int, vp, vp, C.POINTER(C.c_float)),
+    "qa_stream_synchronize": (C.c_int, vp),
     "qa_kv_layout_check": (C.c_int, C.POINTER(KvLayout)),
     "qa_kv_elem_bytes": (sz, i32),
     "qa_kv_cache_bytes": (sz, C.POINTER(KvLayout)),
@@ -85,6 +94,8 @@ SIGNATURES = {
     "qa_decode_attn_workspace_bytes": (sz, i32, i32, i32),
     "qa_workspace_clear": (C.c_int, vp, sz, vp),
     "qa_decode_attn": (C.c_int, vp, vp, C.POINTER(KvLayout), i32, vp, i32, i32, i32, f32, vp, vp, sz, vp),
+    "qa_decode_step_attn": (C.c_int, vp, vp, vp, vp, C.POINTER(KvLayout), i32, vp, i32, i32, i32, f32, f32, f32, vp,
+                            vp, sz, vp),
     "qa_prefill_attn_workspace_bytes": (sz, i32, i32),
     "qa_prefill_attn": (C.c_int, vp, vp, C.POINTER(KvLayout), i32, i32, i32, i32, i32, f32, vp, vp, sz, vp),
     "qa_causal_attn_f32": (C.c_int, vp, vp, vp, i32, i32, i32, f32, vp, vp),
@@ -146,6 +157,56 @@ def iptr(a: np.ndarray):
 
 def device_count() -> int:
     return lib.qa_device_count()
+
+
+class DeviceArray:
+    """A device buffer of device 0 owned through the C ABI (qa_device_malloc), with numpy transfers."""
+
+    def __init__(self, shape, dtype=np.float32, zero: bool = True):
+        self.shape = tuple(int(v) for v in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        h = vp()
+        check(lib.qa_device_malloc(C.byref(h), self.nbytes))
+        self.handle = h
+        if zero:
+            check(lib.qa_memset_device(self.handle, 0, self.nbytes))
+
+    @classmethod
+    def from_numpy(cls, a: np.ndarray) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype, zero=False)
+        d.upload(a)
+        return d
+
+    @property
+    def ptr(self):
+        return self.handle
+
+    def upload(self, a: np.ndarray):
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.nbytes == self.nbytes, (a.shape, self.shape)
+        check(lib.qa_copy_to_device(self.handle, a.ctypes.data, self.nbytes))
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=self.dtype)
+        check(lib.qa_copy_to_host(out.ctypes.data, self.handle, self.nbytes))
+        return out
+
+    def free(self):
+        if getattr(self, "handle", None):
+            lib.qa_device_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def synchronize():
+    check(lib.qa_device_synchronize())
 
 
 # ----------------------------------------------------------------------------------------- model sizes

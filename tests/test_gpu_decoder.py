@@ -87,10 +87,12 @@ def test_small_model_greedy_matches_oracle(qa, orc, f16):
         with pytest.raises(qa.QaError) as e:
             dec.forward(x[:2], 49 + N - 1)
         assert e.value.code == qa.QA_ERR_CAPACITY
-        # a cached forward of the prompt matches the oracle's logits
+        # a cached forward of the prompt matches the oracle's logits, to the attention bar of the
+        # north star (2e-3 max-abs, 1e-3 relative L2): with an f16 cache, p is rounded to f16, so a
+        # 1-ulp f32 difference in a score can move p by one f16 step
         logits = dec.forward(x, 0)
         ref_logits = om.forward_cached(x, 0, om.cache(49 + N, f16))
-        close(logits, ref_logits, atol=1e-3, rtol_l2=1e-4)
+        close(logits, ref_logits, atol=2e-3, rtol_l2=1e-3)
 
 
 @pytest.mark.parametrize("index", [1, 2, 3])

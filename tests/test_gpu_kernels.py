@@ -1,31 +1,21 @@
 """Kernel-level parity of the HIP path against the CPU oracle, through the C ABI.
 
-Device memory comes from torch (plumbing only); every computation is a qa_* entry point of
-libqwenasr_amd.so.  Bars: cache slots, positions and lengths bit-exact;
-attention within 2e-3 max-abs and 1e-3 relative-L2 with f32 accumulation.  The append kernel is
-held to bit-exactness of the whole cache (written rows and untouched rows alike).
+Device memory is allocated and copied through the library's own C ABI (qa_device_malloc and
+friends), so these tests load exactly one HIP runtime: the one libqwenasr_amd.so links.  Every
+computation is a qa_* entry point.  Bars: cache slots, positions and lengths
+bit-exact; attention within 2e-3 max-abs and 1e-3 relative-L2 with f32 accumulation.  The append
+kernel is held to bit-exactness of the whole cache (written rows and untouched rows alike).
 """
 import ctypes as C
 
 import numpy as np
 import pytest
 
-torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
 ATOL, RTOL_L2 = 2e-3, 1e-3
-
-
-def vp(t):
-    return C.c_void_p(t.data_ptr())
-
-
-def stream():
-    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
-
-
-def dev(a):
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+SCALE = 1.0 / np.sqrt(128.0)
+NULL_STREAM = None
 
 
 def check_close(got, ref, atol=ATOL, rtol_l2=RTOL_L2):
@@ -45,20 +35,46 @@ def _gpu(qa):
     print("device:", arch.value.decode(), flush=True)
 
 
+def dev(qa, a):
+    return qa.DeviceArray.from_numpy(a)
+
+
+def zeros(qa, shape, dtype=np.float32):
+    return qa.DeviceArray(shape, dtype)
+
+
 def layout(qa, n_layers, n_streams, max_seq, f16):
     return qa.KvLayout(n_layers, n_streams, 8, 128, max_seq, qa.QA_CACHE_F16 if f16 else qa.QA_CACHE_F32)
 
 
-def cache_tensor(qa, lay):
-    n = qa.lib.qa_kv_cache_bytes(C.byref(lay))
-    return torch.zeros(n // (2 if lay.cache_type == qa.QA_CACHE_F16 else 4),
-                       dtype=torch.float16 if lay.cache_type == qa.QA_CACHE_F16 else torch.float32, device="cuda")
+class Cache:
+    """Host mirror [layer][kv][stream][head][pos][dim] of one device K+V allocation."""
 
+    def __init__(self, qa, lay):
+        self.lay = lay
+        dt = np.float16 if lay.cache_type == qa.QA_CACHE_F16 else np.float32
+        self.host = np.zeros((lay.n_layers, 2, lay.n_streams, lay.n_kv_heads, lay.max_seq, lay.head_dim), dt)
+        assert self.host.nbytes == qa.lib.qa_kv_cache_bytes(C.byref(lay))
+        self.dev = qa.DeviceArray(self.host.shape, dt)
 
-def cache_view(lay, t):
-    """[layer][kv][stream][head][pos][dim] numpy view of the device cache (as f32 values)."""
-    a = t.cpu().numpy().astype(np.float32)
-    return a.reshape(lay.n_layers, 2, lay.n_streams, lay.n_kv_heads, lay.max_seq, lay.head_dim)
+    def fill(self, rng, layer, stream_lens):
+        """Random K/V rows [0, L) per stream at `layer`; returns the f32 values actually stored."""
+        vals = {}
+        for s, L in enumerate(stream_lens):
+            k = rng.standard_normal((8, L, 128)).astype(np.float32)
+            v = rng.standard_normal((8, L, 128)).astype(np.float32)
+            self.host[layer, 0, s, :, :L] = k
+            self.host[layer, 1, s, :, :L] = v
+            vals[s] = (self.host[layer, 0, s, :, :L].astype(np.float32), self.host[layer, 1, s, :, :L].astype(np.float32))
+        self.dev.upload(self.host)
+        return vals
+
+    def read(self):
+        return self.dev.numpy().astype(np.float32)
+
+    @property
+    def ptr(self):
+        return self.dev.ptr
 
 
 # ------------------------------------------------------------------------------------------ append
@@ -67,19 +83,20 @@ def cache_view(lay, t):
 def test_kv_append_bit_exact(qa, orc, f16, T, n_past):
     S = len(n_past)
     lay = layout(qa, 2, S, 4169, f16)
-    cache = cache_tensor(qa, lay)
+    cache = Cache(qa, lay)
     rng = np.random.default_rng(T * 7 + S)
     qkv = (rng.standard_normal((S * T, 4096)) * 0.7).astype(np.float32)
     qn = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
     kn = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
-    d_qkv, d_qn, d_kn = dev(qkv), dev(qn), dev(kn)
-    d_q = torch.zeros(S * T, 2048, device="cuda")
-    d_np = dev(np.array(n_past, np.int32))
+    d_qkv, d_qn, d_kn = dev(qa, qkv), dev(qa, qn), dev(qa, kn)
+    d_q = zeros(qa, (S * T, 2048))
+    d_np = dev(qa, np.array(n_past, np.int32))
     print(f"append f16={f16} T={T} n_past={n_past}", flush=True)
-    qa.check(qa.lib.qa_kv_append(vp(d_qkv), vp(d_qn), vp(d_kn), vp(d_q), vp(cache), C.byref(lay), 1, vp(d_np), S, T,
-                                 16, 1.0e6, 1e-6, stream()))
-    torch.cuda.synchronize()
-    got = cache_view(lay, cache)
+    qa.check(qa.lib.qa_kv_append(d_qkv.ptr, d_qn.ptr, d_kn.ptr, d_q.ptr, cache.ptr, C.byref(lay), 1, d_np.ptr, S, T,
+                                 16, 1.0e6, 1e-6, NULL_STREAM))
+    qa.synchronize()
+    got = cache.read()
+    q_got = d_q.numpy()
     expect = np.zeros_like(got)
     for s in range(S):
         rows = qkv[s * T:(s + 1) * T]
@@ -91,23 +108,17 @@ def test_kv_append_bit_exact(qa, orc, f16, T, n_past):
             v = v.astype(np.float16).astype(np.float32)
         expect[1, 0, s, :, n_past[s]:n_past[s] + T] = k.transpose(1, 0, 2)
         expect[1, 1, s, :, n_past[s]:n_past[s] + T] = v.transpose(1, 0, 2)
-        np.testing.assert_array_equal(d_q[s * T:(s + 1) * T].cpu().numpy().view(np.uint32),
-                                      q.reshape(T, 2048).view(np.uint32))
+        np.testing.assert_array_equal(q_got[s * T:(s + 1) * T].view(np.uint32), q.reshape(T, 2048).view(np.uint32))
     np.testing.assert_array_equal(got.view(np.uint32), expect.view(np.uint32))
 
 
 # ------------------------------------------------------------------------------------------ decode
-def _fill_cache(qa, lay, cache, rng, layer, stream_lens):
-    """Random K/V rows [0, L) per stream at `layer`; returns the f32 values actually stored."""
-    vals = {}
-    full = cache.view(lay.n_layers, 2, lay.n_streams, lay.n_kv_heads, lay.max_seq, lay.head_dim)
-    for s, L in enumerate(stream_lens):
-        k = rng.standard_normal((8, L, 128)).astype(np.float32)
-        v = rng.standard_normal((8, L, 128)).astype(np.float32)
-        full[layer, 0, s, :, :L] = torch.from_numpy(k).to(full.dtype)
-        full[layer, 1, s, :, :L] = torch.from_numpy(v).to(full.dtype)
-        vals[s] = (k, v)
-    return vals
+def _decode(qa, q_dev, cache, lay, layer, lens, max_len, out, ws, ws_bytes):
+    d_lens = dev(qa, np.array(lens, np.int32))
+    qa.check(qa.lib.qa_decode_attn(q_dev.ptr, cache.ptr, C.byref(lay), layer, d_lens.ptr, len(lens), max_len, 16, SCALE,
+                                   out.ptr, ws.ptr, ws_bytes, NULL_STREAM))
+    qa.synchronize()
+    return out.numpy().reshape(len(lens), 16, 128)
 
 
 @pytest.mark.parametrize("f16", [True, False])
@@ -116,24 +127,103 @@ def test_decode_attention(qa, orc, f16, lens):
     S = len(lens)
     max_len = max(lens)
     lay = layout(qa, 3, S, max_len + 3, f16)
-    cache = cache_tensor(qa, lay)
+    cache = Cache(qa, lay)
     rng = np.random.default_rng(sum(lens))
-    vals = _fill_cache(qa, lay, cache, rng, 2, lens)
+    vals = cache.fill(rng, 2, lens)
     q = rng.standard_normal((S, 16, 128)).astype(np.float32)
-    d_q, d_out = dev(q), torch.zeros(S, 2048, device="cuda")
-    d_lens = dev(np.array(lens, np.int32))
-    ws_bytes = qa.lib.qa_decode_attn_workspace_bytes(S, 16, max_len)
-    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device="cuda")
+    d_q, d_out = dev(qa, q), zeros(qa, (S, 2048))
+    ws_bytes = qa.lib.qa_decode_attn_workspace_bytes(S, 16, lay.max_seq)
+    ws = zeros(qa, ws_bytes, np.uint8)
     print(f"decode f16={f16} lens={lens}", flush=True)
     for rep in range(2):   # the second call checks the counters were left at zero
-        qa.check(qa.lib.qa_decode_attn(vp(d_q), vp(cache), C.byref(lay), 2, vp(d_lens), S, max_len, 16,
-                                       1.0 / np.sqrt(128.0), vp(d_out), vp(ws), ws_bytes, stream()))
-        torch.cuda.synchronize()
-        got = d_out.cpu().numpy().reshape(S, 16, 128)
+        got = _decode(qa, d_q, cache, lay, 2, lens, max_len, d_out, ws, ws_bytes)
         for s, L in enumerate(lens):
             k, v = vals[s]
             ref = orc.cache_attention(k, v, q[s:s + 1], L - 1, f16)[0]
             check_close(got[s], ref)
+
+
+@pytest.mark.parametrize("f16", [True, False])
+def test_decode_attention_growing_lengths_one_workspace(qa, orc, f16):
+    """One workspace, never cleared between calls, while the prefix grows across chunk boundaries
+    (1 -> many chunks, and 32/64/128-row boundaries): every call must match the oracle, so the
+    merge counters stay where the capacity put them and are left at zero by each call."""
+    S, cap = 2, 4200
+    lay = layout(qa, 1, S, cap, f16)
+    cache = Cache(qa, lay)
+    rng = np.random.default_rng(7)
+    vals = cache.fill(rng, 0, [cap, cap])
+    q = rng.standard_normal((S, 16, 128)).astype(np.float32)
+    d_q, d_out = dev(qa, q), zeros(qa, (S, 2048))
+    ws_bytes = qa.lib.qa_decode_attn_workspace_bytes(S, 16, cap)
+    ws = zeros(qa, ws_bytes, np.uint8)
+    for lens in ([1, 3], [31, 33], [32, 64], [65, 63], [127, 129], [130, 1], [1023, 2047], [4096, 4100],
+                 [200, 4200], [5, 6]):
+        print(f"decode growing f16={f16} lens={lens}", flush=True)
+        got = _decode(qa, d_q, cache, lay, 0, lens, max(lens), d_out, ws, ws_bytes)
+        for s, L in enumerate(lens):
+            k, v = vals[s]
+            ref = orc.cache_attention(k[:, :L], v[:, :L], q[s:s + 1], L - 1, f16)[0]
+            check_close(got[s], ref)
+
+
+def test_decode_attention_rejects_small_workspace(qa):
+    lay = layout(qa, 1, 1, 4096, True)
+    cache = Cache(qa, lay)
+    d_q, d_out = zeros(qa, (1, 2048)), zeros(qa, (1, 2048))
+    d_lens = dev(qa, np.array([100], np.int32))
+    small = qa.lib.qa_decode_attn_workspace_bytes(1, 16, 1000)
+    ws = zeros(qa, small, np.uint8)
+    rc = qa.lib.qa_decode_attn(d_q.ptr, cache.ptr, C.byref(lay), 0, d_lens.ptr, 1, 100, 16, 0.1, d_out.ptr, ws.ptr,
+                               small, NULL_STREAM)
+    assert rc == qa.QA_ERR_INVALID and b"workspace" in qa.lib.qa_last_error()
+
+
+@pytest.mark.parametrize("f16", [True, False])
+@pytest.mark.parametrize("n_past", [[0], [31], [63], [64], [156], [4095], [156, 3912, 700, 0, 2047, 31]])
+def test_decode_step_fused_equals_append_then_attend(qa, orc, f16, n_past):
+    """qa_decode_step_attn == qa_kv_append + qa_decode_attn at lens = n_past + 1: the whole cache and the
+    output bit-exact (new row written, every other row untouched), and the output within the
+    attention tolerance of the oracle (which runs the reference order: write the row, then attend)."""
+    S = len(n_past)
+    lay = layout(qa, 2, S, max(n_past) + 5, f16)
+    rng = np.random.default_rng(len(n_past) * 1000 + n_past[0])
+    qkv = (rng.standard_normal((S, 4096)) * 0.7).astype(np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    d_qkv, d_qn, d_kn = dev(qa, qkv), dev(qa, qn), dev(qa, kn)
+    d_np = dev(qa, np.array(n_past, np.int32))
+    d_lens = dev(qa, np.array(n_past, np.int32) + 1)
+    ws_bytes = qa.lib.qa_decode_attn_workspace_bytes(S, 16, lay.max_seq)
+    caches, outs = [], []
+    for fused in (True, False):
+        cache = Cache(qa, lay)
+        cache.fill(np.random.default_rng(99), 1, [p_ + 2 for p_ in n_past])
+        ws = zeros(qa, ws_bytes, np.uint8)
+        out = zeros(qa, (S, 2048))
+        print(f"decode step fused={fused} f16={f16} n_past={n_past}", flush=True)
+        if fused:
+            qa.check(qa.lib.qa_decode_step_attn(d_qkv.ptr, d_qn.ptr, d_kn.ptr, cache.ptr, C.byref(lay), 1, d_np.ptr, S,
+                                                max(n_past) + 1, 16, 1.0e6, 1e-6, SCALE, out.ptr, ws.ptr, ws_bytes,
+                                                NULL_STREAM))
+        else:
+            d_q = zeros(qa, (S, 2048))
+            qa.check(qa.lib.qa_kv_append(d_qkv.ptr, d_qn.ptr, d_kn.ptr, d_q.ptr, cache.ptr, C.byref(lay), 1, d_np.ptr,
+                                         S, 1, 16, 1.0e6, 1e-6, NULL_STREAM))
+            qa.check(qa.lib.qa_decode_attn(d_q.ptr, cache.ptr, C.byref(lay), 1, d_lens.ptr, S, max(n_past) + 1, 16,
+                                           SCALE, out.ptr, ws.ptr, ws_bytes, NULL_STREAM))
+        qa.synchronize()
+        caches.append(cache.read())
+        outs.append(out.numpy().reshape(S, 16, 128))
+    np.testing.assert_array_equal(caches[0].view(np.uint32), caches[1].view(np.uint32))
+    np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    for s_, P in enumerate(n_past):
+        k = caches[0][1, 0, s_, :, :P + 1]
+        v = caches[0][1, 1, s_, :, :P + 1]
+        q, _ = orc.qk_prep(qkv[s_:s_ + 1, :2048].reshape(1, 16, 128), qkv[s_:s_ + 1, 2048:3072].reshape(1, 8, 128),
+                           qn, kn, P, 1.0e6, 1e-6)
+        ref = orc.cache_attention(k, v, q, P, f16)[0]
+        check_close(outs[0][s_], ref)
 
 
 # ------------------------------------------------------------------------------------------ prefill
@@ -142,19 +232,19 @@ def test_decode_attention(qa, orc, f16, lens):
 def test_prefill_attention(qa, orc, f16, n_past, T):
     L = n_past + T
     lay = layout(qa, 2, 2, L + 5, f16)
-    cache = cache_tensor(qa, lay)
+    cache = Cache(qa, lay)
     rng = np.random.default_rng(L)
-    vals = _fill_cache(qa, lay, cache, rng, 1, [5, L])        # stream 1 holds the rows under test
+    vals = cache.fill(rng, 1, [5, L])        # stream 1 holds the rows under test
     k, v = vals[1]
     q = rng.standard_normal((T, 16, 128)).astype(np.float32)
-    d_q, d_out = dev(q), torch.zeros(T, 2048, device="cuda")
+    d_q, d_out = dev(qa, q), zeros(qa, (T, 2048))
     ws_bytes = qa.lib.qa_prefill_attn_workspace_bytes(T, 16)
-    ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    ws = zeros(qa, max(ws_bytes, 1), np.uint8)
     print(f"prefill f16={f16} n_past={n_past} T={T}", flush=True)
-    qa.check(qa.lib.qa_prefill_attn(vp(d_q), vp(cache), C.byref(lay), 1, 1, n_past, T, 16, 1.0 / np.sqrt(128.0),
-                                    vp(d_out), vp(ws), ws_bytes, stream()))
-    torch.cuda.synchronize()
-    got = d_out.cpu().numpy().reshape(T, 16, 128)
+    qa.check(qa.lib.qa_prefill_attn(d_q.ptr, cache.ptr, C.byref(lay), 1, 1, n_past, T, 16, SCALE, d_out.ptr, ws.ptr,
+                                    ws_bytes, NULL_STREAM))
+    qa.synchronize()
+    got = d_out.numpy().reshape(T, 16, 128)
     ref = orc.cache_attention(k, v, q, n_past, f16)
     check_close(got, ref)
     # row t of the prefill equals a decode over the prefix t + 1 (cross-piece invariant)
@@ -169,10 +259,10 @@ def test_causal_attention_f32(qa, orc, T):
     q = rng.standard_normal((T, 16, 128)).astype(np.float32)
     k = rng.standard_normal((T, 8, 128)).astype(np.float32)
     v = rng.standard_normal((T, 8, 128)).astype(np.float32)
-    d_q, d_k, d_v, d_o = dev(q), dev(k), dev(v), torch.zeros(T, 2048, device="cuda")
-    qa.check(qa.lib.qa_causal_attn_f32(vp(d_q), vp(d_k), vp(d_v), T, 16, 8, 1.0 / np.sqrt(128.0), vp(d_o), stream()))
-    torch.cuda.synchronize()
-    check_close(d_o.cpu().numpy().reshape(T, 16, 128), orc.causal_attention_f32(q, k, v))
+    d_q, d_k, d_v, d_o = dev(qa, q), dev(qa, k), dev(qa, v), zeros(qa, (T, 2048))
+    qa.check(qa.lib.qa_causal_attn_f32(d_q.ptr, d_k.ptr, d_v.ptr, T, 16, 8, SCALE, d_o.ptr, NULL_STREAM))
+    qa.synchronize()
+    check_close(d_o.numpy().reshape(T, 16, 128), orc.causal_attention_f32(q, k, v))
 
 
 # ------------------------------------------------------------------------------------------ adjacent ops
@@ -183,21 +273,21 @@ def test_gemv(qa, orc, in_dim, out_dim):
     w = (rng.standard_normal((out_dim, in_dim)) * 0.02).astype(np.float32)
     x = rng.standard_normal((2, in_dim)).astype(np.float32)
     y0 = rng.standard_normal((2, out_dim)).astype(np.float32)
-    d_w, d_x, d_y = dev(w), dev(x), dev(y0)
-    qa.check(qa.lib.qa_gemv(vp(d_w), out_dim, in_dim, vp(d_x), 2, vp(d_y), 1, stream()))
-    torch.cuda.synchronize()
-    np.testing.assert_allclose(d_y.cpu().numpy(), y0 + orc.linear(x, w), rtol=1e-5, atol=1e-5)
+    d_w, d_x, d_y = dev(qa, w), dev(qa, x), dev(qa, y0)
+    qa.check(qa.lib.qa_gemv(d_w.ptr, out_dim, in_dim, d_x.ptr, 2, d_y.ptr, 1, NULL_STREAM))
+    qa.synchronize()
+    np.testing.assert_allclose(d_y.numpy(), y0 + orc.linear(x, w), rtol=1e-5, atol=1e-5)
 
 
 def test_rmsnorm_rows_bit_exact(qa, orc):
     rng = np.random.default_rng(3)
     x = (rng.standard_normal((7, 2048)) * 2).astype(np.float32)
     w = (1 + 0.1 * rng.standard_normal(2048)).astype(np.float32)
-    d_x, d_w, d_y = dev(x), dev(w), torch.zeros(7, 2048, device="cuda")
-    qa.check(qa.lib.qa_rmsnorm_rows(vp(d_x), vp(d_w), 7, 2048, 1e-6, vp(d_y), stream()))
-    torch.cuda.synchronize()
+    d_x, d_w, d_y = dev(qa, x), dev(qa, w), zeros(qa, (7, 2048))
+    qa.check(qa.lib.qa_rmsnorm_rows(d_x.ptr, d_w.ptr, 7, 2048, 1e-6, d_y.ptr, NULL_STREAM))
+    qa.synchronize()
     ref = np.stack([orc.rms_norm_row(x[r], w, 1e-6) for r in range(7)])
-    np.testing.assert_array_equal(d_y.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    np.testing.assert_array_equal(d_y.numpy().view(np.uint32), ref.view(np.uint32))
 
 
 def test_argmax_rows_rule(qa, orc):
@@ -209,24 +299,42 @@ def test_argmax_rows_rule(qa, orc):
     rows[2][77777] = -3.0                                      # NaN never wins
     rows.append(np.full(V, -np.inf, np.float32))               # nothing beats -inf -> -1
     logits = np.stack(rows)
-    d_l, d_ids = dev(logits), torch.zeros(4, dtype=torch.int32, device="cuda")
+    d_l, d_ids = dev(qa, logits), zeros(qa, 4, np.int32)
     ws_bytes = qa.lib.qa_argmax_workspace_bytes(4)
-    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device="cuda")
+    ws = zeros(qa, ws_bytes, np.uint8)
     for _ in range(2):
-        qa.check(qa.lib.qa_argmax_rows(vp(d_l), 4, V, vp(d_ids), vp(ws), ws_bytes, stream()))
-        torch.cuda.synchronize()
-        assert d_ids.cpu().tolist() == [orc.argmax(r) for r in rows] == [int(np.argmax(rows[0])), 5, 77777, -1]
+        qa.check(qa.lib.qa_argmax_rows(d_l.ptr, 4, V, d_ids.ptr, ws.ptr, ws_bytes, NULL_STREAM))
+        qa.synchronize()
+        assert d_ids.numpy().tolist() == [orc.argmax(r) for r in rows] == [int(np.argmax(rows[0])), 5, 77777, -1]
 
 
 def test_embed_and_lens(qa):
     table = np.arange(10 * 2048, dtype=np.float32).reshape(10, 2048)
-    d_t, d_ids, d_o = dev(table), dev(np.array([3, -1, 9, 10], np.int32)), torch.ones(4, 2048, device="cuda")
-    qa.check(qa.lib.qa_embed_rows(vp(d_t), 10, 2048, vp(d_ids), 4, vp(d_o), stream()))
-    d_lens = dev(np.array([0, 5, 7], np.int32))
-    qa.check(qa.lib.qa_advance_lens(vp(d_lens), 3, 2, stream()))
-    torch.cuda.synchronize()
-    o = d_o.cpu().numpy()
+    d_t, d_ids = dev(qa, table), dev(qa, np.array([3, -1, 9, 10], np.int32))
+    d_o = dev(qa, np.ones((4, 2048), np.float32))
+    qa.check(qa.lib.qa_embed_rows(d_t.ptr, 10, 2048, d_ids.ptr, 4, d_o.ptr, NULL_STREAM))
+    d_lens = dev(qa, np.array([0, 5, 7], np.int32))
+    qa.check(qa.lib.qa_advance_lens(d_lens.ptr, 3, 2, NULL_STREAM))
+    qa.synchronize()
+    o = d_o.numpy()
     np.testing.assert_array_equal(o[0], table[3])
     np.testing.assert_array_equal(o[2], table[9])
     assert not o[1].any() and not o[3].any()
-    assert d_lens.cpu().tolist() == [2, 7, 9]
+    assert d_lens.numpy().tolist() == [2, 7, 9]
+
+
+def test_event_timing_helpers(qa):
+    """The C-ABI event pair measures a positive interval around device work."""
+    a, b = C.c_void_p(), C.c_void_p()
+    qa.check(qa.lib.qa_event_create(C.byref(a)))
+    qa.check(qa.lib.qa_event_create(C.byref(b)))
+    x = zeros(qa, (1 << 20,))
+    qa.check(qa.lib.qa_event_record(a, NULL_STREAM))
+    for _ in range(10):
+        qa.check(qa.lib.qa_add_inplace(x.ptr, x.ptr, 1 << 20, NULL_STREAM))
+    qa.check(qa.lib.qa_event_record(b, NULL_STREAM))
+    ms = C.c_float()
+    qa.check(qa.lib.qa_event_elapsed_ms(a, b, C.byref(ms)))
+    assert ms.value > 0.0
+    qa.check(qa.lib.qa_event_destroy(a))
+    qa.check(qa.lib.qa_event_destroy(b))

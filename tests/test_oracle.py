@@ -11,7 +11,19 @@ import math
 
 import numpy as np
 import pytest
-import torch
+
+
+class _LazyTorch:
+    """torch, imported on first use: only these CPU cross-checks need it, and a GPU session that
+    collects this file must not load torch's own HIP runtime next to the library's."""
+
+    def __getattr__(self, name):
+        import torch as _torch
+
+        return getattr(_torch, name)
+
+
+torch = _LazyTorch()
 
 
 # ---------------------------------------------------------------------------------------------- f16

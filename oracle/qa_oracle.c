@@ -246,11 +246,16 @@ int32_t orc_argmax(const float * logits, int32_t n) {
     return best_id;
 }
 
-static float top2_margin(const float * logits, int32_t n, int32_t best_id) {
+/* Gap between the greedy pick and the runner-up (the first index of the largest other logit). */
+static float top2_margin(const float * logits, int32_t n, int32_t best_id, int32_t * second_id) {
+    *second_id = -1;
     if (best_id < 0) return 0.0f;
     float second = -INFINITY;
     for (int32_t i = 0; i < n; ++i) {
-        if (i != best_id && logits[i] > second) second = logits[i];
+        if (i != best_id && logits[i] > second) {
+            second = logits[i];
+            *second_id = i;
+        }
     }
     return logits[best_id] - second;
 }
@@ -529,7 +534,7 @@ int orc_forward_cached(const orc_model * m, const float * x, int32_t n_tokens, i
 int orc_generate_cached(const orc_model * m, const float * x, int32_t n_tokens, int32_t max_new,
                         const int32_t * stop_ids, int32_t n_stop, orc_cache * cache,
                         int32_t * out_ids, int32_t * n_out, int32_t * stopped, int32_t * total_tokens,
-                        float * margins) {
+                        float * margins, int32_t * runner_up) {
     const orc_config * c = &m->cfg;
     *n_out = 0;
     *stopped = 0;
@@ -544,7 +549,10 @@ int orc_generate_cached(const orc_model * m, const float * x, int32_t n_tokens, 
     for (int32_t step = 0; step < max_new; ++step) {
         const int32_t id = orc_argmax(logits, c->vocab);
         if (id < 0 || id >= c->vocab) { rc = 6; break; }
-        if (margins) margins[step] = top2_margin(logits, c->vocab, id);
+        int32_t second = -1;
+        const float gap = top2_margin(logits, c->vocab, id, &second);
+        if (margins) margins[step] = gap;
+        if (runner_up) runner_up[step] = second;
         out_ids[(*n_out)++] = id;
         *total_tokens = n_tokens + *n_out;
         int stop = 0;
@@ -558,7 +566,7 @@ int orc_generate_cached(const orc_model * m, const float * x, int32_t n_tokens, 
 }
 
 int orc_decode_steps(const orc_model * m, orc_cache * cache, int32_t first_id, int32_t n_steps,
-                     int32_t * out_ids, float * margins) {
+                     int32_t * out_ids, float * margins, int32_t * runner_up) {
     const orc_config * c = &m->cfg;
     if (cache->cur_len + n_steps > cache->max_seq) return 2;
     float * logits = (float *)malloc(sizeof(float) * (size_t)c->vocab);
@@ -569,7 +577,10 @@ int orc_decode_steps(const orc_model * m, orc_cache * cache, int32_t first_id, i
         orc_forward_cached(m, m->token_embd + (size_t)id * c->hidden, 1, cache->cur_len, cache, logits);
         id = orc_argmax(logits, c->vocab);
         out_ids[k] = id;
-        if (margins) margins[k] = top2_margin(logits, c->vocab, id);
+        int32_t second = -1;
+        const float gap = top2_margin(logits, c->vocab, id, &second);
+        if (margins) margins[k] = gap;
+        if (runner_up) runner_up[k] = second;
     }
     free(logits);
     return rc;

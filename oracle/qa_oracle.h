@@ -92,14 +92,16 @@ int orc_layer_forward_nocache(const orc_model * m, int32_t layer, const float * 
 int orc_logits(const orc_model * m, const float * state, float * logits);
 int orc_forward_cached(const orc_model * m, const float * x, int32_t n_tokens, int32_t n_past,
                        orc_cache * cache, float * logits);
+/* margins[k] / runner_up[k] (either may be NULL): gap between the greedy pick of step k and the
+ * runner-up, and the runner-up's id (first index of the largest other logit).                 */
 int orc_generate_cached(const orc_model * m, const float * x, int32_t n_tokens, int32_t max_new,
                         const int32_t * stop_ids, int32_t n_stop, orc_cache * cache,
                         int32_t * out_ids, int32_t * n_out, int32_t * stopped, int32_t * total_tokens,
-                        float * margins);
+                        float * margins, int32_t * runner_up);
 /* n_steps single-token steps starting from token first_id at cache->cur_len; out_ids[k] is the
  * greedy pick after step k (config 4 per-stream statement). */
 int orc_decode_steps(const orc_model * m, orc_cache * cache, int32_t first_id, int32_t n_steps,
-                     int32_t * out_ids, float * margins);
+                     int32_t * out_ids, float * margins, int32_t * runner_up);
 
 #ifdef __cplusplus
 }

@@ -67,8 +67,8 @@ _sig("orc_layer_forward_cached", C.c_int, C.POINTER(Model), i32, fp, i32, i32, C
 _sig("orc_layer_forward_nocache", C.c_int, C.POINTER(Model), i32, fp, i32, fp)
 _sig("orc_logits", C.c_int, C.POINTER(Model), fp, fp)
 _sig("orc_forward_cached", C.c_int, C.POINTER(Model), fp, i32, i32, C.POINTER(Cache), fp)
-_sig("orc_generate_cached", C.c_int, C.POINTER(Model), fp, i32, i32, ip, i32, C.POINTER(Cache), ip, ip, ip, ip, fp)
-_sig("orc_decode_steps", C.c_int, C.POINTER(Model), C.POINTER(Cache), i32, i32, ip, fp)
+_sig("orc_generate_cached", C.c_int, C.POINTER(Model), fp, i32, i32, ip, i32, C.POINTER(Cache), ip, ip, ip, ip, fp, ip)
+_sig("orc_decode_steps", C.c_int, C.POINTER(Model), C.POINTER(Cache), i32, i32, ip, fp, ip)
 
 
 def fptr(a: np.ndarray):
@@ -244,20 +244,25 @@ class OracleModel:
         x = np.ascontiguousarray(x, dtype=np.float32)
         ids = np.zeros(max(max_new, 1), dtype=np.int32)
         marg = np.zeros(max(max_new, 1), dtype=np.float32)
+        second = np.zeros(max(max_new, 1), dtype=np.int32)
         stops = np.asarray(stop_ids, dtype=np.int32)
         n_out, stopped, total = i32(), i32(), i32()
         rc = lib.orc_generate_cached(C.byref(self.m), fptr(x), x.shape[0], max_new, iptr(stops), len(stops),
                                      C.byref(cache.c), iptr(ids), C.byref(n_out), C.byref(stopped), C.byref(total),
-                                     fptr(marg))
-        return dict(rc=rc, ids=ids[: n_out.value].tolist(), stopped=bool(stopped.value), total_tokens=total.value,
-                    margins=marg[: n_out.value].tolist(), cur_len=cache.cur_len)
+                                     fptr(marg), iptr(second))
+        n = n_out.value
+        return dict(rc=rc, ids=ids[:n].tolist(), stopped=bool(stopped.value), total_tokens=total.value,
+                    margins=marg[:n].tolist(), runner_up=second[:n].tolist(), cur_len=cache.cur_len)
 
     def decode_steps(self, cache: OracleCache, first_id: int, n_steps: int):
+        """-> (ids, margins, runner_up) of n_steps greedy steps from first_id at cache.cur_len."""
         ids = np.zeros(n_steps, dtype=np.int32)
         marg = np.zeros(n_steps, dtype=np.float32)
-        rc = lib.orc_decode_steps(C.byref(self.m), C.byref(cache.c), first_id, n_steps, iptr(ids), fptr(marg))
+        second = np.zeros(n_steps, dtype=np.int32)
+        rc = lib.orc_decode_steps(C.byref(self.m), C.byref(cache.c), first_id, n_steps, iptr(ids), fptr(marg),
+                                  iptr(second))
         assert rc == 0, rc
-        return ids.tolist(), marg.tolist()
+        return ids.tolist(), marg.tolist(), second.tolist()
 
 
 def cache_attention(k: np.ndarray, v: np.ndarray, q: np.ndarray, n_past: int, f16: bool) -> np.ndarray:

@@ -16,7 +16,9 @@
 //                  the chunk's max m_c and double sum_j expf(s_j - m_c);
 //   values kernel  global max M and sum S = sum_c sum_c * exp(m_c - M) from the chunk statistics,
 //                  p_j, the chunk's partial o, and the merge: the last workgroup of each
-//                  (stream, KV head) adds the partials in chunk order.
+//                  (stream, KV head) adds the partials in a fixed order.
+// The two kernels chunk the positions independently: the scores kernel finely (no merge, so many
+// workgroups in flight), the values kernel coarsely (its chunks are the merge participants).
 // Dropping the p rounding would allow a single-pass launch, but it moves logits by up to ~1e-3 and
 // flips greedy near-ties against the reference semantics; identical greedy ids are the contract.
 //
@@ -78,6 +80,7 @@ struct DecodeParams {
     int32_t q_stride, out_stride;
     int32_t n_heads, n_kv_heads, n_streams, max_seq, layer;
     int32_t max_len, max_chunks, score_stride;
+    int32_t stat_chunk;       // positions per scores-kernel chunk (granularity of the statistics)
     float scale;
 };
 
@@ -316,7 +319,8 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
     const int c = static_cast<int>(blockIdx.x) / p.n_kv_heads;
     const int s = blockIdx.y;
     const int L = attended(p, s);
-    const int n_chunks = (L + CHUNK - 1) / CHUNK;
+    const int n_chunks = (L + CHUNK - 1) / CHUNK;                   // values chunks = merge participants
+    const int n_stats = (L + p.stat_chunk - 1) / p.stat_chunk;      // scores chunks
     if (c >= n_chunks) return;
 
     const int lane = threadIdx.x & (kWave - 1);
@@ -351,7 +355,7 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
     const SplitStat * st0 = p.stats + (static_cast<int64_t>(s) * p.n_heads + h0) * p.max_chunks;
     const SplitStat * st1 = st0 + p.max_chunks;
     float M0 = -INFINITY, M1 = -INFINITY;
-    for (int i = lane; i < n_chunks; i += kWave) {
+    for (int i = lane; i < n_stats; i += kWave) {
         M0 = fmaxf(M0, st0[i].m);
         M1 = fmaxf(M1, st1[i].m);
     }
@@ -361,7 +365,7 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
         M1 = fmaxf(M1, __shfl_xor(M1, off, kWave));
     }
     double S0 = 0.0, S1 = 0.0;
-    for (int i = lane; i < n_chunks; i += kWave) {
+    for (int i = lane; i < n_stats; i += kWave) {
         S0 += st0[i].s * exp(static_cast<double>(st0[i].m) - static_cast<double>(M0));
         S1 += st1[i].s * exp(static_cast<double>(st1[i].m) - static_cast<double>(M1));
     }
@@ -463,43 +467,66 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
     *out = s_acc[0][threadIdx.x] + s_acc[1][threadIdx.x];
 }
 
-// Positions per workgroup.  Short single-stream prefixes want more, smaller chunks (more
-// workgroups in flight); many streams already fill the chip and favour fewer partial states.
-int pick_chunk(int32_t n_streams, int32_t n_kv, int32_t max_len) {
-    static const int forced = [] {
-        const char * e = std::getenv("QA_DECODE_CHUNK");
-        return e ? std::atoi(e) : 0;
-    }();
-    if (forced == 32 || forced == 64 || forced == 128) return forced;
-    const int64_t wg64 = static_cast<int64_t>(n_streams) * n_kv * ((max_len + 63) / 64);
-    if (wg64 < 1024) return 32;
-    if (wg64 < 8192) return 64;
-    return 128;
+// Positions per workgroup of each kernel.  The scores kernel has no merge, so it uses small chunks
+// (many workgroups in flight); the values kernel's chunks are the merge participants of one
+// (stream, KV head), so it uses chunks large enough to keep them at <= 16 per unit (every participant
+// increments the same counter).  QA_DECODE_CHUNK / QA_DECODE_VCHUNK override the choice (tuning).
+struct Chunks {
+    int scores, values;
+};
+
+int env_chunk(const char * name) {
+    const char * e = std::getenv(name);
+    const int v = e ? std::atoi(e) : 0;
+    return v == 32 || v == 64 || v == 128 || v == 256 ? v : 0;
 }
 
-template <typename CT, bool R16, int CHUNK>
-void launch_pair(bool fused, dim3 grid, const DecodeParams & p, const RopeTable & rope, hipStream_t stream) {
-    if (fused) {
-        hipLaunchKernelGGL((decode_scores_kernel<CT, R16, CHUNK, true>), grid, dim3(kThreads), 0, stream, p, rope);
-    } else {
-        hipLaunchKernelGGL((decode_scores_kernel<CT, R16, CHUNK, false>), grid, dim3(kThreads), 0, stream, p, rope);
+Chunks pick_chunks(int32_t n_streams, int32_t n_kv, int32_t max_len) {
+    static const int forced_s = env_chunk("QA_DECODE_CHUNK");
+    static const int forced_v = env_chunk("QA_DECODE_VCHUNK");
+    Chunks ch{};
+    const int64_t wg32 = static_cast<int64_t>(n_streams) * n_kv * ((max_len + 31) / 32);
+    ch.scores = forced_s && forced_s <= 128 ? forced_s : wg32 < 2048 ? 32 : wg32 < 16384 ? 64 : 128;
+    int v = 32;
+    while (v < 256 && (max_len + v - 1) / v > 16) v *= 2;
+    ch.values = forced_v ? forced_v : v;
+    if (ch.values < ch.scores) ch.values = ch.scores;
+    return ch;
+}
+
+template <typename CT, bool R16, bool FUSED>
+void launch_scores(int chunk, dim3 grid, const DecodeParams & p, const RopeTable & rope, hipStream_t stream) {
+    switch (chunk) {
+        case 32: hipLaunchKernelGGL((decode_scores_kernel<CT, R16, 32, FUSED>), grid, dim3(kThreads), 0, stream, p, rope); break;
+        case 64: hipLaunchKernelGGL((decode_scores_kernel<CT, R16, 64, FUSED>), grid, dim3(kThreads), 0, stream, p, rope); break;
+        default: hipLaunchKernelGGL((decode_scores_kernel<CT, R16, 128, FUSED>), grid, dim3(kThreads), 0, stream, p, rope); break;
     }
-    hipLaunchKernelGGL((decode_values_kernel<CT, R16, CHUNK>), grid, dim3(kThreads), 0, stream, p);
 }
 
 template <typename CT, bool R16>
-void launch_chunk(int chunk, bool fused, dim3 grid, const DecodeParams & p, const RopeTable & rope,
-                  hipStream_t stream) {
+void launch_values(int chunk, dim3 grid, const DecodeParams & p, hipStream_t stream) {
     switch (chunk) {
-        case 32: launch_pair<CT, R16, 32>(fused, grid, p, rope, stream); break;
-        case 64: launch_pair<CT, R16, 64>(fused, grid, p, rope, stream); break;
-        default: launch_pair<CT, R16, 128>(fused, grid, p, rope, stream); break;
+        case 32: hipLaunchKernelGGL((decode_values_kernel<CT, R16, 32>), grid, dim3(kThreads), 0, stream, p); break;
+        case 64: hipLaunchKernelGGL((decode_values_kernel<CT, R16, 64>), grid, dim3(kThreads), 0, stream, p); break;
+        case 128: hipLaunchKernelGGL((decode_values_kernel<CT, R16, 128>), grid, dim3(kThreads), 0, stream, p); break;
+        default: hipLaunchKernelGGL((decode_values_kernel<CT, R16, 256>), grid, dim3(kThreads), 0, stream, p); break;
     }
+}
+
+template <typename CT, bool R16>
+void launch_both(const Chunks & ch, bool fused, int32_t n_kv, int32_t n_streams, DecodeParams p, const RopeTable & rope,
+                 hipStream_t stream) {
+    p.stat_chunk = ch.scores;
+    const dim3 gs(static_cast<unsigned>((p.max_len + ch.scores - 1) / ch.scores * n_kv), static_cast<unsigned>(n_streams));
+    const dim3 gv(static_cast<unsigned>((p.max_len + ch.values - 1) / ch.values * n_kv), static_cast<unsigned>(n_streams));
+    if (fused) launch_scores<CT, R16, true>(ch.scores, gs, p, rope, stream);
+    else launch_scores<CT, R16, false>(ch.scores, gs, p, rope, stream);
+    launch_values<CT, R16>(ch.values, gv, p, stream);
 }
 
 int launch_decode(DecodeParams p, bool fused, const RopeTable & rope, const qa_kv_layout & layout,
                   int32_t n_streams, void * workspace, size_t workspace_bytes, hipStream_t stream) {
-    const int chunk = pick_chunk(n_streams, layout.n_kv_heads, p.max_len);
+    const Chunks ch = pick_chunks(n_streams, layout.n_kv_heads, p.max_len);
     const Workspace w = workspace_layout(layout.n_streams, layout.n_kv_heads, layout.max_seq);
     if (!workspace || workspace_bytes < w.total) {
         return fail(QA_ERR_INVALID, "decode attention: workspace too small for the cache capacity");
@@ -514,10 +541,8 @@ int launch_decode(DecodeParams p, bool fused, const RopeTable & rope, const qa_k
     p.max_seq = layout.max_seq;
     p.max_chunks = (layout.max_seq + kMinChunk - 1) / kMinChunk;
     p.score_stride = p.max_chunks * kMinChunk;
-    const int32_t grid_chunks = (p.max_len + chunk - 1) / chunk;
-    const dim3 grid(static_cast<unsigned>(grid_chunks * layout.n_kv_heads), static_cast<unsigned>(n_streams));
-    if (layout.cache_type == QA_CACHE_F16) launch_chunk<_Float16, true>(chunk, fused, grid, p, rope, stream);
-    else launch_chunk<float, false>(chunk, fused, grid, p, rope, stream);
+    if (layout.cache_type == QA_CACHE_F16) launch_both<_Float16, true>(ch, fused, layout.n_kv_heads, n_streams, p, rope, stream);
+    else launch_both<float, false>(ch, fused, layout.n_kv_heads, n_streams, p, rope, stream);
     QA_LAUNCH_CHECK("decode attention kernels");
     return QA_OK;
 }

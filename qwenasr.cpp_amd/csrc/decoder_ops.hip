@@ -218,7 +218,32 @@ __device__ inline Cand better(Cand a, Cand b) {
 constexpr int kArgmaxBlocks = 64;
 constexpr int32_t kNoIndex = 0x7fffffff;
 
-__global__ __launch_bounds__(256) void argmax_kernel(const float * logits, int vocab, Cand * partial,
+// Block candidates are published as one 8-byte agent-scope atomic store each and read back by the
+// last block with agent-scope atomic loads (coherent across XCDs without an L2 write-back/invalidate
+// fence); a vmcnt wait orders the store before the counter increment.
+__device__ inline uint64_t pack_cand(Cand c) {
+    return static_cast<uint64_t>(__float_as_uint(c.v)) | (static_cast<uint64_t>(static_cast<uint32_t>(c.i)) << 32);
+}
+
+__device__ inline Cand unpack_cand(uint64_t u) {
+    Cand c;
+    c.v = __uint_as_float(static_cast<uint32_t>(u));
+    c.i = static_cast<int32_t>(static_cast<uint32_t>(u >> 32));
+    return c;
+}
+
+__device__ inline Cand wave_best(Cand c) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        Cand o;
+        o.v = __shfl_xor(c.v, off, kWave);
+        o.i = __shfl_xor(c.i, off, kWave);
+        c = better(c, o);
+    }
+    return c;
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const float * logits, int vocab, uint64_t * partial,
                                                      uint32_t * counters, int32_t * ids) {
     const int row = blockIdx.y;
     const int chunk = (vocab + kArgmaxBlocks - 1) / kArgmaxBlocks;
@@ -230,38 +255,26 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float * logits, int v
         const float v = lr[i];
         if (v > c.v) { c.v = v; c.i = i; }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        Cand o;
-        o.v = __shfl_xor(c.v, off, kWave);
-        o.i = __shfl_xor(c.i, off, kWave);
-        c = better(c, o);
-    }
+    c = wave_best(c);
     __shared__ Cand wc[4];
     if ((threadIdx.x & 63) == 0) wc[threadIdx.x >> 6] = c;
     __syncthreads();
     __shared__ int is_last;
     if (threadIdx.x == 0) {
-        Cand b = better(better(wc[0], wc[1]), better(wc[2], wc[3]));
-        partial[row * kArgmaxBlocks + blockIdx.x] = b;
-        __threadfence();
-        const uint32_t old = atomicAdd(counters + row, 1u);
+        const Cand b = better(better(wc[0], wc[1]), better(wc[2], wc[3]));
+        __hip_atomic_store(partial + row * kArgmaxBlocks + blockIdx.x, pack_cand(b), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const uint32_t old = __hip_atomic_fetch_add(counters + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         is_last = old == kArgmaxBlocks - 1;
-        if (is_last) atomicExch(counters + row, 0u);
+        if (is_last) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    if (threadIdx.x == 0) {
-        Cand b{-INFINITY, kNoIndex};
-        for (int k = 0; k < kArgmaxBlocks; ++k) {
-            Cand o;
-            o.v = __builtin_nontemporal_load(&partial[row * kArgmaxBlocks + k].v);
-            o.i = __builtin_nontemporal_load(&partial[row * kArgmaxBlocks + k].i);
-            b = better(b, o);
-        }
-        ids[row] = b.i == kNoIndex ? -1 : b.i;
-    }
+    if (!is_last || threadIdx.x >= kArgmaxBlocks) return;
+    Cand b = unpack_cand(__hip_atomic_load(partial + row * kArgmaxBlocks + threadIdx.x, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT));
+    b = wave_best(b);
+    if (threadIdx.x == 0) ids[row] = b.i == kNoIndex ? -1 : b.i;
 }
 
 }  // namespace
@@ -281,7 +294,8 @@ size_t argmax_workspace_bytes(int32_t rows) {
 
 int argmax_launch(const float * logits, int32_t rows, int32_t vocab, int32_t * ids, void * workspace,
                   hipStream_t stream) {
-    Cand * partial = static_cast<Cand *>(workspace);
+    static_assert(sizeof(Cand) == sizeof(uint64_t), "a candidate is published as one 8-byte store");
+    uint64_t * partial = static_cast<uint64_t *>(workspace);
     uint32_t * counters = reinterpret_cast<uint32_t *>(partial + static_cast<size_t>(rows) * kArgmaxBlocks);
     hipLaunchKernelGGL(argmax_kernel, dim3(kArgmaxBlocks, static_cast<unsigned>(rows)), dim3(256), 0, stream,
                        logits, vocab, partial, counters, ids);

@@ -67,7 +67,8 @@ def greedy(index: int):
     write(f"cfg{index}.json", dict(config=index, input_digest=digest(x, model.tensor("text.blk.0.attn_q.weight")),
                                    prompt_tokens=w.prompt, requested=w.new_tokens, ids=out["ids"],
                                    stopped=out["stopped"], total_tokens=out["total_tokens"], cur_len=out["cur_len"],
-                                   margins=out["margins"], oracle_seconds=round(time.time() - t0, 1)))
+                                   margins=out["margins"], runner_up=out["runner_up"],
+                                   oracle_seconds=round(time.time() - t0, 1)))
 
 
 def cfg4(n_check: int):
@@ -86,8 +87,9 @@ def cfg4(n_check: int):
         cache = om.cache(L + w.steps, f16=True)
         cache.fill(k, v, L)
         del k, v
-        ids, marg = om.decode_steps(cache, int(first[s]), w.steps)
-        streams[str(s)] = dict(length=L, first_id=int(first[s]), ids=ids, margins=marg, cur_len=cache.cur_len)
+        ids, marg, second = om.decode_steps(cache, int(first[s]), w.steps)
+        streams[str(s)] = dict(length=L, first_id=int(first[s]), ids=ids, margins=marg, runner_up=second,
+                               cur_len=cache.cur_len)
         print(f"  cfg4 stream {s} (len {L}) done at {time.time() - t0:.0f}s", flush=True)
     write("cfg4.json", dict(config=4, lengths=lens.tolist(), first_ids=first.tolist(), steps=w.steps,
                             streams=streams, oracle_seconds=round(time.time() - t0, 1)))

@@ -26,6 +26,27 @@ def golden(index):
         return json.load(f)
 
 
+# Logits of two f32 evaluations of the 28-layer decoder that differ only in summation order agree to
+# LOGIT_ATOL (asserted by test_teacher_forced_logits_within_tolerance on the long-context config).
+# A greedy pick can then differ only where the two top logits are closer than 2 * LOGIT_ATOL.
+LOGIT_ATOL = 2e-3
+TIE_EPS = 2 * LOGIT_ATOL
+
+
+def assert_greedy_match(got, ref, margins, runner_up, what):
+    """Greedy ids identical.  The one accepted difference is a first divergence at an oracle near-tie
+    (top-2 margin < TIE_EPS) where the GPU picked the oracle's runner-up; after it the two sequences
+    feed different tokens and are not compared further.  Returns the divergence index or None."""
+    for i, (a, b) in enumerate(zip(got, ref)):
+        if a != b:
+            assert margins[i] < TIE_EPS and a == runner_up[i], (what, i, a, b, margins[i], runner_up[i])
+            print(f"{what}: near-tie divergence at step {i} (oracle margin {margins[i]:.2e}, GPU took the "
+                  f"runner-up {a})", flush=True)
+            return i
+    assert len(got) == len(ref), (what, len(got), len(ref))
+    return None
+
+
 def close(got, ref, atol=2e-3, rtol_l2=1e-3):
     got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
     err = np.abs(got - ref).max()
@@ -71,7 +92,7 @@ def test_small_model_greedy_matches_oracle(qa, orc, f16):
     ref = om.generate(x, N, qa.STOP_IDS, om.cache(49 + N, f16))
     with qa.Decoder(model, 1, 49 + N, qa.QA_CACHE_F16 if f16 else qa.QA_CACHE_F32) as dec:
         out = dec.generate(x, N, margins=True)
-        assert out["ids"] == ref["ids"], (out["margins"], ref["margins"])
+        assert assert_greedy_match(out["ids"], ref["ids"], ref["margins"], ref["runner_up"], "small") is None
         assert out["total_tokens"] == ref["total_tokens"] and out["stopped"] == ref["stopped"]
         assert dec.cur_len(0) == ref["cur_len"] == 49 + N - 1
         assert dec.device_lens().tolist() == [ref["cur_len"]]
@@ -107,10 +128,13 @@ def test_config_greedy_matches_golden(qa, index):
     print(f"config {index}: prompt {w.prompt}, {w.new_tokens} tokens", flush=True)
     with qa.Decoder(model, 1, w.max_seq, w.cache_type) as dec:
         out = dec.generate(x, w.new_tokens, margins=True)
-        first_diff = next((i for i, (a, b) in enumerate(zip(out["ids"], g["ids"])) if a != b), None)
-        assert out["ids"] == g["ids"], (first_diff, g["margins"][first_diff] if first_diff is not None else None)
-        assert out["stopped"] == g["stopped"] and out["total_tokens"] == g["total_tokens"]
-        assert dec.cur_len(0) == g["cur_len"] and dec.device_lens().tolist() == [g["cur_len"]]
+        div = assert_greedy_match(out["ids"], g["ids"], g["margins"], g["runner_up"], f"config {index}")
+        if div is None:
+            assert out["stopped"] == g["stopped"] and out["total_tokens"] == g["total_tokens"]
+            assert dec.cur_len(0) == g["cur_len"]
+        # bookkeeping is exact whatever the ids: one prefill + (n - 1) decode forwards
+        assert dec.cur_len(0) == w.prompt + len(out["ids"]) - 1 == out["total_tokens"] - 1
+        assert dec.device_lens().tolist() == [dec.cur_len(0)]
 
 
 def test_config4_ragged_streams_match_golden(qa):
@@ -131,9 +155,41 @@ def test_config4_ragged_streams_match_golden(qa):
         ids = dec.decode_streams(first, w.steps)
         assert ids.shape == (w.steps, w.streams)
         for s, ref in g["streams"].items():
-            assert ids[:, int(s)].tolist() == ref["ids"], s
+            assert_greedy_match(ids[:, int(s)].tolist(), ref["ids"], ref["margins"], ref["runner_up"], f"stream {s}")
         assert dec.device_lens().tolist() == (lens + w.steps).tolist()
         assert [dec.cur_len(s) for s in range(w.streams)] == (lens + w.steps).tolist()
+
+
+def test_teacher_forced_logits_within_tolerance(qa, orc):
+    """Config-4 stream 11 (context 3648, the stream with the smallest oracle margin): GPU and oracle
+    decode the same tokens (the oracle's picks) step by step from bit-identical caches; every logit of
+    every step agrees to LOGIT_ATOL.  This is the bound the near-tie rule of assert_greedy_match uses."""
+    from qwenasr_amd import configs
+
+    w = configs.CONFIGS[4]
+    s = 11
+    L = int(configs.cfg4_lengths(w.streams)[s])
+    tok = int(configs.cfg4_first_ids(w.streams)[s])
+    model = qa.Model(w.size, n_layers=w.n_layers)
+    om = orc.OracleModel.from_product_model(model)
+    k, v = configs.cfg4_stream_kv(s, L)
+    steps = 6
+    cache = om.cache(L + steps, True)
+    cache.fill(k, v, L)
+    worst = 0.0
+    with qa.Decoder(model, 1, L + steps, qa.QA_CACHE_F16) as dec:
+        dec.fill_cache(0, k, v, L)
+        del k, v
+        for step in range(steps):
+            x = model.embed([tok])
+            got = dec.forward(x, L + step)
+            ref = om.forward_cached(x, L + step, cache)
+            err = float(np.abs(got.astype(np.float64) - ref).max())
+            worst = max(worst, err)
+            print(f"step {step}: max|dlogit| {err:.2e}", flush=True)
+            assert err < LOGIT_ATOL, (step, err)
+            tok = int(np.argmax(ref))
+    print(f"worst max|dlogit| {worst:.2e} (bound {LOGIT_ATOL})", flush=True)
 
 
 def test_drop_in_tool_generate(qa, orc):

@@ -118,6 +118,22 @@ def attention_roofline(qa, dec, reps: int):
     return us, L, bytes_per_launch, n
 
 
+def copy_calibration(reps: int = 10, mib: int = 256):
+    """A plain device-to-device copy of known size: the reference that rocprofv3's FETCH_SIZE and
+    WRITE_SIZE counters (KiB per dispatch) are scaled by when they are turned into HBM bytes."""
+    import numpy as np
+    import qwenasr_amd as qa
+
+    n = mib << 20
+    src = qa.DeviceArray(n, np.uint8)
+    dst = qa.DeviceArray(n, np.uint8, zero=False)
+    qa.synchronize()
+    for _ in range(reps):
+        qa.check(qa.lib.qa_copy_device(dst.ptr, src.ptr, n, None))
+    qa.synchronize()
+    print(json.dumps({"copy_calibration": {"bytes_per_copy": n, "copies": reps}}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -128,7 +144,12 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 256 MiB device copy 10 times (reference for HBM traffic counters)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the KV-cache path would shard by "
               "KV head or by stream); run with --gpus 1", file=sys.stderr)

@@ -55,6 +55,8 @@ int qa_device_synchronize(void);
 int qa_device_malloc(void ** out, size_t bytes);
 int qa_device_free(void * dev_ptr);
 int qa_copy_to_device(void * dev_dst, const void * host_src, size_t bytes);
+/* Device-to-device copy on `stream` (also the known-size reference for HBM traffic counters). */
+int qa_copy_device(void * dev_dst, const void * dev_src, size_t bytes, void * stream);
 int qa_memset_device(void * dev_dst, int value, size_t bytes);
 int qa_event_create(void ** event);
 int qa_event_destroy(void * event);

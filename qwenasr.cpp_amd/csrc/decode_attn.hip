@@ -470,7 +470,10 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
 // Positions per workgroup of each kernel.  The scores kernel has no merge, so it uses small chunks
 // (many workgroups in flight); the values kernel's chunks are the merge participants of one
 // (stream, KV head), so it uses chunks large enough to keep them at <= 16 per unit (every participant
-// increments the same counter).  QA_DECODE_CHUNK / QA_DECODE_VCHUNK override the choice (tuning).
+// increments the same counter).  The choice depends on the cache capacity only, never on a call's
+// length, so a captured decode step (grids sized by capacity) and an eager one (grids sized by the
+// longest stream) run the same tiling and produce the same bits.  QA_DECODE_CHUNK / QA_DECODE_VCHUNK
+// override the choice (tuning).
 struct Chunks {
     int scores, values;
 };
@@ -481,14 +484,14 @@ int env_chunk(const char * name) {
     return v == 32 || v == 64 || v == 128 || v == 256 ? v : 0;
 }
 
-Chunks pick_chunks(int32_t n_streams, int32_t n_kv, int32_t max_len) {
+Chunks pick_chunks(int32_t n_streams, int32_t n_kv, int32_t capacity) {
     static const int forced_s = env_chunk("QA_DECODE_CHUNK");
     static const int forced_v = env_chunk("QA_DECODE_VCHUNK");
     Chunks ch{};
-    const int64_t wg32 = static_cast<int64_t>(n_streams) * n_kv * ((max_len + 31) / 32);
+    const int64_t wg32 = static_cast<int64_t>(n_streams) * n_kv * ((capacity + 31) / 32);
     ch.scores = forced_s && forced_s <= 128 ? forced_s : wg32 < 2048 ? 32 : wg32 < 16384 ? 64 : 128;
     int v = 32;
-    while (v < 256 && (max_len + v - 1) / v > 16) v *= 2;
+    while (v < 256 && (capacity + v - 1) / v > 16) v *= 2;
     ch.values = forced_v ? forced_v : v;
     if (ch.values < ch.scores) ch.values = ch.scores;
     return ch;
@@ -526,7 +529,7 @@ void launch_both(const Chunks & ch, bool fused, int32_t n_kv, int32_t n_streams,
 
 int launch_decode(DecodeParams p, bool fused, const RopeTable & rope, const qa_kv_layout & layout,
                   int32_t n_streams, void * workspace, size_t workspace_bytes, hipStream_t stream) {
-    const Chunks ch = pick_chunks(n_streams, layout.n_kv_heads, p.max_len);
+    const Chunks ch = pick_chunks(layout.n_streams, layout.n_kv_heads, layout.max_seq);
     const Workspace w = workspace_layout(layout.n_streams, layout.n_kv_heads, layout.max_seq);
     if (!workspace || workspace_bytes < w.total) {
         return fail(QA_ERR_INVALID, "decode attention: workspace too small for the cache capacity");

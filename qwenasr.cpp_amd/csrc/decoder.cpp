@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -67,6 +68,12 @@ struct qa_decoder {
     float * staging = nullptr;
     size_t staging_bytes = 0;
     float scale = 0.0f;
+    // captured decode step (one token per stream, grids sized by capacity), replayed every step
+    hipGraphExec_t step_exec = nullptr;
+    int32_t step_rows = 0;
+    uint64_t act_gen = 1;       // bumped whenever the activation buffers are reallocated
+    uint64_t step_gen = 0;
+    bool use_graph = true;
     // profiling
     bool prof = false;
     struct Rec { int fam; hipEvent_t a, b; };
@@ -145,6 +152,7 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
         return rc;
     }
     d->cap_rows = rows;
+    ++d->act_gen;
     return QA_OK;
 }
 
@@ -170,7 +178,7 @@ int32_t host_max_len(const qa_decoder * d, int32_t n, int32_t add) {
 //   kDecode : rows = number of streams (one token each), positions d_lens[s], keys [0, d_lens[s] + 1)
 //   kPrefill: rows = T tokens of stream 0 at positions n_past.., keys [0, n_past + t]
 //   kNoCache: rows = T tokens, positions 0..T-1, f32 K/V never stored
-int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past) {
+int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past, int32_t max_len = 0) {
     const qa_text_config & c = d->cfg;
     const DevLayer & L = d->layers[l];
     const int32_t H = c.hidden, QD = c.n_heads * kHeadDim, KD = c.n_kv_heads * kHeadDim, I = c.intermediate;
@@ -202,8 +210,8 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past)
         // append + attend in one launch: one token per stream at position d_lens[s]
         Prof pr(d, kFamDecodeAttn);
         rc = decode_step_attn_launch(d->qkv, L.q_norm, L.k_norm, d->cache, d->layout, l, d->d_lens, rows,
-                                     host_max_len(d, rows, 1), c.n_heads, c.rope_theta, c.rms_norm_eps, d->scale,
-                                     d->attn, d->attn_ws, d->attn_ws_bytes, s);
+                                     max_len > 0 ? max_len : host_max_len(d, rows, 1), c.n_heads, c.rope_theta,
+                                     c.rms_norm_eps, d->scale, d->attn, d->attn_ws, d->attn_ws_bytes, s);
         if (rc != QA_OK) return rc;
     } else {
         {
@@ -278,6 +286,58 @@ int forward_device(qa_decoder * d, int32_t n_tokens, int32_t n_past, bool pick) 
     return rc;
 }
 
+// One decode step of `rows` streams with the token ids already in d_ids: embedding gather, every
+// layer (fused append + attention at position d_lens[s]), LM head, greedy pick into d_ids, and
+// d_lens[s] += 1.  Only device memory is read for lengths and ids, so the sequence is capturable.
+int decode_step_ops(qa_decoder * d, int32_t rows, int32_t max_len) {
+    int rc = embed_rows_launch(d->embd, d->cfg.vocab, d->cfg.hidden, d->d_ids, rows, d->x, d->stream);
+    for (int32_t l = 0; l < d->cfg.n_layers && rc == QA_OK; ++l) rc = run_layer(d, l, rows, kDecode, 0, max_len);
+    if (rc == QA_OK) rc = logits_and_pick(d, 0, rows, true);
+    if (rc == QA_OK) rc = advance_lens_launch(d->d_lens, rows, 1, d->stream);
+    return rc;
+}
+
+void drop_step_graph(qa_decoder * d) {
+    if (d->step_exec) (void)hipGraphExecDestroy(d->step_exec);
+    d->step_exec = nullptr;
+    d->step_rows = 0;
+}
+
+// Single-stream steps replay a captured graph (every kernel of the step is this library's; the
+// multi-stream projections go through rocBLAS and stay eager).  The capture sizes the attention grids
+// by the cache capacity; workgroups past a stream's length exit at once, and the tiling depends on
+// the capacity only, so replay and eager execution give the same bits.
+int decode_step(qa_decoder * d, int32_t rows) {
+    if (!d->use_graph || d->prof || rows != 1) {
+        const int rc = decode_step_ops(d, rows, host_max_len(d, rows, 1));
+        if (rc != QA_OK) return rc;
+    } else {
+        if (!d->step_exec || d->step_rows != rows || d->step_gen != d->act_gen) {
+            drop_step_graph(d);
+            QA_HIP(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
+            const int rc = decode_step_ops(d, rows, d->max_seq);
+            hipGraph_t graph = nullptr;
+            const hipError_t end = hipStreamEndCapture(d->stream, &graph);
+            if (rc != QA_OK) {
+                if (graph) (void)hipGraphDestroy(graph);
+                return rc;
+            }
+            if (end != hipSuccess) return hip_fail(end, "hipStreamEndCapture (decode step)");
+            const hipError_t inst = hipGraphInstantiate(&d->step_exec, graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            if (inst != hipSuccess) {
+                d->step_exec = nullptr;
+                return hip_fail(inst, "hipGraphInstantiate (decode step)");
+            }
+            d->step_rows = rows;
+            d->step_gen = d->act_gen;
+        }
+        QA_HIP(hipGraphLaunch(d->step_exec, d->stream));
+    }
+    for (int32_t s = 0; s < rows; ++s) d->cur_len[s] += 1;
+    return QA_OK;
+}
+
 float top2_margin(const std::vector<float> & v, int32_t best) {
     float second = -INFINITY;
     for (size_t i = 0; i < v.size(); ++i) {
@@ -312,6 +372,7 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
     d->cache_type = cache_type;
     d->scale = 1.0f / std::sqrt(static_cast<float>(cfg->head_dim));
     d->cur_len.assign(static_cast<size_t>(n_streams), 0);
+    if (const char * e = std::getenv("QA_DECODE_GRAPH")) d->use_graph = std::strcmp(e, "0") != 0;
     auto bail = [&](int rc) {
         qa_decoder_destroy(d);
         return rc;
@@ -404,6 +465,7 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
 extern "C" void qa_decoder_destroy(qa_decoder * d) {
     if (!d) return;
     if (d->stream) (void)hipStreamSynchronize(d->stream);
+    drop_step_graph(d);
     for (auto & r : d->recs) {
         if (r.a) (void)hipEventDestroy(r.a);
         if (r.b) (void)hipEventDestroy(r.b);
@@ -503,8 +565,7 @@ extern "C" int qa_decoder_generate(qa_decoder * d, const float * x, int32_t n_to
             break;
         }
         if (step + 1 >= max_new) break;
-        rc = embed_rows_launch(d->embd, V, d->cfg.hidden, d->d_ids, 1, d->x, d->stream);
-        if (rc == QA_OK) rc = forward_device(d, 1, d->cur_len[0], true);
+        rc = decode_step(d, 1);
         if (rc != QA_OK) return rc;
     }
     QA_HIP(hipStreamSynchronize(d->stream));
@@ -528,12 +589,8 @@ extern "C" int qa_decoder_decode_streams(qa_decoder * d, const int32_t * first_i
     if (rc != QA_OK) return rc;
     QA_HIP(hipMemcpyAsync(d->d_ids, first_ids, sizeof(int32_t) * S, hipMemcpyHostToDevice, d->stream));
     for (int32_t k = 0; k < n_steps; ++k) {
-        rc = embed_rows_launch(d->embd, d->cfg.vocab, d->cfg.hidden, d->d_ids, S, d->x, d->stream);
-        for (int32_t l = 0; l < d->cfg.n_layers && rc == QA_OK; ++l) rc = run_layer(d, l, S, kDecode, 0);
-        if (rc == QA_OK) rc = logits_and_pick(d, 0, S, true);
-        if (rc == QA_OK) rc = advance_lens_launch(d->d_lens, S, 1, d->stream);
+        rc = decode_step(d, S);
         if (rc != QA_OK) return rc;
-        for (int32_t s = 0; s < S; ++s) d->cur_len[s] += 1;
         QA_HIP(hipMemcpyAsync(d->h_ids + static_cast<size_t>(k) * S, d->d_ids, sizeof(int32_t) * S,
                               hipMemcpyDeviceToHost, d->stream));
     }

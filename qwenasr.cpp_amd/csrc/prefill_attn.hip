@@ -9,9 +9,10 @@
 // before QK^T and the normalised probabilities are rounded to f16 before PV; scores are scaled,
 // the max is exact, expf(x - max) is summed in double and multiplied by (float)(1/sum).
 //
-// prefill_rows_kernel: one workgroup per (query, KV head); both query heads of the GQA group share
-// every loaded K/V element.  The scores of the query are kept in LDS (keys <= 8192), so K and V are
-// each read once per query.  Used for f32 K/V (a8 and f32 caches) and as the general fallback.
+// f16 caches run on CDNA4 f16 MFMA (prefill_mfma.hip).  prefill_rows_kernel serves f32 K/V (the
+// non-cached layer of text-decoder.cpp:265-345 and f32 caches), where the reference's arithmetic is
+// f32 throughout: one workgroup per (query, KV head), both query heads of the GQA group share every
+// loaded K/V element, the scores of the query stay in LDS (keys <= 8192).
 #include "ops.hpp"
 
 #include <cmath>
@@ -223,8 +224,18 @@ int prefill_attn_launch(const float * q, int32_t q_stride, const void * cache, c
         n_past < 0 || n_tokens <= 0 || n_past + n_tokens > layout.max_seq) {
         return fail(QA_ERR_INVALID, "prefill attention: invalid layer, stream or range");
     }
+    const size_t esz = qa_kv_elem_bytes(layout.cache_type);
+    const char * base = static_cast<const char *>(cache);
+    const void * k0 = base + esz * cache_row_offset(layer, 0, stream_idx, 0, 0, layout.n_streams, layout.n_kv_heads,
+                                                    layout.max_seq);
+    const void * v0 = base + esz * cache_row_offset(layer, 1, stream_idx, 0, 0, layout.n_streams, layout.n_kv_heads,
+                                                    layout.max_seq);
+    if (layout.cache_type == QA_CACHE_F16) {
+        return prefill_mfma_launch(q, q_stride, k0, v0, static_cast<int64_t>(layout.max_seq) * kHeadDim, n_past,
+                                   n_tokens, layout.n_kv_heads, scale, out, stream);
+    }
     if (n_past + n_tokens > kMaxRowsKeys) {
-        return fail(QA_ERR_INVALID, "prefill attention: more than 8192 keys");
+        return fail(QA_ERR_INVALID, "prefill attention: more than 8192 keys with an f32 cache");
     }
     RowsParams p{};
     p.q = q;
@@ -235,11 +246,8 @@ int prefill_attn_launch(const float * q, int32_t q_stride, const void * cache, c
     p.scale = scale;
     p.head_stride = static_cast<int64_t>(layout.max_seq) * kHeadDim;
     p.row_stride = kHeadDim;
-    const size_t esz = qa_kv_elem_bytes(layout.cache_type);
-    const char * base = static_cast<const char *>(cache);
-    p.k = base + esz * cache_row_offset(layer, 0, stream_idx, 0, 0, layout.n_streams, layout.n_kv_heads, layout.max_seq);
-    p.v = base + esz * cache_row_offset(layer, 1, stream_idx, 0, 0, layout.n_streams, layout.n_kv_heads, layout.max_seq);
-    if (layout.cache_type == QA_CACHE_F16) return launch_rows<_Float16, true>(p, layout.n_kv_heads, stream);
+    p.k = k0;
+    p.v = v0;
     return launch_rows<float, false>(p, layout.n_kv_heads, stream);
 }
 

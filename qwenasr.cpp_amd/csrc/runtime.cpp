@@ -89,6 +89,12 @@ extern "C" int qa_copy_to_device(void * dev_dst, const void * host_src, size_t b
     return QA_OK;
 }
 
+extern "C" int qa_copy_device(void * dev_dst, const void * dev_src, size_t bytes, void * stream) {
+    if (!dev_dst || !dev_src) return fail(QA_ERR_INVALID, "qa_copy_device: null pointer");
+    QA_HIP(hipMemcpyAsync(dev_dst, dev_src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)));
+    return QA_OK;
+}
+
 extern "C" int qa_memset_device(void * dev_dst, int value, size_t bytes) {
     if (!dev_dst) return fail(QA_ERR_INVALID, "qa_memset_device: null pointer");
     QA_HIP(hipMemset(dev_dst, value, bytes));

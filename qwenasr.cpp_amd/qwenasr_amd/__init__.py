@@ -76,6 +76,7 @@ SIGNATURES = {
     "qa_device_malloc": (C.c_int, C.POINTER(vp), sz),
     "qa_device_free": (C.c_int, vp),
     "qa_copy_to_device": (C.c_int, vp, vp, sz),
+    "qa_copy_device": (C.c_int, vp, vp, sz, vp),
     "qa_memset_device": (C.c_int, vp, C.c_int, sz),
     "qa_event_create": (C.c_int, C.POINTER(vp)),
     "qa_event_destroy": (C.c_int, vp),

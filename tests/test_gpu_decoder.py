@@ -160,6 +160,25 @@ def test_config4_ragged_streams_match_golden(qa):
         assert [dec.cur_len(s) for s in range(w.streams)] == (lens + w.steps).tolist()
 
 
+def test_graph_replay_equals_eager(qa, monkeypatch):
+    """The captured decode step (HIP graph, replayed every token) and the eager launch sequence give
+    bit-identical ids and logit margins, over repeated generate calls with eager prefills in between
+    (each call re-runs the prefill eagerly and replays the same graph)."""
+    model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=4)
+    x = qa.prompt_input(model, 30, 7)
+    runs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("QA_DECODE_GRAPH", mode)
+        with qa.Decoder(model, 1, 37 + 20, qa.QA_CACHE_F16) as dec:
+            outs = [dec.generate(x, 20, stop_ids=[], margins=True) for _ in range(3)]
+            logits = dec.forward(x, 0)
+        for o in outs[1:]:
+            assert o == outs[0]
+        runs[mode] = (outs[0], logits)
+    assert runs["1"][0] == runs["0"][0]
+    np.testing.assert_array_equal(runs["1"][1].view(np.uint32), runs["0"][1].view(np.uint32))
+
+
 def test_teacher_forced_logits_within_tolerance(qa, orc):
     """Config-4 stream 11 (context 3648, the stream with the smallest oracle margin): GPU and oracle
     decode the same tokens (the oracle's picks) step by step from bit-identical caches; every logit of

@@ -69,6 +69,20 @@ def cpu_baseline(model, length: int, steps: int):
                        f"context {length + 1}..{length + steps + 1}, f16 cache, {dt:.1f} s")
 
 
+def measured_traffic(bytes_per_launch: int):
+    """HBM bytes per decode-attention launch pair from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    measurement (scaled by the plain-copy calibration), carried to this run's context by the measured
+    traffic / algorithmic ratio; None when the measurement file is absent."""
+    path = os.path.join(ROOT, "profiles", "decode_attention_traffic.json")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        t = json.load(f)
+    ratio = t["traffic_bytes"] / t["algorithmic_bytes"]
+    return round(ratio * bytes_per_launch), {"measured_at_positions": t["attended_positions"],
+                                            "traffic_over_algorithmic": round(ratio, 4), "source": t["source"]}
+
+
 def attention_roofline(qa, dec, reps: int):
     """Average duration of one layer's decode-step attention (fused append + split-K attention: the
     scores and values kernels), back to back on the decoder stream, HIP events from the C ABI."""
@@ -132,6 +146,60 @@ def copy_calibration(reps: int = 10, mib: int = 256):
         qa.check(qa.lib.qa_copy_device(dst.ptr, src.ptr, n, None))
     qa.synchronize()
     print(json.dumps({"copy_calibration": {"bytes_per_copy": n, "copies": reps}}), flush=True)
+
+
+def multistream_roofline(qa, cfg, reps: int):
+    """Config-4 shapes: 32 streams, context lengths U[156, 3913] (the config's seeded lengths), one
+    decode-step attention launch pair per layer covering all streams, rotating over 28 layer caches
+    (14.6 GB of f16 KV).  Cache contents do not change the bytes moved, so the cache stays zeroed."""
+    import ctypes as C
+
+    import numpy as np
+    from qwenasr_amd import configs
+
+    w = configs.CONFIGS[4]
+    lens = configs.cfg4_lengths(w.streams).astype(np.int32)
+    S = w.streams
+    cap = int(lens.max()) + 2
+    lay = qa.KvLayout(cfg.n_layers, S, cfg.n_kv_heads, cfg.head_dim, cap, qa.QA_CACHE_F16)
+    cache = qa.DeviceArray(qa.lib.qa_kv_cache_bytes(C.byref(lay)), np.uint8)
+    q_dim, kv_dim = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    qkv = qa.DeviceArray.from_numpy(np.random.default_rng(6).standard_normal((S, q_dim + 2 * kv_dim)).astype(np.float32))
+    ones = qa.DeviceArray.from_numpy(np.ones(cfg.head_dim, np.float32))
+    n_past = qa.DeviceArray.from_numpy(lens)
+    out = qa.DeviceArray((S, q_dim))
+    ws_bytes = qa.lib.qa_decode_attn_workspace_bytes(S, cfg.n_heads, cap)
+    ws = qa.DeviceArray(ws_bytes, np.uint8)
+    qa.synchronize()
+    scale = 1.0 / (cfg.head_dim ** 0.5)
+    max_len = int(lens.max()) + 1
+
+    def launch(layer):
+        qa.check(qa.lib.qa_decode_step_attn(qkv.ptr, ones.ptr, ones.ptr, cache.ptr, C.byref(lay), layer, n_past.ptr, S,
+                                            max_len, cfg.n_heads, cfg.rope_theta, cfg.rms_norm_eps, scale, out.ptr,
+                                            ws.ptr, ws_bytes, None))
+
+    for layer in range(lay.n_layers):
+        launch(layer)
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    qa.check(qa.lib.qa_event_create(C.byref(e0)))
+    qa.check(qa.lib.qa_event_create(C.byref(e1)))
+    qa.check(qa.lib.qa_event_record(e0, None))
+    for _ in range(reps):
+        for layer in range(lay.n_layers):
+            launch(layer)
+    qa.check(qa.lib.qa_event_record(e1, None))
+    ms = C.c_float()
+    qa.check(qa.lib.qa_event_elapsed_ms(e0, e1, C.byref(ms)))
+    qa.lib.qa_event_destroy(e0)
+    qa.lib.qa_event_destroy(e1)
+    us = ms.value * 1e3 / (reps * lay.n_layers)
+    nbytes = int(sum(4096 * (int(L) + 1) + 16384 for L in lens))
+    achieved = nbytes / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3),
+            "workload": f"config 4 shapes: {S} streams, contexts {int(lens.min()) + 1}..{int(lens.max()) + 1} "
+                        f"(mean {float(lens.mean()) + 1:.0f}), one layer's decode-step attention per launch pair"}
 
 
 def main():
@@ -202,6 +270,12 @@ def main():
     log(f"decode-step attention: {attn_us:.2f} us per launch over {n_launch} launches at L={L}: "
         f"{achieved:.0f} GB/s")
 
+    dec.close()
+    roof4 = multistream_roofline(qa, model.cfg, max(2, args.roofline_reps // 4))
+    log(f"config-4 multi-stream attention: {roof4['avg_launch_us']:.1f} us per layer, {roof4['achieved']:.0f} GB/s "
+        f"({100 * roof4['frac']:.1f}% of peak)")
+
+    traffic, traffic_note = measured_traffic(attn_bytes)
     weight_bytes = int(4 * sum(model.tensor(n).size for n in (
         [f"text.blk.{l}.{t}.weight" for l in range(model.cfg.n_layers) for t in
          ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")] + ["text.output.weight"])))
@@ -223,16 +297,16 @@ def main():
                                f"f32 weights, batch 1",
                    "kv_cache": "f16", "prompt_positions": w.prompt},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": traffic_note,
                      "kernel": "decode attention of one layer: decode_scores_kernel (fused K/V append) + "
                                "decode_values_kernel, launched back to back",
                      "bytes_per_launch": attn_bytes, "attended_positions": L, "avg_launch_us": round(attn_us, 3)},
+        "roofline_multistream": roof4,
         "attn_us_per_layer": round(attn_us, 3),
         "prefill_ms": round(prefill_ms, 2),
         "weight_bytes_per_token": weight_bytes,
         "weight_stream_gbs": round(weight_bytes / (dt / args.steps) / 1e9, 1),
     }
-    dec.close()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(model, ctx0, args.cpu_steps)
     else:

@@ -73,7 +73,7 @@ struct qa_decoder {
     int32_t step_rows = 0;
     uint64_t act_gen = 1;       // bumped whenever the activation buffers are reallocated
     uint64_t step_gen = 0;
-    bool use_graph = true;
+    bool use_graph = false;     // QA_DECODE_GRAPH=1: replay the captured step (measured no faster here)
     // profiling
     bool prof = false;
     struct Rec { int fam; hipEvent_t a, b; };
@@ -303,8 +303,10 @@ void drop_step_graph(qa_decoder * d) {
     d->step_rows = 0;
 }
 
-// Single-stream steps replay a captured graph (every kernel of the step is this library's; the
-// multi-stream projections go through rocBLAS and stay eager).  The capture sizes the attention grids
+// With QA_DECODE_GRAPH=1, single-stream steps replay a captured graph (every kernel of the step is
+// this library's; the multi-stream projections go through rocBLAS and stay eager).  On MI355X the
+// replay measured the same per-token time as eager launches (the step's kernels are large enough that
+// dispatch latency is hidden), so eager is the default.  The capture sizes the attention grids
 // by the cache capacity; workgroups past a stream's length exit at once, and the tiling depends on
 // the capacity only, so replay and eager execution give the same bits.
 int decode_step(qa_decoder * d, int32_t rows) {
@@ -372,7 +374,7 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
     d->cache_type = cache_type;
     d->scale = 1.0f / std::sqrt(static_cast<float>(cfg->head_dim));
     d->cur_len.assign(static_cast<size_t>(n_streams), 0);
-    if (const char * e = std::getenv("QA_DECODE_GRAPH")) d->use_graph = std::strcmp(e, "0") != 0;
+    if (const char * e = std::getenv("QA_DECODE_GRAPH")) d->use_graph = std::strcmp(e, "1") == 0;
     auto bail = [&](int rc) {
         qa_decoder_destroy(d);
         return rc;

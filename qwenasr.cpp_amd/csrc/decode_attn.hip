@@ -149,10 +149,39 @@ struct Slice<float> {
 
 __device__ inline float round_f16(float x) { return static_cast<float>(static_cast<_Float16>(x)); }
 
-// Sum over the 16 lanes that hold one row (lane bits 0-3).
+// Probabilities are kept as f16 when V is f16 (the rounding the reference applies before PV), else f32.
+template <bool R16>
+struct PStore {
+    typedef float type;
+};
+template <>
+struct PStore<true> {
+    typedef _Float16 type;
+};
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// Elements 2I, 2I + 1 of an f16 slice as one packed pair.
+template <int I>
+__device__ inline h2 pair_of(const Slice<_Float16> & s) {
+    return __builtin_shufflevector(s.x, s.x, 2 * I, 2 * I + 1);
+}
+
+// DPP lane permutation of a float within rows of 16 lanes (VALU, no LDS round trip).
+template <int CTRL>
+__device__ inline float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 16 lanes that hold one row (lane bits 0-3): quad_perm [1,0,3,2] and [2,3,0,1] pair the
+// lanes of each quad, row_half_mirror pairs the two quads of each half row, row_mirror the two halves.
+// Every step adds two partial sums in both lanes (a + b == b + a), so all 16 lanes end with the same
+// bits.
 __device__ inline float row_sum16(float v) {
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    v += dpp<0xB1>(v);      // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);      // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);     // row_half_mirror
+    v += dpp<0x140>(v);     // row_mirror
     return v;
 }
 
@@ -259,14 +288,35 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(DecodeParams p,
     float m0 = -INFINITY, m1 = -INFINITY;
     float * sc0 = p.scores + (static_cast<int64_t>(s) * p.n_heads + h0) * p.score_stride;
     float * sc1 = sc0 + p.score_stride;
+    // f16 cache: q (already rounded to f16) and K as f16 pairs on v_dot2_f32_f16: exact f16 products,
+    // f32 sums -- the f16 dot type of the reference's mul_mat with f32 precision, in 8 instead of 24
+    // VALU operations per row and head
+    h2 qa2[4], qb2[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        qa2[i] = h2{static_cast<_Float16>(q0[2 * i]), static_cast<_Float16>(q0[2 * i + 1])};
+        qb2[i] = h2{static_cast<_Float16>(q1[2 * i]), static_cast<_Float16>(q1[2 * i + 1])};
+    }
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
         float a = 0.0f, b = 0.0f;
+        if constexpr (R16) {
+            const h2 k0 = pair_of<0>(ks[k]), k1 = pair_of<1>(ks[k]), k2 = pair_of<2>(ks[k]), k3 = pair_of<3>(ks[k]);
+            a = __builtin_amdgcn_fdot2(k0, qa2[0], a, false);
+            b = __builtin_amdgcn_fdot2(k0, qb2[0], b, false);
+            a = __builtin_amdgcn_fdot2(k1, qa2[1], a, false);
+            b = __builtin_amdgcn_fdot2(k1, qb2[1], b, false);
+            a = __builtin_amdgcn_fdot2(k2, qa2[2], a, false);
+            b = __builtin_amdgcn_fdot2(k2, qb2[2], b, false);
+            a = __builtin_amdgcn_fdot2(k3, qa2[3], a, false);
+            b = __builtin_amdgcn_fdot2(k3, qb2[3], b, false);
+        } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float kv = ks[k].get(i);
-            a = fmaf(q0[i], kv, a);
-            b = fmaf(q1[i], kv, b);
+            for (int i = 0; i < 8; ++i) {
+                const float kv = ks[k].get(i);
+                a = fmaf(q0[i], kv, a);
+                b = fmaf(q1[i], kv, b);
+            }
         }
         a = row_sum16(a) * p.scale;
         b = row_sum16(b) * p.scale;
@@ -330,24 +380,32 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
     const int h0 = g * kRep;
     const int row0 = c * CHUNK + wave * (CHUNK / 4);
 
-    // V rows and the scores of the chunk in flight first
+    // V rows of the chunk in flight first; each lane also loads the one score it turns into p below
+    // (the wave's CHUNK / 4 rows are row0 .. row0 + RW - 1; lane -> row lane % RW, and for RW <= 32
+    // head (lane / RW) & 1, so every (row, head) probability is computed once, not by all 16 lanes
+    // that hold a slice of that row)
+    constexpr int RW = CHUNK / 4;
     const CT * vb = static_cast<const CT *>(p.cache) +
                     cache_row_offset(p.layer, 1, s, g, 0, p.n_streams, p.n_kv_heads, p.max_seq) + part * 8;
     const float * sc0 = p.scores + (static_cast<int64_t>(s) * p.n_heads + h0) * p.score_stride;
     const float * sc1 = sc0 + p.score_stride;
     Slice<CT> vs[RPT];
-    float x0[RPT], x1[RPT];
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
         const int j = row0 + k * 4 + sub;
-        if (j < L) {
-            vs[k].load(vb + static_cast<int64_t>(j) * kHeadDim);
-            x0[k] = sc0[j];
-            x1[k] = sc1[j];
+        if (j < L) vs[k].load(vb + static_cast<int64_t>(j) * kHeadDim);
+        else vs[k].zero();
+    }
+    const int own = lane % RW;
+    const int jr = row0 + own;
+    const int hsel = RW >= kWave ? 0 : (lane / RW) & 1;
+    float xs0 = -INFINITY, xs1 = -INFINITY;
+    if (jr < L) {
+        if constexpr (RW >= kWave) {
+            xs0 = sc0[jr];
+            xs1 = sc1[jr];
         } else {
-            vs[k].zero();
-            x0[k] = -INFINITY;
-            x1[k] = -INFINITY;
+            xs0 = (hsel ? sc1 : sc0)[jr];
         }
     }
 
@@ -377,39 +435,83 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
     const float r0 = static_cast<float>(1.0 / S0);
     const float r1 = static_cast<float>(1.0 / S1);
 
+    // normalised probabilities of this lane's (row, head), rounded to f16 for an f16 V, shared in LDS.
+    // Row k * 4 + sub of the wave is stored at sub * RPT + k, so the lanes of group `sub` read the pair
+    // (k, k + 1) as one 32-bit word.
+    typedef typename PStore<R16>::type PT;
+    __shared__ __attribute__((aligned(16))) PT s_p[4][kRep][kWave];
+    {
+        const float Ma = hsel ? M1 : M0, ra = hsel ? r1 : r0;
+        float pa = xs0 == -INFINITY ? 0.0f : expf(xs0 - Ma) * ra;
+        const int slot = (own & 3) * RPT + (own >> 2);
+        if constexpr (RW >= kWave) {
+            const float pb = xs1 == -INFINITY ? 0.0f : expf(xs1 - M1) * r1;
+            s_p[wave][0][slot] = static_cast<PT>(pa);
+            s_p[wave][1][slot] = static_cast<PT>(pb);
+        } else if (lane < kRep * RW) {
+            s_p[wave][hsel][slot] = static_cast<PT>(pa);
+        }
+    }
+    __syncthreads();
     float a0[8], a1[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) { a0[i] = 0.0f; a1[i] = 0.0f; }
+    if constexpr (R16) {
+        // pairs of rows on v_dot2_f32_f16: exact f16 products of p and V, f32 sums
 #pragma unroll
-    for (int k = 0; k < RPT; ++k) {
-        float pa = x0[k] == -INFINITY ? 0.0f : expf(x0[k] - M0) * r0;
-        float pb = x1[k] == -INFINITY ? 0.0f : expf(x1[k] - M1) * r1;
-        if (R16) { pa = round_f16(pa); pb = round_f16(pb); }
+        for (int k = 0; k < RPT; k += 2) {
+            const h2 pa = *reinterpret_cast<const h2 *>(&s_p[wave][0][sub * RPT + k]);
+            const h2 pb = *reinterpret_cast<const h2 *>(&s_p[wave][1][sub * RPT + k]);
+            const h2 v0 = __builtin_shufflevector(vs[k].x, vs[k + 1].x, 0, 8);
+            const h2 v1 = __builtin_shufflevector(vs[k].x, vs[k + 1].x, 1, 9);
+            const h2 v2 = __builtin_shufflevector(vs[k].x, vs[k + 1].x, 2, 10);
+            const h2 v3 = __builtin_shufflevector(vs[k].x, vs[k + 1].x, 3, 11);
+            const h2 v4 = __builtin_shufflevector(vs[k].x, vs[k + 1].x, 4, 12);
+            const h2 v5 = __builtin_shufflevector(vs[k].x, vs[k + 1].x, 5, 13);
+            const h2 v6 = __builtin_shufflevector(vs[k].x, vs[k + 1].x, 6, 14);
+            const h2 v7 = __builtin_shufflevector(vs[k].x, vs[k + 1].x, 7, 15);
+            a0[0] = __builtin_amdgcn_fdot2(v0, pa, a0[0], false); a1[0] = __builtin_amdgcn_fdot2(v0, pb, a1[0], false);
+            a0[1] = __builtin_amdgcn_fdot2(v1, pa, a0[1], false); a1[1] = __builtin_amdgcn_fdot2(v1, pb, a1[1], false);
+            a0[2] = __builtin_amdgcn_fdot2(v2, pa, a0[2], false); a1[2] = __builtin_amdgcn_fdot2(v2, pb, a1[2], false);
+            a0[3] = __builtin_amdgcn_fdot2(v3, pa, a0[3], false); a1[3] = __builtin_amdgcn_fdot2(v3, pb, a1[3], false);
+            a0[4] = __builtin_amdgcn_fdot2(v4, pa, a0[4], false); a1[4] = __builtin_amdgcn_fdot2(v4, pb, a1[4], false);
+            a0[5] = __builtin_amdgcn_fdot2(v5, pa, a0[5], false); a1[5] = __builtin_amdgcn_fdot2(v5, pb, a1[5], false);
+            a0[6] = __builtin_amdgcn_fdot2(v6, pa, a0[6], false); a1[6] = __builtin_amdgcn_fdot2(v6, pb, a1[6], false);
+            a0[7] = __builtin_amdgcn_fdot2(v7, pa, a0[7], false); a1[7] = __builtin_amdgcn_fdot2(v7, pb, a1[7], false);
+        }
+    } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float v = vs[k].get(i);
-            a0[i] = fmaf(pa, v, a0[i]);
-            a1[i] = fmaf(pb, v, a1[i]);
+        for (int k = 0; k < RPT; ++k) {
+            const float pa = s_p[wave][0][sub * RPT + k];
+            const float pb = s_p[wave][1][sub * RPT + k];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float v = vs[k].get(i);
+                a0[i] = fmaf(pa, v, a0[i]);
+                a1[i] = fmaf(pb, v, a1[i]);
+            }
         }
     }
-    // reduce over the 4 row groups of the wave (lane bits 4-5), then over the 4 waves in LDS
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        a0[i] += __shfl_xor(a0[i], 16, kWave); a0[i] += __shfl_xor(a0[i], 32, kWave);
-        a1[i] += __shfl_xor(a1[i], 16, kWave); a1[i] += __shfl_xor(a1[i], 32, kWave);
-    }
-    __shared__ float s_o[4][kRep][kHeadDim];
-    if (sub == 0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            s_o[wave][0][part * 8 + i] = a0[i];
-            s_o[wave][1][part * 8 + i] = a1[i];
-        }
+    // reduce over the 16 row groups of the workgroup (4 per wave x 4 waves) in LDS: every lane stores
+    // its 16 partial sums, then thread (head, dim) adds the 16 groups in a fixed order
+    __shared__ __attribute__((aligned(16))) float s_o[4][4][kRep][kHeadDim];
+    {
+        float4 * o0 = reinterpret_cast<float4 *>(&s_o[wave][sub][0][part * 8]);
+        float4 * o1 = reinterpret_cast<float4 *>(&s_o[wave][sub][1][part * 8]);
+        o0[0] = make_float4(a0[0], a0[1], a0[2], a0[3]);
+        o0[1] = make_float4(a0[4], a0[5], a0[6], a0[7]);
+        o1[0] = make_float4(a1[0], a1[1], a1[2], a1[3]);
+        o1[1] = make_float4(a1[4], a1[5], a1[6], a1[7]);
     }
     __syncthreads();
     const int hh = threadIdx.x >> 7;               // query head of the group this thread finishes
     const int d = threadIdx.x & (kHeadDim - 1);
-    const float o = (s_o[0][hh][d] + s_o[1][hh][d]) + (s_o[2][hh][d] + s_o[3][hh][d]);
+    float o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o += s_o[w][r][hh][d];
+    }
     float * out = p.out + static_cast<int64_t>(s) * p.out_stride + (h0 + hh) * kHeadDim + d;
     if (n_chunks == 1) {
         *out = o;

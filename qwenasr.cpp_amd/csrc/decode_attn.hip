@@ -185,6 +185,74 @@ __device__ inline float row_sum16(float v) {
     return v;
 }
 
+// One reduce-scatter stage over the lane pairs of DPP pattern CTRL (an XOR of the lane index within
+// 16 whose top set bit is BIT): of the N live values the lane keeps the half selected by its own BIT
+// and adds the partner's copy of that half; with N == 1 the stage is a plain butterfly add.
+template <int N, int CTRL, int BIT>
+__device__ inline void rs_stage(float (&v)[16], int part) {
+    if constexpr (N > 1) {
+        const bool up = (part & BIT) != 0;
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) {
+            const float send = up ? v[i] : v[i + N / 2];
+            const float keep = up ? v[i + N / 2] : v[i];
+            v[i] = keep + dpp<CTRL>(send);
+        }
+    } else {
+        v[0] += dpp<CTRL>(v[0]);
+    }
+}
+
+// Sums each of N values (N = 2, 4, 8 or 16) over the 16 lanes of a row group and leaves lane `part`
+// with the full sum of value part / (16 / N).  Partners are lane XOR 15 (row_mirror), XOR 7
+// (row_half_mirror), XOR 2 and XOR 1 (quad_perm): linearly independent masks, so the four stages
+// cover all 16 lanes, and each stage pairs lanes that hold the same index subset.  A full butterfly
+// per value would cost 4 shuffle-adds per value per lane; this costs N - 1 + (4 - log2 N).
+template <int N>
+__device__ inline float reduce_scatter16(const float (&in)[N], int part) {
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = in[i];
+    rs_stage<N, 0x140, 8>(v, part);
+    rs_stage<(N > 1 ? N / 2 : 1), 0x141, 4>(v, part);
+    rs_stage<(N > 2 ? N / 4 : 1), 0x4E, 2>(v, part);
+    rs_stage<(N > 4 ? N / 8 : 1), 0xB1, 1>(v, part);
+    return v[0];
+}
+
+__device__ inline float wave_max(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    v = fmaxf(v, dpp<0x140>(v));
+    v = fmaxf(v, __shfl_xor(v, 16, kWave));
+    return fmaxf(v, __shfl_xor(v, 32, kWave));
+}
+
+// A double moved across lanes by DPP as two 32-bit halves.
+template <int CTRL>
+__device__ inline double dpp_d(double v) {
+    const uint64_t u = __double_as_longlong(v);
+    const uint32_t lo = __builtin_amdgcn_mov_dpp(static_cast<int>(static_cast<uint32_t>(u)), CTRL, 0xf, 0xf, false);
+    const uint32_t hi = __builtin_amdgcn_mov_dpp(static_cast<int>(static_cast<uint32_t>(u >> 32)), CTRL, 0xf, 0xf, false);
+    return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+__device__ inline double wave_sum_dpp_d(double v) {
+    v += dpp_d<0xB1>(v);
+    v += dpp_d<0x4E>(v);
+    v += dpp_d<0x141>(v);
+    v += dpp_d<0x140>(v);
+    v += __shfl_xor(v, 16, kWave);
+    return v + __shfl_xor(v, 32, kWave);
+}
+
+__device__ inline float wave_sum(float v) {
+    v = row_sum16(v);
+    v += __shfl_xor(v, 16, kWave);
+    return v + __shfl_xor(v, 32, kWave);
+}
+
 __device__ inline void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 __device__ inline void publish(float * p, float v) {
@@ -283,11 +351,10 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(DecodeParams p,
         for (int i = 0; i < 8; ++i) { q0[i] = round_f16(q0[i]); q1[i] = round_f16(q1[i]); }
     }
 
-    // scores of both heads; every lane of a 16-lane row group ends with the full row sum
-    float x0[RPT], x1[RPT];
-    float m0 = -INFINITY, m1 = -INFINITY;
+    // partial dot products of this lane's 8 dims: v[2k + h] for row row0 + 4k + sub and head h
     float * sc0 = p.scores + (static_cast<int64_t>(s) * p.n_heads + h0) * p.score_stride;
     float * sc1 = sc0 + p.score_stride;
+    float vdot[2 * RPT];
     // f16 cache: q (already rounded to f16) and K as f16 pairs on v_dot2_f32_f16: exact f16 products,
     // f32 sums -- the f16 dot type of the reference's mul_mat with f32 precision, in 8 instead of 24
     // VALU operations per row and head
@@ -318,38 +385,34 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(DecodeParams p,
                 b = fmaf(q1[i], kv, b);
             }
         }
-        a = row_sum16(a) * p.scale;
-        b = row_sum16(b) * p.scale;
-        const int j = row0 + k * 4 + sub;
-        const bool valid = j < L;
-        if (valid && part == 0) {
-            sc0[j] = a;
-            sc1[j] = b;
-        }
-        x0[k] = valid ? a : -INFINITY;
-        x1[k] = valid ? b : -INFINITY;
-        m0 = fmaxf(m0, x0[k]);
-        m1 = fmaxf(m1, x1[k]);
+        vdot[2 * k] = a;
+        vdot[2 * k + 1] = b;
     }
-    m0 = fmaxf(m0, __shfl_xor(m0, 16, kWave)); m0 = fmaxf(m0, __shfl_xor(m0, 32, kWave));
-    m1 = fmaxf(m1, __shfl_xor(m1, 16, kWave)); m1 = fmaxf(m1, __shfl_xor(m1, 32, kWave));
+    // After the reduce-scatter lane `part` of row group `sub` holds the full score of value index
+    // part / kDup, i.e. row row0 + 4 kk + sub and head hh; each score is then scaled, stored, and fed
+    // to the statistics exactly once (kDup lanes hold a copy when 2 RPT < 16; only the first counts).
+    constexpr int kDup = 16 / (2 * RPT);
+    const float dot = reduce_scatter16<2 * RPT>(vdot, part);
+    const int idx = part / kDup;
+    const int kk = idx >> 1, hh = idx & 1;
+    const int j = row0 + kk * 4 + sub;
+    const bool valid = j < L;
+    const bool primary = part % kDup == 0;
+    const float x = valid ? dot * p.scale : -INFINITY;
+    if (valid && primary) (hh ? sc1 : sc0)[j] = x;
+
     __shared__ float s_max[kRep][4];
     __shared__ double s_sum[kRep][4];
+    float m0 = wave_max(hh == 0 ? x : -INFINITY);
+    float m1 = wave_max(hh == 1 ? x : -INFINITY);
     if (lane == 0) { s_max[0][wave] = m0; s_max[1][wave] = m1; }
     __syncthreads();
     m0 = fmaxf(fmaxf(s_max[0][0], s_max[0][1]), fmaxf(s_max[0][2], s_max[0][3]));
     m1 = fmaxf(fmaxf(s_max[1][0], s_max[1][1]), fmaxf(s_max[1][2], s_max[1][3]));
-
-    double e0 = 0.0, e1 = 0.0;
-    if (part == 0) {
-#pragma unroll
-        for (int k = 0; k < RPT; ++k) {
-            if (x0[k] != -INFINITY) e0 += static_cast<double>(expf(x0[k] - m0));
-            if (x1[k] != -INFINITY) e1 += static_cast<double>(expf(x1[k] - m1));
-        }
-    }
-    e0 += __shfl_xor(e0, 16, kWave); e0 += __shfl_xor(e0, 32, kWave);
-    e1 += __shfl_xor(e1, 16, kWave); e1 += __shfl_xor(e1, 32, kWave);
+    // sum of expf(x - max) per head: f32 within the wave (at most 32 terms), double across waves
+    const float e = valid && primary ? expf(x - (hh ? m1 : m0)) : 0.0f;
+    const float e0 = wave_sum(hh == 0 ? e : 0.0f);
+    const float e1 = wave_sum(hh == 1 ? e : 0.0f);
     if (lane == 0) { s_sum[0][wave] = e0; s_sum[1][wave] = e1; }
     __syncthreads();
     if (threadIdx.x < kRep) {
@@ -422,16 +485,15 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
         M0 = fmaxf(M0, __shfl_xor(M0, off, kWave));
         M1 = fmaxf(M1, __shfl_xor(M1, off, kWave));
     }
+    // rescaled chunk sums, accumulated in double (the rescale factor in f32: its rounding is far below
+    // the f32 resolution of the final 1 / sum)
     double S0 = 0.0, S1 = 0.0;
     for (int i = lane; i < n_stats; i += kWave) {
-        S0 += st0[i].s * exp(static_cast<double>(st0[i].m) - static_cast<double>(M0));
-        S1 += st1[i].s * exp(static_cast<double>(st1[i].m) - static_cast<double>(M1));
+        S0 += st0[i].s * static_cast<double>(expf(st0[i].m - M0));
+        S1 += st1[i].s * static_cast<double>(expf(st1[i].m - M1));
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        S0 += __shfl_xor(S0, off, kWave);
-        S1 += __shfl_xor(S1, off, kWave);
-    }
+    S0 = wave_sum_dpp_d(S0);
+    S1 = wave_sum_dpp_d(S1);
     const float r0 = static_cast<float>(1.0 / S0);
     const float r1 = static_cast<float>(1.0 / S1);
 

@@ -57,8 +57,13 @@ namespace {
 constexpr int kThreads = 256;   // 4 waves
 constexpr int kRep = 2;         // query heads per KV head (Qwen3-ASR: 16 / 8)
 constexpr int kMinChunk = 32;   // the workspace is laid out for the smallest chunk size
+// Merge counters sit 256 bytes apart.  Device-scope atomics on one cache line are serialised (about
+// 10 ns each whichever word of the line they hit), so counters packed 8 to a line made every
+// participant of 8 units queue behind each other; one line per counter leaves only the participants
+// of one unit in the queue.
+constexpr int kCounterStride = 64;
 
-struct SplitStat {
+struct alignas(16) SplitStat {
     float m;
     float pad;
     double s;
@@ -72,7 +77,7 @@ struct DecodeParams {
     float * scores;           // [S_cap][n_heads][score_stride]
     SplitStat * stats;        // [S_cap][n_heads][max_chunks]
     float * partial;          // [S_cap][n_kv][max_chunks][2][128]
-    uint32_t * counters;      // [S_cap][n_kv]
+    uint32_t * counters;      // [S_cap][n_kv][kCounterStride]
     const float * q_norm_w;   // fused mode only
     const float * k_norm_w;
     float eps;
@@ -83,6 +88,12 @@ struct DecodeParams {
     int32_t stat_chunk;       // positions per scores-kernel chunk (granularity of the statistics)
     float scale;
 };
+
+// The double sum of a SplitStat loaded as 16 raw bytes (m, pad, s).
+__device__ inline double stat_sum(const float4 & raw) {
+    const uint64_t lo = __float_as_uint(raw.z), hi = __float_as_uint(raw.w);
+    return __longlong_as_double(static_cast<long long>((hi << 32) | lo));
+}
 
 struct Workspace {
     size_t scores, stats, partial, counters, total;
@@ -100,7 +111,7 @@ Workspace workspace_layout(int32_t n_streams, int32_t n_kv, int32_t max_seq) {
     w.stats = align256(w.scores + sizeof(float) * units * kRep * chunks * kMinChunk);
     w.partial = align256(w.stats + sizeof(SplitStat) * units * kRep * chunks);
     w.counters = align256(w.partial + sizeof(float) * units * chunks * kRep * kHeadDim);
-    w.total = align256(w.counters + sizeof(uint32_t) * units);
+    w.total = align256(w.counters + sizeof(uint32_t) * units * kCounterStride);
     return w;
 }
 
@@ -285,34 +296,55 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(DecodeParams p,
               cache_row_offset(p.layer, 0, s, g, 0, p.n_streams, p.n_kv_heads, p.max_seq);
     const CT * kb = kc + part * 8;
 
+    // Every load of the workgroup is issued before the first use of any of them, the prologue's
+    // inputs first: vector memory loads complete in issue order, so waiting for a prologue input never
+    // waits for the K rows behind it, and the prologue runs while the K rows are in flight.
+    // Fused mode: waves 0/1 load query head h0 + wave, wave 2 the new k row and wave 3 the new v row of
+    // KV head g, each with its norm weight (every workgroup loads them; only the owner of the new
+    // position uses waves 2/3).  Unfused mode: the prepared q slices of both heads.
+    const float * row = p.q + static_cast<int64_t>(s) * p.q_stride;
+    float pa = 0.0f, pb = 0.0f, wa = 0.0f, wb = 0.0f;
+    double inv_freq = 0.0;
+    float4 qv[4];
+    if constexpr (FUSED) {
+        const int q_dim = p.n_heads * kHeadDim;
+        const float * src = wave < 2 ? row + (h0 + wave) * kHeadDim
+                                     : row + q_dim + (wave == 2 ? 0 : p.n_kv_heads * kHeadDim) + g * kHeadDim;
+        const float * w = wave < 2 ? p.q_norm_w : p.k_norm_w;
+        pa = src[lane];
+        pb = src[lane + 64];
+        wa = w[lane];
+        wb = w[lane + 64];
+        inv_freq = rope.inv_freq[lane];   // kernel argument, indexed per lane: also a memory load
+    } else {
+        const float * qp = row + h0 * kHeadDim + part * 8;
+        qv[0] = *reinterpret_cast<const float4 *>(qp);
+        qv[1] = *reinterpret_cast<const float4 *>(qp + 4);
+        qv[2] = *reinterpret_cast<const float4 *>(qp + kHeadDim);
+        qv[3] = *reinterpret_cast<const float4 *>(qp + kHeadDim + 4);
+    }
+    // K rows.  Rows past the end re-read the last row instead of branching around the load (a branch
+    // would split the loads with a wait); their scores are masked below.  In fused mode the new row
+    // is not in the cache yet: its stale contents are loaded and replaced from LDS.
     Slice<CT> ks[RPT];
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
-        const int j = row0 + k * 4 + sub;
-        if (j < L && !(FUSED && j == pos_new)) ks[k].load(kb + static_cast<int64_t>(j) * kHeadDim);
-        else ks[k].zero();
+        const int j = min(row0 + k * 4 + sub, L - 1);
+        ks[k].load(kb + static_cast<int64_t>(j) * kHeadDim);
     }
 
     float q0[8], q1[8];
-    if (FUSED) {
-        // waves 0/1: the two query heads; waves 2/3 of the owner: k (norm + RoPE) and v of the new row
+    if constexpr (FUSED) {
         __shared__ float s_q[kRep][kHeadDim];
         __shared__ float s_k[kHeadDim];
-        const float * row = p.q + static_cast<int64_t>(s) * p.q_stride;
-        const int q_dim = p.n_heads * kHeadDim;
         if (wave < 2) {
-            float a = row[(h0 + wave) * kHeadDim + lane];
-            float b = row[(h0 + wave) * kHeadDim + lane + 64];
-            norm_rope_pair(a, b, p.q_norm_w, p.eps, pos_new, rope, lane);
-            s_q[wave][lane] = a;
-            s_q[wave][lane + 64] = b;
+            norm_rope_pair(pa, pb, wa, wb, p.eps, pos_new, inv_freq);
+            s_q[wave][lane] = pa;
+            s_q[wave][lane + 64] = pb;
         } else if (owner) {
             const bool is_k = wave == 2;
-            const float * src = row + q_dim + (is_k ? 0 : p.n_kv_heads * kHeadDim) + g * kHeadDim;
-            float a = src[lane];
-            float b = src[lane + 64];
-            if (is_k) norm_rope_pair(a, b, p.k_norm_w, p.eps, pos_new, rope, lane);
-            const CT ca = static_cast<CT>(a), cb = static_cast<CT>(b);
+            if (is_k) norm_rope_pair(pa, pb, wa, wb, p.eps, pos_new, inv_freq);
+            const CT ca = static_cast<CT>(pa), cb = static_cast<CT>(pb);
             const int64_t v_delta = cache_row_offset(0, 1, 0, 0, 0, p.n_streams, p.n_kv_heads, p.max_seq);
             CT * dst = kc + (is_k ? 0 : v_delta) + static_cast<int64_t>(pos_new) * kHeadDim;
             dst[lane] = ca;
@@ -338,13 +370,10 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(DecodeParams p,
             }
         }
     } else {
-        const float * qp = p.q + static_cast<int64_t>(s) * p.q_stride + h0 * kHeadDim + part * 8;
-        const float4 a = *reinterpret_cast<const float4 *>(qp);
-        const float4 b = *reinterpret_cast<const float4 *>(qp + 4);
-        const float4 e = *reinterpret_cast<const float4 *>(qp + kHeadDim);
-        const float4 f = *reinterpret_cast<const float4 *>(qp + kHeadDim + 4);
-        q0[0] = a.x; q0[1] = a.y; q0[2] = a.z; q0[3] = a.w; q0[4] = b.x; q0[5] = b.y; q0[6] = b.z; q0[7] = b.w;
-        q1[0] = e.x; q1[1] = e.y; q1[2] = e.z; q1[3] = e.w; q1[4] = f.x; q1[5] = f.y; q1[6] = f.z; q1[7] = f.w;
+        q0[0] = qv[0].x; q0[1] = qv[0].y; q0[2] = qv[0].z; q0[3] = qv[0].w;
+        q0[4] = qv[1].x; q0[5] = qv[1].y; q0[6] = qv[1].z; q0[7] = qv[1].w;
+        q1[0] = qv[2].x; q1[1] = qv[2].y; q1[2] = qv[2].z; q1[3] = qv[2].w;
+        q1[4] = qv[3].x; q1[5] = qv[3].y; q1[6] = qv[3].z; q1[7] = qv[3].w;
     }
     if (R16) {
 #pragma unroll
@@ -443,52 +472,74 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
     const int h0 = g * kRep;
     const int row0 = c * CHUNK + wave * (CHUNK / 4);
 
-    // V rows of the chunk in flight first; each lane also loads the one score it turns into p below
-    // (the wave's CHUNK / 4 rows are row0 .. row0 + RW - 1; lane -> row lane % RW, and for RW <= 32
-    // head (lane / RW) & 1, so every (row, head) probability is computed once, not by all 16 lanes
-    // that hold a slice of that row)
+    // Loads are issued in the order statistics, scores, V rows, all before the first use of any of
+    // them: vector memory loads complete in issue order, so the softmax normalisation below waits for
+    // the statistics and scores only and runs while the V rows are in flight.  Out-of-range indices
+    // re-read the last valid entry instead of branching around the load (a branch would split the
+    // loads with a wait) and are masked where the value is used.
+    // The first kStatRegs * 64 statistics of each head are held in registers (one 16-byte load each);
+    // longer prefixes loop over the rest.
+    const SplitStat * st0 = p.stats + (static_cast<int64_t>(s) * p.n_heads + h0) * p.max_chunks;
+    const SplitStat * st1 = st0 + p.max_chunks;
+    constexpr int kStatRegs = 4;
+    float4 sa[kStatRegs], sb[kStatRegs];
+#pragma unroll
+    for (int u = 0; u < kStatRegs; ++u) {
+        const int i = min(lane + u * kWave, n_stats - 1);
+        sa[u] = *reinterpret_cast<const float4 *>(st0 + i);
+        sb[u] = *reinterpret_cast<const float4 *>(st1 + i);
+    }
+    // Each lane loads the one score it turns into p below (the wave's CHUNK / 4 rows are row0 ..
+    // row0 + RW - 1; lane -> row lane % RW, and for RW <= 32 head (lane / RW) & 1, so every (row, head)
+    // probability is computed once, not by all 16 lanes that hold a slice of that row).
     constexpr int RW = CHUNK / 4;
-    const CT * vb = static_cast<const CT *>(p.cache) +
-                    cache_row_offset(p.layer, 1, s, g, 0, p.n_streams, p.n_kv_heads, p.max_seq) + part * 8;
     const float * sc0 = p.scores + (static_cast<int64_t>(s) * p.n_heads + h0) * p.score_stride;
     const float * sc1 = sc0 + p.score_stride;
+    const int own = lane % RW;
+    const int jr = row0 + own;
+    const int jrc = min(jr, L - 1);
+    const int hsel = RW >= kWave ? 0 : (lane / RW) & 1;
+    float xs0, xs1 = 0.0f;
+    if constexpr (RW >= kWave) {
+        xs0 = sc0[jrc];
+        xs1 = sc1[jrc];
+    } else {
+        xs0 = (hsel ? sc1 : sc0)[jrc];
+    }
+    const CT * vb = static_cast<const CT *>(p.cache) +
+                    cache_row_offset(p.layer, 1, s, g, 0, p.n_streams, p.n_kv_heads, p.max_seq) + part * 8;
     Slice<CT> vs[RPT];
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
-        const int j = row0 + k * 4 + sub;
-        if (j < L) vs[k].load(vb + static_cast<int64_t>(j) * kHeadDim);
-        else vs[k].zero();
-    }
-    const int own = lane % RW;
-    const int jr = row0 + own;
-    const int hsel = RW >= kWave ? 0 : (lane / RW) & 1;
-    float xs0 = -INFINITY, xs1 = -INFINITY;
-    if (jr < L) {
-        if constexpr (RW >= kWave) {
-            xs0 = sc0[jr];
-            xs1 = sc1[jr];
-        } else {
-            xs0 = (hsel ? sc1 : sc0)[jr];
-        }
+        const int j = min(row0 + k * 4 + sub, L - 1);   // rows past the end get p = 0
+        vs[k].load(vb + static_cast<int64_t>(j) * kHeadDim);
     }
 
-    // global max and sum of both heads from the chunk statistics (every wave, redundantly)
-    const SplitStat * st0 = p.stats + (static_cast<int64_t>(s) * p.n_heads + h0) * p.max_chunks;
-    const SplitStat * st1 = st0 + p.max_chunks;
+    // global max and sum of both heads from the chunk statistics (every wave, redundantly); a repeated
+    // entry leaves the max unchanged and is excluded from the sum
     float M0 = -INFINITY, M1 = -INFINITY;
-    for (int i = lane; i < n_stats; i += kWave) {
+#pragma unroll
+    for (int u = 0; u < kStatRegs; ++u) {
+        M0 = fmaxf(M0, sa[u].x);
+        M1 = fmaxf(M1, sb[u].x);
+    }
+    for (int i = lane + kStatRegs * kWave; i < n_stats; i += kWave) {
         M0 = fmaxf(M0, st0[i].m);
         M1 = fmaxf(M1, st1[i].m);
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        M0 = fmaxf(M0, __shfl_xor(M0, off, kWave));
-        M1 = fmaxf(M1, __shfl_xor(M1, off, kWave));
-    }
+    M0 = wave_max(M0);
+    M1 = wave_max(M1);
     // rescaled chunk sums, accumulated in double (the rescale factor in f32: its rounding is far below
     // the f32 resolution of the final 1 / sum)
     double S0 = 0.0, S1 = 0.0;
-    for (int i = lane; i < n_stats; i += kWave) {
+#pragma unroll
+    for (int u = 0; u < kStatRegs; ++u) {
+        if (lane + u * kWave < n_stats) {
+            S0 += stat_sum(sa[u]) * static_cast<double>(expf(sa[u].x - M0));
+            S1 += stat_sum(sb[u]) * static_cast<double>(expf(sb[u].x - M1));
+        }
+    }
+    for (int i = lane + kStatRegs * kWave; i < n_stats; i += kWave) {
         S0 += st0[i].s * static_cast<double>(expf(st0[i].m - M0));
         S1 += st1[i].s * static_cast<double>(expf(st1[i].m - M1));
     }
@@ -496,6 +547,7 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
     S1 = wave_sum_dpp_d(S1);
     const float r0 = static_cast<float>(1.0 / S0);
     const float r1 = static_cast<float>(1.0 / S1);
+    const bool row_valid = jr < L;
 
     // normalised probabilities of this lane's (row, head), rounded to f16 for an f16 V, shared in LDS.
     // Row k * 4 + sub of the wave is stored at sub * RPT + k, so the lanes of group `sub` read the pair
@@ -504,10 +556,10 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
     __shared__ __attribute__((aligned(16))) PT s_p[4][kRep][kWave];
     {
         const float Ma = hsel ? M1 : M0, ra = hsel ? r1 : r0;
-        float pa = xs0 == -INFINITY ? 0.0f : expf(xs0 - Ma) * ra;
+        const float pa = row_valid ? expf(xs0 - Ma) * ra : 0.0f;
         const int slot = (own & 3) * RPT + (own >> 2);
         if constexpr (RW >= kWave) {
-            const float pb = xs1 == -INFINITY ? 0.0f : expf(xs1 - M1) * r1;
+            const float pb = row_valid ? expf(xs1 - M1) * r1 : 0.0f;
             s_p[wave][0][slot] = static_cast<PT>(pa);
             s_p[wave][1][slot] = static_cast<PT>(pb);
         } else if (lane < kRep * RW) {
@@ -588,7 +640,7 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
     __syncthreads();
     __shared__ int s_last;
     if (threadIdx.x == 0) {
-        uint32_t * ctr = p.counters + unit;
+        uint32_t * ctr = p.counters + unit * kCounterStride;
         const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = prev == static_cast<uint32_t>(n_chunks - 1);
         if (s_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -597,32 +649,29 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
     if (!s_last) return;
 
     // Sum of the partials: thread t owns the float pair j = t % 128 of the 256-float state and the
-    // chunks c = t / 128, t / 128 + 2, ...; up to 32 8-byte loads per thread in flight at once.  The
-    // two chunk groups are then added in LDS.  Fixed order, so the result is deterministic.
+    // chunks c = t / 128, t / 128 + 2, ...; 32 8-byte loads per thread in flight at once (chunks past
+    // the end load nothing and add +0).  The two chunk groups are then added in LDS.  Fixed order, so
+    // the result is deterministic.
     const int pair = threadIdx.x & 127;
     const int grp = threadIdx.x >> 7;
     const uint64_t * pp = reinterpret_cast<const uint64_t *>(part_base) + pair;
     constexpr int kStride = kRep * kHeadDim / 2;    // uint64 per chunk state
+    constexpr int kBatch = 32;
     float acc_lo = 0.0f, acc_hi = 0.0f;
-    int i = grp;
-    for (; i + 2 * 31 < n_chunks; i += 2 * 32) {
-        uint64_t v[32];
+    for (int i0 = grp; i0 < n_chunks; i0 += 2 * kBatch) {
+        uint64_t v[kBatch];
 #pragma unroll
-        for (int u = 0; u < 32; ++u) {
-            v[u] = __hip_atomic_load(pp + static_cast<int64_t>(i + 2 * u) * kStride, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
+        for (int u = 0; u < kBatch; ++u) {
+            const int i = i0 + 2 * u;
+            v[u] = i < n_chunks ? __hip_atomic_load(pp + static_cast<int64_t>(i) * kStride, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT)
+                                : 0;
         }
 #pragma unroll
-        for (int u = 0; u < 32; ++u) {
+        for (int u = 0; u < kBatch; ++u) {
             acc_lo += __uint_as_float(static_cast<uint32_t>(v[u]));
             acc_hi += __uint_as_float(static_cast<uint32_t>(v[u] >> 32));
         }
-    }
-    for (; i < n_chunks; i += 2) {
-        const uint64_t v = __hip_atomic_load(pp + static_cast<int64_t>(i) * kStride, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-        acc_lo += __uint_as_float(static_cast<uint32_t>(v));
-        acc_hi += __uint_as_float(static_cast<uint32_t>(v >> 32));
     }
     __shared__ float s_acc[2][kRep * kHeadDim];
     s_acc[grp][2 * pair] = acc_lo;

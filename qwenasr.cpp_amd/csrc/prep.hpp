@@ -19,21 +19,28 @@ __device__ inline double wave_sum_d(double v) {
     return v;
 }
 
-// a = x[lane], b = x[lane + 64] in, rotated pair out.
-__device__ inline void norm_rope_pair(float & a, float & b, const float * w, float eps, int pos,
-                                      const RopeTable & rope, int lane) {
+// a = x[lane], b = x[lane + 64] in, rotated pair out; wa = w[lane], wb = w[lane + 64] of the norm
+// weight and inv_freq = rope.inv_freq[lane] (passed as values, so a caller can issue every load of its
+// prologue before the first use).
+__device__ inline void norm_rope_pair(float & a, float & b, float wa, float wb, float eps, int pos,
+                                      double inv_freq) {
 #pragma clang fp contract(off)
     const double ss = wave_sum_d(static_cast<double>(a) * a + static_cast<double>(b) * b);
     const double ms = ss / static_cast<double>(kHeadDim);
     const float scale = 1.0f / sqrtf(static_cast<float>(ms) + eps);
-    const float na = a * scale * w[lane];
-    const float nb = b * scale * w[lane + 64];
+    const float na = a * scale * wa;
+    const float nb = b * scale * wb;
     double sn, cs;
-    sincos(static_cast<double>(pos) * rope.inv_freq[lane], &sn, &cs);
+    sincos(static_cast<double>(pos) * inv_freq, &sn, &cs);
     const float c = static_cast<float>(cs);
     const float s = static_cast<float>(sn);
     a = na * c - nb * s;
     b = nb * c + na * s;
+}
+
+__device__ inline void norm_rope_pair(float & a, float & b, const float * w, float eps, int pos,
+                                      const RopeTable & rope, int lane) {
+    norm_rope_pair(a, b, w[lane], w[lane + 64], eps, pos, rope.inv_freq[lane]);
 }
 
 }  // namespace qa

@@ -454,7 +454,7 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(DecodeParams p,
     }
 }
 
-template <typename CT, bool R16, int CHUNK>
+template <typename CT, bool R16, int CHUNK, int SR, int MB>
 __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p) {
     constexpr int RPT = CHUNK / 16;
     const int g = static_cast<int>(blockIdx.x) % p.n_kv_heads;
@@ -477,11 +477,12 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
     // the statistics and scores only and runs while the V rows are in flight.  Out-of-range indices
     // re-read the last valid entry instead of branching around the load (a branch would split the
     // loads with a wait) and are masked where the value is used.
-    // The first kStatRegs * 64 statistics of each head are held in registers (one 16-byte load each);
-    // longer prefixes loop over the rest.
+    // The first SR * 64 statistics of each head are held in registers (one 16-byte load each; SR is
+    // chosen from the cache capacity so that this covers every call); longer prefixes loop over the
+    // rest.
     const SplitStat * st0 = p.stats + (static_cast<int64_t>(s) * p.n_heads + h0) * p.max_chunks;
     const SplitStat * st1 = st0 + p.max_chunks;
-    constexpr int kStatRegs = 4;
+    constexpr int kStatRegs = SR;
     float4 sa[kStatRegs], sb[kStatRegs];
 #pragma unroll
     for (int u = 0; u < kStatRegs; ++u) {
@@ -656,7 +657,7 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
     const int grp = threadIdx.x >> 7;
     const uint64_t * pp = reinterpret_cast<const uint64_t *>(part_base) + pair;
     constexpr int kStride = kRep * kHeadDim / 2;    // uint64 per chunk state
-    constexpr int kBatch = 32;
+    constexpr int kBatch = MB;   // chosen from the capacity: one round of loads for every call
     float acc_lo = 0.0f, acc_hi = 0.0f;
     for (int i0 = grp; i0 < n_chunks; i0 += 2 * kBatch) {
         uint64_t v[kBatch];
@@ -719,13 +720,30 @@ void launch_scores(int chunk, dim3 grid, const DecodeParams & p, const RopeTable
     }
 }
 
+template <typename CT, bool R16, int CHUNK, int MB>
+void launch_values_sr(int sr, dim3 grid, const DecodeParams & p, hipStream_t stream) {
+    switch (sr) {
+        case 1: hipLaunchKernelGGL((decode_values_kernel<CT, R16, CHUNK, 1, MB>), grid, dim3(kThreads), 0, stream, p); break;
+        case 2: hipLaunchKernelGGL((decode_values_kernel<CT, R16, CHUNK, 2, MB>), grid, dim3(kThreads), 0, stream, p); break;
+        case 4: hipLaunchKernelGGL((decode_values_kernel<CT, R16, CHUNK, 4, MB>), grid, dim3(kThreads), 0, stream, p); break;
+        default: hipLaunchKernelGGL((decode_values_kernel<CT, R16, CHUNK, 8, MB>), grid, dim3(kThreads), 0, stream, p); break;
+    }
+}
+
+template <typename CT, bool R16, int CHUNK>
+void launch_values_mb(int sr, int mb, dim3 grid, const DecodeParams & p, hipStream_t stream) {
+    if (mb <= 8) launch_values_sr<CT, R16, CHUNK, 8>(sr, grid, p, stream);
+    else if (mb <= 16) launch_values_sr<CT, R16, CHUNK, 16>(sr, grid, p, stream);
+    else launch_values_sr<CT, R16, CHUNK, 40>(sr, grid, p, stream);
+}
+
 template <typename CT, bool R16>
-void launch_values(int chunk, dim3 grid, const DecodeParams & p, hipStream_t stream) {
+void launch_values(int chunk, int sr, int mb, dim3 grid, const DecodeParams & p, hipStream_t stream) {
     switch (chunk) {
-        case 32: hipLaunchKernelGGL((decode_values_kernel<CT, R16, 32>), grid, dim3(kThreads), 0, stream, p); break;
-        case 64: hipLaunchKernelGGL((decode_values_kernel<CT, R16, 64>), grid, dim3(kThreads), 0, stream, p); break;
-        case 128: hipLaunchKernelGGL((decode_values_kernel<CT, R16, 128>), grid, dim3(kThreads), 0, stream, p); break;
-        default: hipLaunchKernelGGL((decode_values_kernel<CT, R16, 256>), grid, dim3(kThreads), 0, stream, p); break;
+        case 32: launch_values_mb<CT, R16, 32>(sr, mb, grid, p, stream); break;
+        case 64: launch_values_mb<CT, R16, 64>(sr, mb, grid, p, stream); break;
+        case 128: launch_values_mb<CT, R16, 128>(sr, mb, grid, p, stream); break;
+        default: launch_values_mb<CT, R16, 256>(sr, mb, grid, p, stream); break;
     }
 }
 
@@ -737,7 +755,15 @@ void launch_both(const Chunks & ch, bool fused, int32_t n_kv, int32_t n_streams,
     const dim3 gv(static_cast<unsigned>((p.max_len + ch.values - 1) / ch.values * n_kv), static_cast<unsigned>(n_streams));
     if (fused) launch_scores<CT, R16, true>(ch.scores, gs, p, rope, stream);
     else launch_scores<CT, R16, false>(ch.scores, gs, p, rope, stream);
-    launch_values<CT, R16>(ch.values, gv, p, stream);
+    // statistics per head at the capacity, in registers: 64 per register slot, 1/2/4/8 slots
+    const int n_stats_cap = (p.max_seq + ch.scores - 1) / ch.scores;
+    const int sr = n_stats_cap <= 64 ? 1 : n_stats_cap <= 128 ? 2 : n_stats_cap <= 256 ? 4 : 8;
+    // merge loads per thread and round: the participants (values chunks at the capacity) split over
+    // two thread groups, so MB loads cover 2 MB participants in one round; fewer registers held means
+    // more workgroups in flight
+    const int n_vchunks_cap = (p.max_seq + ch.values - 1) / ch.values;
+    const int mb = n_vchunks_cap <= 16 ? 8 : n_vchunks_cap <= 32 ? 16 : 40;
+    launch_values<CT, R16>(ch.values, sr, mb, gv, p, stream);
 }
 
 int launch_decode(DecodeParams p, bool fused, const RopeTable & rope, const qa_kv_layout & layout,

@@ -228,7 +228,7 @@ def test_decode_step_fused_equals_append_then_attend(qa, orc, f16, n_past):
 
 # ------------------------------------------------------------------------------------------ prefill
 @pytest.mark.parametrize("f16", [True, False])
-@pytest.mark.parametrize("n_past,T", [(0, 1), (0, 2), (0, 37), (0, 156), (100, 50), (0, 600)])
+@pytest.mark.parametrize("n_past,T", [(0, 1), (0, 2), (0, 37), (0, 156), (100, 50), (0, 600), (70, 700), (0, 1024)])
 def test_prefill_attention(qa, orc, f16, n_past, T):
     L = n_past + T
     lay = layout(qa, 2, 2, L + 5, f16)

@@ -202,6 +202,64 @@ def multistream_roofline(qa, cfg, reps: int):
                         f"(mean {float(lens.mean()) + 1:.0f}), one layer's decode-step attention per launch pair"}
 
 
+def kernel_only(which: str, reps: int):
+    """One hot-path kernel on synthetic inputs at the config-3 shape, for rocprofv3 passes (the counters
+    of every dispatch are then the kernel's alone).  prefill: causal prefill attention over 3913
+    positions of one layer (f16 cache, n_past 0); decode-attn: the decode-step attention of one layer
+    at L = 4186, rotating 28 layer caches."""
+    import ctypes as C
+
+    import numpy as np
+    import qwenasr_amd as qa
+
+    cfg = qa.QWEN3_ASR_1_7B.config()
+    scale = 1.0 / (cfg.head_dim ** 0.5)
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    qa.check(qa.lib.qa_event_create(C.byref(e0)))
+    qa.check(qa.lib.qa_event_create(C.byref(e1)))
+    if which == "prefill":
+        T = 3913
+        lay = qa.KvLayout(2, 1, cfg.n_kv_heads, cfg.head_dim, T + 8, qa.QA_CACHE_F16)
+        cache = qa.DeviceArray(qa.lib.qa_kv_cache_bytes(C.byref(lay)), np.uint8)
+        q = qa.DeviceArray.from_numpy(np.random.default_rng(3).standard_normal((T, cfg.n_heads * cfg.head_dim)).astype(np.float32))
+        out = qa.DeviceArray((T, cfg.n_heads * cfg.head_dim))
+        wsb = qa.lib.qa_prefill_attn_workspace_bytes(T, cfg.n_heads)
+        ws = qa.DeviceArray(max(wsb, 256), np.uint8)
+
+        def launch(i):
+            qa.check(qa.lib.qa_prefill_attn(q.ptr, cache.ptr, C.byref(lay), i % 2, 0, 0, T, cfg.n_heads, scale, out.ptr,
+                                            ws.ptr, wsb, None))
+        flops = 4.0 * cfg.n_heads * cfg.head_dim * T * (T + 1) / 2
+        unit = dict(useful_gflop_per_launch=round(flops / 1e9, 3))
+    else:
+        L = 4186
+        lay = qa.KvLayout(cfg.n_layers, 1, cfg.n_kv_heads, cfg.head_dim, L + 8, qa.QA_CACHE_F16)
+        cache = qa.DeviceArray(qa.lib.qa_kv_cache_bytes(C.byref(lay)), np.uint8)
+        q_dim, kv_dim = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+        qkv = qa.DeviceArray.from_numpy(np.random.default_rng(5).standard_normal((1, q_dim + 2 * kv_dim)).astype(np.float32))
+        ones = qa.DeviceArray.from_numpy(np.ones(cfg.head_dim, np.float32))
+        n_past = qa.DeviceArray.from_numpy(np.array([L - 1], np.int32))
+        out = qa.DeviceArray((1, q_dim))
+        wsb = qa.lib.qa_decode_attn_workspace_bytes(1, cfg.n_heads, lay.max_seq)
+        ws = qa.DeviceArray(wsb, np.uint8)
+
+        def launch(i):
+            qa.check(qa.lib.qa_decode_step_attn(qkv.ptr, ones.ptr, ones.ptr, cache.ptr, C.byref(lay), i % cfg.n_layers,
+                                                n_past.ptr, 1, L, cfg.n_heads, cfg.rope_theta, cfg.rms_norm_eps, scale,
+                                                out.ptr, ws.ptr, wsb, None))
+        unit = dict(algorithmic_bytes_per_launch=4096 * L + 16384)
+    launch(0)
+    qa.synchronize()
+    qa.check(qa.lib.qa_event_record(e0, None))
+    for i in range(reps):
+        launch(i)
+    qa.check(qa.lib.qa_event_record(e1, None))
+    ms = C.c_float()
+    qa.check(qa.lib.qa_event_elapsed_ms(e0, e1, C.byref(ms)))
+    us = ms.value * 1e3 / reps
+    print(json.dumps(dict(kernel=which, launches=reps + 1, avg_us=round(us, 3), **unit)), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -214,7 +272,13 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 10 times (reference for HBM traffic counters)")
+    ap.add_argument("--kernel", choices=["prefill", "decode-attn"],
+                    help="only run one hot-path kernel on synthetic inputs (short program for rocprofv3 passes)")
+    ap.add_argument("--kernel-reps", type=int, default=20)
     args = ap.parse_args()
+    if args.kernel:
+        kernel_only(args.kernel, args.kernel_reps)
+        return
     if args.copy_calibration:
         copy_calibration()
         return

@@ -204,9 +204,10 @@ def multistream_roofline(qa, cfg, reps: int):
 
 def kernel_only(which: str, reps: int):
     """One hot-path kernel on synthetic inputs at the config-3 shape, for rocprofv3 passes (the counters
-    of every dispatch are then the kernel's alone).  prefill: causal prefill attention over 3913
-    positions of one layer (f16 cache, n_past 0); decode-attn: the decode-step attention of one layer
-    at L = 4186, rotating 28 layer caches."""
+    of every dispatch are then the kernel's alone).  append: the prefill K/V append of 3913 positions
+    (q/k norm + RoPE, f16 cache write); prefill: causal prefill attention over 3913 positions of one
+    layer (f16 cache, n_past 0); decode-attn: the decode-step attention of one layer at L = 4186,
+    rotating 28 layer caches."""
     import ctypes as C
 
     import numpy as np
@@ -217,7 +218,22 @@ def kernel_only(which: str, reps: int):
     e0, e1 = C.c_void_p(), C.c_void_p()
     qa.check(qa.lib.qa_event_create(C.byref(e0)))
     qa.check(qa.lib.qa_event_create(C.byref(e1)))
-    if which == "prefill":
+    if which == "append":
+        T = 3913
+        lay = qa.KvLayout(2, 1, cfg.n_kv_heads, cfg.head_dim, T + 8, qa.QA_CACHE_F16)
+        cache = qa.DeviceArray(qa.lib.qa_kv_cache_bytes(C.byref(lay)), np.uint8)
+        q_dim, kv_dim = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+        qkv = qa.DeviceArray.from_numpy(np.random.default_rng(4).standard_normal((T, q_dim + 2 * kv_dim)).astype(np.float32))
+        ones = qa.DeviceArray.from_numpy(np.ones(cfg.head_dim, np.float32))
+        q_out = qa.DeviceArray((T, q_dim))
+        n_past = qa.DeviceArray.from_numpy(np.zeros(1, np.int32))
+
+        def launch(i):
+            qa.check(qa.lib.qa_kv_append(qkv.ptr, ones.ptr, ones.ptr, q_out.ptr, cache.ptr, C.byref(lay), i % 2,
+                                         n_past.ptr, 1, T, cfg.n_heads, cfg.rope_theta, cfg.rms_norm_eps, None))
+        # read q|k|v rows (f32), write q (f32) and the K and V rows (f16)
+        unit = dict(algorithmic_bytes_per_launch=T * ((q_dim + 2 * kv_dim) * 4 + q_dim * 4 + 2 * kv_dim * 2))
+    elif which == "prefill":
         T = 3913
         lay = qa.KvLayout(2, 1, cfg.n_kv_heads, cfg.head_dim, T + 8, qa.QA_CACHE_F16)
         cache = qa.DeviceArray(qa.lib.qa_kv_cache_bytes(C.byref(lay)), np.uint8)
@@ -272,7 +288,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 10 times (reference for HBM traffic counters)")
-    ap.add_argument("--kernel", choices=["prefill", "decode-attn"],
+    ap.add_argument("--kernel", choices=["append", "prefill", "decode-attn"],
                     help="only run one hot-path kernel on synthetic inputs (short program for rocprofv3 passes)")
     ap.add_argument("--kernel-reps", type=int, default=20)
     args = ap.parse_args()

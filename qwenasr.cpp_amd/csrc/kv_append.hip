@@ -39,77 +39,91 @@ struct PrepParams {
     float eps;
 };
 
+// One workgroup per token row; wave w prepares the head slots w, w + 4, w + 8, ... of the row (q heads,
+// then k heads, then v heads).  The RoPE angles depend only on the position, so each wave evaluates
+// its lane's cos/sin once for all of its q and k heads.  Every load of a group of 8 slots is issued
+// before the first arithmetic; slots past the end re-read the last slot and are not stored.
 template <int MODE>
 __global__ __launch_bounds__(256) void qkv_prep_kernel(PrepParams p, RopeTable rope) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = static_cast<int>((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int wave = threadIdx.x >> 6;
+    const int row = blockIdx.x;
     const int slots = MODE == kPrepInPlace ? p.n_heads + p.n_kv_heads : p.n_heads + 2 * p.n_kv_heads;
-    const int row = wave / slots;
-    const int slot = wave - row * slots;
     if (row >= p.n_rows) return;
 
     const int stream = row / p.n_tokens;
     const int t = row - stream * p.n_tokens;
     const int pos = MODE == kPrepInPlace ? p.pos0 + t : p.n_past[stream] + t;
-    if (MODE != kPrepInPlace && (pos < 0 || pos >= p.max_seq)) return;
+    if (MODE != kPrepInPlace && (pos < 0 || pos >= p.max_seq)) return;   // uniform for the workgroup
 
     const int q_dim = p.n_heads * kHeadDim;
     const int row_width = (p.n_heads + 2 * p.n_kv_heads) * kHeadDim;
-    float * src = p.qkv + static_cast<int64_t>(row) * row_width + slot * kHeadDim;
-    float a = src[lane];
-    float b = src[lane + 64];
-
-    if (slot < p.n_heads + p.n_kv_heads) {
-        const bool is_q = slot < p.n_heads;
-        norm_rope_pair(a, b, is_q ? p.q_norm_w : p.k_norm_w, p.eps, pos, rope, lane);
-        const float ra = a, rb = b;
-
-        if (MODE == kPrepInPlace) {
-            src[lane] = ra;
-            src[lane + 64] = rb;
-            return;
-        }
-        if (is_q) {
-            float * dst = p.q_out + static_cast<int64_t>(row) * q_dim + slot * kHeadDim;
-            dst[lane] = ra;
-            dst[lane + 64] = rb;
-            return;
-        }
-        const int head = slot - p.n_heads;
-        const int64_t off = cache_row_offset(p.layer, 0, stream, head, pos, p.n_streams, p.n_kv_heads, p.max_seq);
-        if (MODE == kPrepCacheF16) {
-            _Float16 * dst = static_cast<_Float16 *>(p.cache) + off;
-            dst[lane] = static_cast<_Float16>(ra);
-            dst[lane + 64] = static_cast<_Float16>(rb);
-        } else {
-            float * dst = static_cast<float *>(p.cache) + off;
-            dst[lane] = ra;
-            dst[lane + 64] = rb;
-        }
-        return;
+    float * src_row = p.qkv + static_cast<int64_t>(row) * row_width;
+    const double inv_freq = rope.inv_freq[lane];
+    const float wqa = p.q_norm_w[lane], wqb = p.q_norm_w[lane + 64];
+    const float wka = p.k_norm_w[lane], wkb = p.k_norm_w[lane + 64];
+    constexpr int kPer = 8;
+    float a[kPer], b[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int slot = min(wave + 4 * u, slots - 1);
+        a[u] = src_row[slot * kHeadDim + lane];
+        b[u] = src_row[slot * kHeadDim + lane + 64];
     }
-
-    // V head: stored raw (no norm, no RoPE), cast to the cache dtype (text-decoder.cpp:411, 433).
-    const int head = slot - p.n_heads - p.n_kv_heads;
-    const int64_t off = cache_row_offset(p.layer, 1, stream, head, pos, p.n_streams, p.n_kv_heads, p.max_seq);
-    if (MODE == kPrepCacheF16) {
-        _Float16 * dst = static_cast<_Float16 *>(p.cache) + off;
-        dst[lane] = static_cast<_Float16>(a);
-        dst[lane + 64] = static_cast<_Float16>(b);
-    } else {
-        float * dst = static_cast<float *>(p.cache) + off;
-        dst[lane] = a;
-        dst[lane + 64] = b;
+    float c, s;
+    rope_cos_sin(pos, inv_freq, c, s);
+    for (int s0 = wave;; s0 += 4 * kPer) {
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int slot = s0 + 4 * u;
+            if (slot >= slots) break;                   // uniform for the wave
+            float ra = a[u], rb = b[u];
+            if (slot < p.n_heads + p.n_kv_heads) {
+                const bool is_q = slot < p.n_heads;
+                norm_rope_pair_cs(ra, rb, is_q ? wqa : wka, is_q ? wqb : wkb, p.eps, c, s);
+                if (MODE == kPrepInPlace) {
+                    src_row[slot * kHeadDim + lane] = ra;
+                    src_row[slot * kHeadDim + lane + 64] = rb;
+                    continue;
+                }
+                if (is_q) {
+                    float * dst = p.q_out + static_cast<int64_t>(row) * q_dim + slot * kHeadDim;
+                    dst[lane] = ra;
+                    dst[lane + 64] = rb;
+                    continue;
+                }
+            }
+            // k (normed and rotated above) or v (stored raw, text-decoder.cpp:411, 433), cast to the
+            // cache dtype
+            const bool is_v = slot >= p.n_heads + p.n_kv_heads;
+            const int head = slot - p.n_heads - (is_v ? p.n_kv_heads : 0);
+            const int64_t off = cache_row_offset(p.layer, is_v ? 1 : 0, stream, head, pos, p.n_streams, p.n_kv_heads,
+                                                 p.max_seq);
+            if (MODE == kPrepCacheF16) {
+                _Float16 * dst = static_cast<_Float16 *>(p.cache) + off;
+                dst[lane] = static_cast<_Float16>(ra);
+                dst[lane + 64] = static_cast<_Float16>(rb);
+            } else {
+                float * dst = static_cast<float *>(p.cache) + off;
+                dst[lane] = ra;
+                dst[lane + 64] = rb;
+            }
+        }
+        if (s0 + 4 * kPer >= slots) break;
+        // next group of slots (more than 32 head slots per row)
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int slot = min(s0 + 4 * kPer + 4 * u, slots - 1);
+            a[u] = src_row[slot * kHeadDim + lane];
+            b[u] = src_row[slot * kHeadDim + lane + 64];
+        }
     }
 }
 
 int launch_prep(int mode, const PrepParams & p, float rope_theta, hipStream_t stream) {
-    const int slots = mode == kPrepInPlace ? p.n_heads + p.n_kv_heads : p.n_heads + 2 * p.n_kv_heads;
-    const int64_t waves = static_cast<int64_t>(p.n_rows) * slots;
-    const int64_t blocks = (waves + 3) / 4;
+    const int64_t blocks = p.n_rows;
     if (blocks <= 0) return QA_OK;
-    if (blocks > 0x7fffffff) return fail(QA_ERR_INVALID, "qkv prep: too many rows");
     const RopeTable rope = make_rope_table(rope_theta);
     const dim3 grid(static_cast<unsigned>(blocks));
     switch (mode) {

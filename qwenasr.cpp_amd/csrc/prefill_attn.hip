@@ -39,14 +39,6 @@ template <typename CT>
 __device__ inline void load8(const CT * p, float (&v)[8]);
 
 template <>
-__device__ inline void load8<_Float16>(const _Float16 * p, float (&v)[8]) {
-    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-    const h8 x = *reinterpret_cast<const h8 *>(p);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = static_cast<float>(x[i]);
-}
-
-template <>
 __device__ inline void load8<float>(const float * p, float (&v)[8]) {
     const float4 a = *reinterpret_cast<const float4 *>(p);
     const float4 b = *reinterpret_cast<const float4 *>(p + 4);

@@ -19,23 +19,34 @@ __device__ inline double wave_sum_d(double v) {
     return v;
 }
 
+// cos and sin of the RoPE angle pos * inv_freq, evaluated in double and rounded to f32 (the
+// reference's apply_rope_position, text-decoder.cpp:604-625).
+__device__ inline void rope_cos_sin(int pos, double inv_freq, float & c, float & s) {
+    double sn, cs;
+    sincos(static_cast<double>(pos) * inv_freq, &sn, &cs);
+    c = static_cast<float>(cs);
+    s = static_cast<float>(sn);
+}
+
 // a = x[lane], b = x[lane + 64] in, rotated pair out; wa = w[lane], wb = w[lane + 64] of the norm
-// weight and inv_freq = rope.inv_freq[lane] (passed as values, so a caller can issue every load of its
-// prologue before the first use).
-__device__ inline void norm_rope_pair(float & a, float & b, float wa, float wb, float eps, int pos,
-                                      double inv_freq) {
+// weight, (c, s) = rope_cos_sin of this lane's frequency (passed as values, so a caller can issue
+// every load of its prologue before the first use and share one angle evaluation between heads).
+__device__ inline void norm_rope_pair_cs(float & a, float & b, float wa, float wb, float eps, float c, float s) {
 #pragma clang fp contract(off)
     const double ss = wave_sum_d(static_cast<double>(a) * a + static_cast<double>(b) * b);
     const double ms = ss / static_cast<double>(kHeadDim);
     const float scale = 1.0f / sqrtf(static_cast<float>(ms) + eps);
     const float na = a * scale * wa;
     const float nb = b * scale * wb;
-    double sn, cs;
-    sincos(static_cast<double>(pos) * inv_freq, &sn, &cs);
-    const float c = static_cast<float>(cs);
-    const float s = static_cast<float>(sn);
     a = na * c - nb * s;
     b = nb * c + na * s;
+}
+
+__device__ inline void norm_rope_pair(float & a, float & b, float wa, float wb, float eps, int pos,
+                                      double inv_freq) {
+    float c, s;
+    rope_cos_sin(pos, inv_freq, c, s);
+    norm_rope_pair_cs(a, b, wa, wb, eps, c, s);
 }
 
 __device__ inline void norm_rope_pair(float & a, float & b, const float * w, float eps, int pos,

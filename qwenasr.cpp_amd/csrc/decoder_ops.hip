@@ -9,6 +9,7 @@
 #include "ops.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cmath>
 
 namespace qa {
@@ -48,43 +49,27 @@ __device__ inline float dot4(const f4 a, const f4 b, float acc) {
 }
 
 // IN4 = in_dim / 256 (each lane holds 4 * IN4 input elements), NR rows per wave iteration.
+// Load order: x and the norm weight first, then the weight rows of the wave's first iteration, so the
+// RMSNorm of x (which waits for its own loads only: vector loads complete in issue order) runs while
+// the weight rows stream in.  Rows past out_dim re-read the last row and are not stored.
 template <int IN4, int NR, int EPI, bool PRENORM>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x >> 6;
-    f4 xv[IN4];
-#pragma unroll
-    for (int k = 0; k < IN4; ++k) xv[k] = *reinterpret_cast<const f4 *>(p.x + k * 256 + lane * 4);
-    if (PRENORM) {
-        // rms_norm_row (text-decoder.cpp:542-557): squares in double, float scale, (x * scale) * w
-        double ss = 0.0;
-#pragma unroll
-        for (int k = 0; k < IN4; ++k) {
-            ss += static_cast<double>(xv[k].x) * xv[k].x + static_cast<double>(xv[k].y) * xv[k].y +
-                  static_cast<double>(xv[k].z) * xv[k].z + static_cast<double>(xv[k].w) * xv[k].w;
-        }
-        ss = wave_sum_d(ss);
-        const float scale = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(p.in_dim)) + p.eps);
-#pragma unroll
-        for (int k = 0; k < IN4; ++k) {
-            const f4 w = *reinterpret_cast<const f4 *>(p.norm_w + k * 256 + lane * 4);
-            xv[k].x = xv[k].x * scale * w.x;
-            xv[k].y = xv[k].y * scale * w.y;
-            xv[k].z = xv[k].z * scale * w.z;
-            xv[k].w = xv[k].w * scale * w.w;
-        }
-    }
     const int gw = blockIdx.x * 4 + wave;
     const int nw = gridDim.x * 4;
     const int64_t in = p.in_dim;
-    for (int o0 = gw * NR; o0 < p.out_dim; o0 += nw * NR) {
-        float acc[NR];
-        float accu[NR];
+    f4 xv[IN4], nv[IN4];
 #pragma unroll
-        for (int r = 0; r < NR; ++r) { acc[r] = 0.0f; accu[r] = 0.0f; }
-        f4 wv[NR][IN4];
-        f4 wu[NR][IN4];
+    for (int k = 0; k < IN4; ++k) xv[k] = *reinterpret_cast<const f4 *>(p.x + k * 256 + lane * 4);
+    if (PRENORM) {
+#pragma unroll
+        for (int k = 0; k < IN4; ++k) nv[k] = *reinterpret_cast<const f4 *>(p.norm_w + k * 256 + lane * 4);
+    }
+    f4 wv[NR][IN4];
+    f4 wu[NR][IN4];
+    auto load_rows = [&](int o0) {
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
             const int o = min(o0 + r, p.out_dim - 1);
@@ -101,6 +86,39 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
                 }
             }
         }
+    };
+    int o0 = gw * NR;
+    if (o0 >= p.out_dim) return;
+    asm volatile("" ::: "memory");   // x and the norm weight are issued before the weight rows
+    load_rows(o0);
+    // every load above is issued before the norm arithmetic: the empty asm orders the loads before it
+    // (memory clobber) and the arithmetic after it (it redefines x), otherwise the scheduler hoists the
+    // reduction, and its wait for x, above the weight loads
+#pragma unroll
+    for (int k = 0; k < IN4; ++k) asm volatile("" : "+v"(xv[k]) : : "memory");
+    if (PRENORM) {
+        // rms_norm_row (text-decoder.cpp:542-557): squares in double, float scale, (x * scale) * w
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < IN4; ++k) {
+            ss += static_cast<double>(xv[k].x) * xv[k].x + static_cast<double>(xv[k].y) * xv[k].y +
+                  static_cast<double>(xv[k].z) * xv[k].z + static_cast<double>(xv[k].w) * xv[k].w;
+        }
+        ss = wave_sum_d(ss);
+        const float scale = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(p.in_dim)) + p.eps);
+#pragma unroll
+        for (int k = 0; k < IN4; ++k) {
+            xv[k].x = xv[k].x * scale * nv[k].x;
+            xv[k].y = xv[k].y * scale * nv[k].y;
+            xv[k].z = xv[k].z * scale * nv[k].z;
+            xv[k].w = xv[k].w * scale * nv[k].w;
+        }
+    }
+    for (;;) {
+        float acc[NR];
+        float accu[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) { acc[r] = 0.0f; accu[r] = 0.0f; }
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
 #pragma unroll
@@ -121,6 +139,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
                 else p.y[o] = (a / (1.0f + expf(-a))) * u;   // silu(gate) * up (text-decoder.cpp:602)
             }
         }
+        o0 += nw * NR;
+        if (o0 >= p.out_dim) break;
+        load_rows(o0);
     }
 }
 
@@ -135,14 +156,36 @@ int launch_gemv_t(const GemvParams & p, hipStream_t stream) {
     return QA_OK;
 }
 
+// Rows per wave: the default keeps 16-32 KB of weights in flight per wave (measured on the 1.7B decode
+// step: 2 rows at in_dim 2048 beat 4 by 1.6%); QA_GEMV_NR = 1, 2 or 4 overrides it (tuning).
+int gemv_rows_override() {
+    static const int v = [] {
+        const char * e = std::getenv("QA_GEMV_NR");
+        const int n = e ? std::atoi(e) : 0;
+        return n == 1 || n == 2 || n == 4 ? n : 0;
+    }();
+    return v;
+}
+
+template <int IN4, int EPI, bool PRENORM>
+int launch_gemv_nr(int nr, const GemvParams & p, hipStream_t stream) {
+    switch (nr) {
+        case 1: return launch_gemv_t<IN4, 1, EPI, PRENORM>(p, stream);
+        case 2: return launch_gemv_t<IN4, 2, EPI, PRENORM>(p, stream);
+        default: return launch_gemv_t<IN4, 4, EPI, PRENORM>(p, stream);
+    }
+}
+
 template <int EPI, bool PRENORM>
 int launch_gemv_in(const GemvParams & p, hipStream_t stream) {
+    const int forced = gemv_rows_override();
+    const bool sw = EPI == kEpiSwiglu;
     switch (p.in_dim) {
-        case 1024: return launch_gemv_t<4, EPI == kEpiSwiglu ? 2 : 4, EPI, PRENORM>(p, stream);
-        case 2048: return launch_gemv_t<8, EPI == kEpiSwiglu ? 2 : 4, EPI, PRENORM>(p, stream);
-        case 3072: return launch_gemv_t<12, EPI == kEpiSwiglu ? 1 : 2, EPI, PRENORM>(p, stream);
-        case 4096: return launch_gemv_t<16, EPI == kEpiSwiglu ? 1 : 2, EPI, PRENORM>(p, stream);
-        case 6144: return launch_gemv_t<24, 1, EPI, PRENORM>(p, stream);
+        case 1024: return launch_gemv_nr<4, EPI, PRENORM>(forced ? forced : sw ? 2 : 4, p, stream);
+        case 2048: return launch_gemv_nr<8, EPI, PRENORM>(forced ? forced : 2, p, stream);
+        case 3072: return launch_gemv_nr<12, EPI, PRENORM>(forced ? forced : sw ? 1 : 2, p, stream);
+        case 4096: return launch_gemv_nr<16, EPI, PRENORM>(forced ? forced : sw ? 1 : 2, p, stream);
+        case 6144: return launch_gemv_nr<24, EPI, PRENORM>(forced ? forced : 1, p, stream);
         default: return fail(QA_ERR_INVALID, "gemv: in_dim must be one of 1024, 2048, 3072, 4096, 6144");
     }
 }

@@ -248,6 +248,16 @@ void qa_model_free(qa_model * model);
 /* Host view of one tensor by GGUF name (e.g. "text.blk.3.attn_q.weight"); NULL if absent. */
 const float * qa_model_tensor(const qa_model * model, const char * name, int64_t * n_elems);
 int qa_model_config(const qa_model * model, qa_text_config * cfg);
+
+/* Decoder-input assembly (qwenasr_decoder_input_from_audio, decoder-input.cpp:26-101, after the
+ * prompt has been tokenized): row t of out [n_tokens][hidden] is the embedding row of ids[t], except
+ * that the i-th id equal to audio_token_id takes audio row i of audio [audio_tokens][hidden].  All
+ * host memory.  Everything is validated before out is written, with the reference's errors: no ids,
+ * a negative audio_token_id, an empty audio block, an id outside [0, vocab), more placeholders than
+ * audio rows, or fewer.                                                                          */
+int qa_decoder_input_assemble(const float * token_embd, int32_t vocab, int32_t hidden, const int32_t * ids,
+                              int32_t n_tokens, int32_t audio_token_id, const float * audio, int32_t audio_tokens,
+                              float * out);
 int qa_model_weights_view(const qa_model * model, qa_layer_weights * layers, int32_t n_layers,
                           qa_model_weights * weights);
 

@@ -34,7 +34,7 @@ def test_c_abi_exports_every_declared_symbol(qa):
     assert set(names) == set(qa.SIGNATURES), set(names) ^ set(qa.SIGNATURES)
 
 
-@pytest.mark.parametrize("header", ["text-decoder.h", "ggml-backends.h", "gguf-model.h"])
+@pytest.mark.parametrize("header", ["text-decoder.h", "ggml-backends.h", "gguf-model.h", "decoder-input.h"])
 def test_cpp_drop_in_exports(header):
     syms = exported()
     names = header_functions(header)
@@ -93,3 +93,40 @@ def test_tool_argument_errors():
     assert r.returncode == 2 and "up to 1024" in r.stderr
     r = subprocess.run([TOOL, "--device", "tpu"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 2 and "auto, cpu, gpu, or cuda" in r.stderr
+
+
+def test_decoder_input_assembly(qa):
+    """qwenasr_decoder_input_from_audio after tokenization (decoder-input.cpp:26-101): embedding rows of
+    the prompt ids, the i-th audio placeholder replaced by audio row i; errors before any write."""
+    vocab, hidden, pad = 50, 16, 7
+    rng = np.random.default_rng(3)
+    embd = rng.standard_normal((vocab, hidden)).astype(np.float32)
+    audio = rng.standard_normal((4, hidden)).astype(np.float32)
+    ids = np.array([1, 2, 3, pad, pad, pad, pad, 4, 5, 49, 0], np.int32)
+    out = np.zeros((len(ids), hidden), np.float32)
+
+    def run(ids, audio, out, audio_token_id=pad, vocab=vocab):
+        return qa.lib.qa_decoder_input_assemble(embd.ctypes.data, vocab, hidden, ids.ctypes.data, len(ids),
+                                                audio_token_id, audio.ctypes.data, len(audio), out.ctypes.data)
+
+    assert run(ids, audio, out) == qa.QA_OK
+    expect = embd[ids].copy()
+    expect[3:7] = audio
+    np.testing.assert_array_equal(out.view(np.uint32), expect.view(np.uint32))
+    cases = [
+        (np.array([1, pad, pad, 2], np.int32), audio, "audio placeholder count does not match"),
+        (np.array([pad] * 5, np.int32), audio, "more audio placeholders than audio encoder outputs"),
+        (np.array([1, pad, pad, pad, pad, vocab], np.int32), audio, "out of embedding range"),
+        (np.array([-1, pad, pad, pad, pad], np.int32), audio, "out of embedding range"),
+    ]
+    for bad_ids, a, msg in cases:
+        sentinel = np.full((len(bad_ids), hidden), 7.5, np.float32)
+        assert run(bad_ids, a, sentinel) == qa.QA_ERR_INVALID
+        assert msg in qa.lib.qa_last_error().decode(), msg
+        assert (sentinel == 7.5).all()                     # nothing written on error
+    assert run(ids, audio, out, audio_token_id=-1) == qa.QA_ERR_INVALID
+    assert "invalid decoder input configuration" in qa.lib.qa_last_error().decode()
+    empty = np.zeros((0,), np.int32)
+    assert qa.lib.qa_decoder_input_assemble(embd.ctypes.data, vocab, hidden, empty.ctypes.data, 0, pad,
+                                            audio.ctypes.data, len(audio), out.ctypes.data) == qa.QA_ERR_INVALID
+    assert "no tokens" in qa.lib.qa_last_error().decode()

@@ -167,6 +167,27 @@ def test_decode_attention_growing_lengths_one_workspace(qa, orc, f16):
             check_close(got[s], ref)
 
 
+@pytest.mark.parametrize("f16,L", [(True, 9000), (False, 9000), (True, 16385), (True, 40000)])
+def test_decode_attention_long_context(qa, orc, f16, L):
+    """Long single-stream contexts: the capacity selects the values kernel's register budgets (chunk
+    statistics held in 2-8 register slots plus the loop beyond them at 40000, merge rounds of 40 loads
+    over 36-157 participants), so every variant is held to the same bar."""
+    lay = layout(qa, 1, 1, L + 3, f16)
+    cache = Cache(qa, lay)
+    rng = np.random.default_rng(L)
+    vals = cache.fill(rng, 0, [L])
+    q = rng.standard_normal((1, 16, 128)).astype(np.float32)
+    d_q, d_out = dev(qa, q), zeros(qa, (1, 2048))
+    ws_bytes = qa.lib.qa_decode_attn_workspace_bytes(1, 16, lay.max_seq)
+    ws = zeros(qa, ws_bytes, np.uint8)
+    print(f"decode long f16={f16} L={L}", flush=True)
+    k, v = vals[0]
+    ref = orc.cache_attention(k, v, q, L - 1, f16)[0]
+    for rep in range(2):
+        got = _decode(qa, d_q, cache, lay, 0, [L], L, d_out, ws, ws_bytes)
+        check_close(got[0], ref)
+
+
 def test_decode_attention_rejects_small_workspace(qa):
     lay = layout(qa, 1, 1, 4096, True)
     cache = Cache(qa, lay)

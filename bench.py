@@ -203,11 +203,19 @@ def multistream_roofline(qa, cfg, reps: int):
 
 
 def kernel_only(which: str, reps: int):
+    if which == "multistream":
+        import qwenasr_amd as qa
+        from qwenasr_amd import configs
+
+        w = configs.CONFIGS[4]
+        model = qa.Model(w.size, n_layers=w.n_layers)
+        print(json.dumps(dict(kernel=which, **multistream_decode(qa, model, reps))), flush=True)
+        return
     """One hot-path kernel on synthetic inputs at the config-3 shape, for rocprofv3 passes (the counters
     of every dispatch are then the kernel's alone).  append: the prefill K/V append of 3913 positions
     (q/k norm + RoPE, f16 cache write); prefill: causal prefill attention over 3913 positions of one
     layer (f16 cache, n_past 0); decode-attn: the decode-step attention of one layer at L = 4186,
-    rotating 28 layer caches."""
+    rotating 28 layer caches; multistream: the config-4 decode step of 32 streams (end to end)."""
     import ctypes as C
 
     import numpy as np
@@ -276,6 +284,32 @@ def kernel_only(which: str, reps: int):
     print(json.dumps(dict(kernel=which, launches=reps + 1, avg_us=round(us, 3), **unit)), flush=True)
 
 
+def multistream_decode(qa, model, steps: int):
+    """Config 4 end to end: 32 streams at the config's seeded ragged lengths (156..3913), lock-step
+    greedy decode (per step: embedding, 28 layers with f32 projections of 32 rows, fused append +
+    split-K attention over every stream, LM head, argmax).  Cache contents do not change the time, so
+    the lengths are set without filling K/V.  value = aggregate generated tokens per second."""
+    import numpy as np
+    from qwenasr_amd import configs
+
+    w = configs.CONFIGS[4]
+    lens = configs.cfg4_lengths(w.streams)
+    first = configs.cfg4_first_ids(w.streams).astype(np.int32)
+    with qa.Decoder(model, w.streams, w.max_seq, w.cache_type) as dec:
+        for s_ in range(w.streams):
+            dec.set_cur_len(s_, int(lens[s_]))
+        ids = dec.decode_streams(first, 2)                  # warm
+        qa.check(qa.lib.qa_device_synchronize())
+        t0 = time.perf_counter()
+        dec.decode_streams(ids[-1].astype(np.int32), steps)
+        qa.check(qa.lib.qa_device_synchronize())
+        dt = time.perf_counter() - t0
+    return {"streams": w.streams, "steps": steps, "ms_per_step": round(dt * 1e3 / steps, 3),
+            "tok_s": round(w.streams * steps / dt, 1),
+            "workload": f"config 4: {w.streams} streams, contexts {int(lens.min())}..{int(lens.max())} + {steps + 2}, "
+                        f"lock-step greedy decode, f16 cache, f32 weights"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -284,11 +318,12 @@ def main():
     ap.add_argument("--config", type=int, default=3, choices=[2, 3])
     ap.add_argument("--roofline-reps", type=int, default=20)
     ap.add_argument("--profile-steps", type=int, default=8)
+    ap.add_argument("--multistream-steps", type=int, default=16)
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 10 times (reference for HBM traffic counters)")
-    ap.add_argument("--kernel", choices=["append", "prefill", "decode-attn"],
+    ap.add_argument("--kernel", choices=["append", "prefill", "decode-attn", "multistream"],
                     help="only run one hot-path kernel on synthetic inputs (short program for rocprofv3 passes)")
     ap.add_argument("--kernel-reps", type=int, default=20)
     args = ap.parse_args()
@@ -355,6 +390,9 @@ def main():
     log(f"config-4 multi-stream attention: {roof4['avg_launch_us']:.1f} us per layer, {roof4['achieved']:.0f} GB/s "
         f"({100 * roof4['frac']:.1f}% of peak)")
 
+    ms4 = multistream_decode(qa, model, args.multistream_steps)
+    log(f"config-4 decode, {ms4['streams']} streams: {ms4['ms_per_step']:.2f} ms per step, {ms4['tok_s']:.0f} tok/s")
+
     traffic, traffic_note = measured_traffic(attn_bytes)
     weight_bytes = int(4 * sum(model.tensor(n).size for n in (
         [f"text.blk.{l}.{t}.weight" for l in range(model.cfg.n_layers) for t in
@@ -382,6 +420,7 @@ def main():
                                "decode_values_kernel, launched back to back",
                      "bytes_per_launch": attn_bytes, "attended_positions": L, "avg_launch_us": round(attn_us, 3)},
         "roofline_multistream": roof4,
+        "multistream_decode": ms4,
         "attn_us_per_layer": round(attn_us, 3),
         "prefill_ms": round(prefill_ms, 2),
         "weight_bytes_per_token": weight_bytes,

@@ -176,6 +176,16 @@ int qa_qk_prep(float * qkv, int32_t n_tokens, int32_t n_heads, int32_t n_kv_head
 
 /* ---------------------------------------------------------------- adjacent decoder ops (row f1)
  * f32 weights stored row-major [out][in] (GGML ne = [in, out], text-decoder.cpp:219-227).       */
+/* Skinny GEMM for the multi-stream decode step (one token per stream): y[rows][out] (+)= x[rows][in] *
+ * W[out][in]^T for 1 <= rows <= 64 and in_dim a multiple of 32, on f32 MFMA (exact f32 products,  *
+ * f32 sums).  Replaces the decode-time linear_ggml calls (text-decoder.cpp:83-90) at batch > 1.     *
+ * The workspace (qa_gemm_rows_workspace_bytes, zeroed once) holds tile counters that every call  *
+ * leaves at zero, in a fixed region, then per-slice partials: a workspace sized for the largest   *
+ * shape serves every smaller one; calls sharing it must be stream-ordered.  out_dim <= 262144.    */
+size_t qa_gemm_rows_workspace_bytes(int32_t out_dim, int32_t in_dim, int32_t rows);
+int qa_gemm_rows(const float * W, int32_t out_dim, int32_t in_dim, const float * x, int32_t rows, float * y,
+                 int32_t accumulate, void * workspace, size_t workspace_bytes, void * stream);
+
 /* y[r][o] = sum_i W[o][i] * x[r][i]  (+ y[r][o] when accumulate != 0); rows small (decode).     */
 int qa_gemv(const float * W, int32_t out_dim, int32_t in_dim, const float * x, int32_t rows,
             float * y, int32_t accumulate, void * stream);

@@ -35,6 +35,8 @@ struct DevLayer {
 
 enum Kind { kDecode = 0, kPrefill = 1, kNoCache = 2 };
 
+constexpr int32_t kSkinnyRows = 64;   // token rows up to which projections use the skinny MFMA GEMM
+
 enum Family { kFamAppend = 0, kFamDecodeAttn, kFamPrefillAttn, kFamProj, kFamLogits, kFamCount };
 const char * kFamNames[kFamCount] = {"kv_append", "decode_attn", "prefill_attn", "projections", "logits"};
 
@@ -63,6 +65,8 @@ struct qa_decoder {
     size_t attn_ws_bytes = 0;
     void * am_ws = nullptr;
     size_t am_ws_bytes = 0;
+    void * gr_ws = nullptr;      // skinny-GEMM partials and tile counters (activation allocation)
+    size_t gr_ws_bytes = 0;
     int32_t * d_ids = nullptr;
     int32_t * h_ids = nullptr;   // pinned
     float * staging = nullptr;
@@ -130,6 +134,19 @@ void free_acts(qa_decoder * d) {
     for (void * p : d->act_allocs) (void)hipFree(p);
     d->act_allocs.clear();
     d->cap_rows = 0;
+    d->gr_ws = nullptr;
+    d->gr_ws_bytes = 0;
+}
+
+// Workspace of the skinny GEMM for the layer projections at up to `rows` token rows and the LM head at
+// up to `logit_rows` (its size grows with the row count, so the largest count covers all smaller ones).
+size_t gemm_rows_bytes_for(const qa_text_config & c, int32_t rows, int32_t logit_rows) {
+    const int32_t H = c.hidden, QD = c.n_heads * kHeadDim, KD = c.n_kv_heads * kHeadDim, I = c.intermediate;
+    const int32_t shapes[4][2] = {{QD + 2 * KD, H}, {H, QD}, {2 * I, H}, {H, I}};
+    size_t m = 0;
+    for (const auto & sh : shapes) m = std::max(m, gemm_rows_workspace_bytes(sh[0], sh[1], rows));
+    if (logit_rows >= 2) m = std::max(m, gemm_rows_workspace_bytes(c.vocab, H, logit_rows));
+    return m;
 }
 
 int ensure_rows(qa_decoder * d, int32_t rows) {
@@ -147,6 +164,15 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
     rc = rc ? rc : dmalloc_t(d->act_allocs, R * QD, &d->attn);
     rc = rc ? rc : dmalloc_t(d->act_allocs, R * 2 * I, &d->gu);
     rc = rc ? rc : dmalloc_t(d->act_allocs, R * I, &d->act);
+    // the LM head runs on one row per stream (decode) or the last row (prefill)
+    const size_t gr = rows >= 2 ? gemm_rows_bytes_for(d->cfg, std::min<int32_t>(rows, kSkinnyRows),
+                                                      std::min<int32_t>(d->n_streams, kSkinnyRows))
+                                : 0;
+    if (rc == QA_OK && gr > 0) {
+        rc = dmalloc(d->act_allocs, gr, &d->gr_ws);
+        if (rc == QA_OK && hipMemset(d->gr_ws, 0, gr) != hipSuccess) rc = fail(QA_ERR_DEVICE, "workspace clear failed");
+        if (rc == QA_OK) d->gr_ws_bytes = gr;
+    }
     if (rc != QA_OK) {
         free_acts(d);
         return rc;
@@ -158,7 +184,12 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
 
 int sgemm(qa_decoder * d, const float * W, int32_t out_dim, int32_t in_dim, const float * X, int32_t rows, float * Y,
           float beta) {
-    // Y[rows][out] (+)= X[rows][in] * W[out][in]^T, as column-major C(out x rows) = W^T(out x in) * X(in x rows)
+    // Y[rows][out] (+)= X[rows][in] * W[out][in]^T.  Up to kSkinnyRows rows (multi-stream decode, short
+    // prefills) the weights are streamed once by the skinny MFMA GEMM; longer prefills use rocBLAS.
+    if (rows <= kSkinnyRows && in_dim % 32 == 0 && d->gr_ws) {
+        return gemm_rows_launch(W, out_dim, in_dim, X, rows, Y, beta != 0.0f, d->gr_ws, d->gr_ws_bytes, d->stream);
+    }
+    // column-major C(out x rows) = W^T(out x in) * X(in x rows)
     const float alpha = 1.0f;
     const rocblas_status st = rocblas_sgemm(d->blas, rocblas_operation_transpose, rocblas_operation_none, out_dim,
                                             rows, in_dim, &alpha, W, in_dim, X, in_dim, &beta, Y, out_dim);

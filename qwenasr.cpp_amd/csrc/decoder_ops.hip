@@ -190,6 +190,232 @@ int launch_gemv_in(const GemvParams & p, hipStream_t stream) {
     }
 }
 
+// ---------------------------------------------------------------- skinny GEMM (2..64 token rows)
+// Y[rows][N] (+)= X[rows][K] W[N][K]^T for the multi-stream decode step (one token per stream), on
+// f32 MFMA (v_mfma_f32_16x16x4_f32: exact f32 products, f32 sums, as the reference's PREC_F32 GEMM).
+// The weights dominate the bytes (each W element meets every token row once), so the kernel is built
+// to stream W at HBM rate:
+// - a workgroup owns 64 output rows (16 per wave) over one K slice; the tile's slices are consecutive
+//   workgroups, and the number of slices is chosen so that ~512 workgroups cover the matrix;
+// - the X slice of every token (<= 64 KB) is staged once in LDS and read as the B operand;
+// - W streams straight from HBM into the A operand: lane l reads row l % 16 of its wave's block,
+//   8 consecutive k at 8 (l / 16), i.e. 128 contiguous bytes per row per wave instruction pair; the
+//   k order inside an MFMA step is a permutation shared by A and B, which the sum does not see;
+// - slices are merged by the last workgroup of each tile (agent-scope publish + counter on its own
+//   cache line), in slice order, so the result does not depend on scheduling.
+constexpr int kGrTile = 64;          // output rows per workgroup
+constexpr int kGrMaxRows = 64;       // token rows supported
+constexpr int kGrLdsBytes = 64 * 1024;
+constexpr int kGrCounterStride = 64; // uint32 per tile counter (256 bytes)
+// The workspace starts with a fixed counter region for kGrMaxTiles tiles, followed by the partials:
+// one layout for every shape, so calls of different shapes can share a workspace without one call's
+// partials landing on another call's counters.
+constexpr int kGrMaxTiles = 4096;    // N <= 262144
+constexpr size_t kGrCounterBytes = static_cast<size_t>(kGrMaxTiles) * kGrCounterStride * sizeof(uint32_t);
+
+struct GemmRowsParams {
+    const float * W;          // [N][K]
+    const float * X;          // [rows][K]
+    float * Y;                // [rows][N]
+    float * partial;          // [ks][rows][N] (ks > 1)
+    uint32_t * counters;      // [tiles][kGrCounterStride]
+    int32_t N, K, rows, ks, slice, accumulate;
+};
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+template <int TB>
+__global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
+#pragma clang fp contract(off)
+    extern __shared__ __attribute__((aligned(16))) float sX[];      // [16 TB][slice + 4]
+    const int tile = static_cast<int>(blockIdx.x) / p.ks;
+    const int sl = static_cast<int>(blockIdx.x) - tile * p.ks;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x >> 6;
+    const int k_begin = sl * p.slice;
+    const int k_len = min(p.slice, p.K - k_begin);                 // multiple of 32
+    const int xs = p.slice + 4;                                      // LDS row stride (floats)
+
+    // W rows of this lane: row n0 + lane % 16 (clamped; rows past N are not stored)
+    const int n0 = tile * kGrTile + wave * 16;
+    const int nrow = min(n0 + (lane & 15), p.N - 1);
+    const int g = lane >> 4;
+    const float * wr = p.W + static_cast<int64_t>(nrow) * p.K + k_begin + 8 * g;
+
+    // X slice first (at most 16 16-byte loads per thread; token rows past `rows` are zero), then the
+    // first batch of W: vector loads complete in issue order, so staging X into LDS waits for X only
+    // while W streams in
+    constexpr int kXPer = 16;
+    const int x_vecs = 16 * TB * (k_len / 4);
+    v4f xv[kXPer];
+#pragma unroll
+    for (int u = 0; u < kXPer; ++u) {
+        const int i = min(static_cast<int>(threadIdx.x) + 256 * u, x_vecs - 1);
+        const int t = min(i / (k_len / 4), p.rows - 1), c = i - (i / (k_len / 4)) * (k_len / 4);
+        xv[u] = *reinterpret_cast<const v4f *>(p.X + static_cast<int64_t>(t) * p.K + k_begin + 4 * c);
+    }
+    asm volatile("" ::: "memory");
+    constexpr int kB = 16;                                           // 32-k steps per batch (slices <= 512: one)
+    const int n_steps = k_len / 32;
+    v4f wa[kB][2];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+        const int st = min(u, n_steps - 1);
+        wa[u][0] = *reinterpret_cast<const v4f *>(wr + 32 * st);
+        wa[u][1] = *reinterpret_cast<const v4f *>(wr + 32 * st + 4);
+    }
+#pragma unroll
+    for (int u = 0; u < kXPer; ++u) {
+        const int i = static_cast<int>(threadIdx.x) + 256 * u;
+        if (i < x_vecs) {
+            const int t = i / (k_len / 4), c = i - t * (k_len / 4);
+            *reinterpret_cast<v4f *>(sX + t * xs + 4 * c) = t < p.rows ? xv[u] : v4f{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    __syncthreads();
+
+    // two accumulator chains per token block (even and odd 4-k substeps), added at the end in a fixed
+    // order: twice the independent MFMAs in flight
+    v4f acc[TB], acc2[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) { acc[tb] = v4f{0.f, 0.f, 0.f, 0.f}; acc2[tb] = acc[tb]; }
+    const float * xr = sX + (lane & 15) * xs + 8 * g;
+    for (int s0 = 0; s0 < n_steps; s0 += kB) {
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+            if (s0 + u < n_steps) {
+                const int kk = 32 * (s0 + u);
+#pragma unroll
+                for (int tb = 0; tb < TB; ++tb) {
+                    const v4f x0 = *reinterpret_cast<const v4f *>(xr + tb * 16 * xs + kk);
+                    const v4f x1 = *reinterpret_cast<const v4f *>(xr + tb * 16 * xs + kk + 4);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        acc[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[u][0][j], x0[j], acc[tb], 0, 0, 0);
+                        acc2[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[u][1][j], x1[j], acc2[tb], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        // slices longer than one batch (one token block only): the next batch
+        if (s0 + kB < n_steps) {
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                const int st = min(s0 + kB + u, n_steps - 1);
+                wa[u][0] = *reinterpret_cast<const v4f *>(wr + 32 * st);
+                wa[u][1] = *reinterpret_cast<const v4f *>(wr + 32 * st + 4);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) acc[tb] += acc2[tb];
+    // acc[tb][i] = sum for W row n0 + 4 g + i and token 16 tb + lane % 16
+    const int nr = n0 + 4 * g;
+    if (p.ks == 1) {
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+            const int t = 16 * tb + (lane & 15);
+            if (t >= p.rows) continue;
+            float * y = p.Y + static_cast<int64_t>(t) * p.N + nr;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (nr + i < p.N) y[i] = p.accumulate ? y[i] + acc[tb][i] : acc[tb][i];
+            }
+        }
+        return;
+    }
+    // publish this slice's partial (rows nr .. nr + 3 of a token: two 8-byte agent-scope stores; the
+    // partial buffer is padded to whole 4-row groups), then the last slice of the tile merges in slice
+    // order
+    const int np = (p.N + 3) / 4 * 4;                                // partial row pitch
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+        const int t = 16 * tb + (lane & 15);
+        if (t >= p.rows || nr >= p.N) continue;
+        uint64_t * q = reinterpret_cast<uint64_t *>(p.partial + (static_cast<int64_t>(sl) * p.rows + t) * np + nr);
+        const uint64_t lo = static_cast<uint64_t>(__float_as_uint(acc[tb][0])) |
+                            (static_cast<uint64_t>(__float_as_uint(acc[tb][1])) << 32);
+        const uint64_t hi = static_cast<uint64_t>(__float_as_uint(acc[tb][2])) |
+                            (static_cast<uint64_t>(__float_as_uint(acc[tb][3])) << 32);
+        __hip_atomic_store(q, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(q + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __shared__ int s_last;
+    if (threadIdx.x == 0) {
+        uint32_t * ctr = p.counters + static_cast<int64_t>(tile) * kGrCounterStride;
+        const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == static_cast<uint32_t>(p.ks - 1);
+        if (s_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    // all loads of a group of 8 slices in flight before the sums (slice order kept)
+    float sum[TB][4];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sum[tb][i] = 0.0f;
+    }
+    const bool live = nr < p.N;
+    for (int k0 = 0; k0 < p.ks; k0 += 8) {
+        uint64_t v[8][TB][2];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) {
+                const int t = min(16 * tb + (lane & 15), p.rows - 1);
+                const int k = min(k0 + u, p.ks - 1);
+                const uint64_t * q =
+                    reinterpret_cast<const uint64_t *>(p.partial + (static_cast<int64_t>(k) * p.rows + t) * np + min(nr, np - 4));
+                v[u][tb][0] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                v[u][tb][1] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (k0 + u >= p.ks) break;
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) {
+                sum[tb][0] += __uint_as_float(static_cast<uint32_t>(v[u][tb][0]));
+                sum[tb][1] += __uint_as_float(static_cast<uint32_t>(v[u][tb][0] >> 32));
+                sum[tb][2] += __uint_as_float(static_cast<uint32_t>(v[u][tb][1]));
+                sum[tb][3] += __uint_as_float(static_cast<uint32_t>(v[u][tb][1] >> 32));
+            }
+        }
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+        const int t = 16 * tb + (lane & 15);
+        if (t >= p.rows || !live) continue;
+        float * y = p.Y + static_cast<int64_t>(t) * p.N + nr;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (nr + i < p.N) y[i] = p.accumulate ? y[i] + sum[tb][i] : sum[tb][i];
+        }
+    }
+}
+
+struct GemmRowsPlan {
+    int ks, slice, tiles;
+};
+
+GemmRowsPlan gemm_rows_plan(int32_t N, int32_t K, int32_t rows) {
+    GemmRowsPlan pl{};
+    pl.tiles = (N + kGrTile - 1) / kGrTile;
+    const int rows_pad = (rows + 15) / 16 * 16;
+    // ~512 workgroups, and the X slice of every token (padded row stride) within the LDS budget
+    int ks = std::max(1, std::min((512 + pl.tiles - 1) / pl.tiles, K / 32));
+    for (;; ++ks) {
+        pl.slice = ((K + ks - 1) / ks + 31) / 32 * 32;
+        if (static_cast<size_t>(rows_pad) * (pl.slice + 4) * sizeof(float) <= kGrLdsBytes || pl.slice == 32) break;
+    }
+    pl.ks = (K + pl.slice - 1) / pl.slice;
+    return pl;
+}
+
 // ---------------------------------------------------------------- row RMSNorm (T > 1 paths)
 __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float * x, const float * w, int dim, float eps,
                                                            float * y) {
@@ -329,6 +555,47 @@ int gemv_launch(int epi, bool prenorm, const float * W, int32_t out_dim, int32_t
     if (epi == kEpiStore) return prenorm ? launch_gemv_in<kEpiStore, true>(p, stream) : launch_gemv_in<kEpiStore, false>(p, stream);
     if (epi == kEpiAccum) return prenorm ? launch_gemv_in<kEpiAccum, true>(p, stream) : launch_gemv_in<kEpiAccum, false>(p, stream);
     return prenorm ? launch_gemv_in<kEpiSwiglu, true>(p, stream) : launch_gemv_in<kEpiSwiglu, false>(p, stream);
+}
+
+size_t gemm_rows_workspace_bytes(int32_t N, int32_t K, int32_t rows) {
+    if (N <= 0 || N > kGrMaxTiles * kGrTile || K <= 0 || rows <= 0 || rows > kGrMaxRows || K % 32 != 0) return 0;
+    const GemmRowsPlan pl = gemm_rows_plan(N, K, rows);
+    const size_t partial = pl.ks > 1 ? static_cast<size_t>(pl.ks) * rows * ((N + 3) / 4 * 4) * sizeof(float) : 0;
+    return kGrCounterBytes + partial;
+}
+
+int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int32_t rows, float * Y, bool accumulate,
+                     void * workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!W || !X || !Y || N <= 0 || N > kGrMaxTiles * kGrTile || K <= 0 || K % 32 != 0 || rows < 1 ||
+        rows > kGrMaxRows) {
+        return fail(QA_ERR_INVALID, "gemm_rows: invalid shape");
+    }
+    const GemmRowsPlan pl = gemm_rows_plan(N, K, rows);
+    const size_t need = gemm_rows_workspace_bytes(N, K, rows);
+    if (!workspace || workspace_bytes < need) return fail(QA_ERR_INVALID, "gemm_rows: workspace too small");
+    GemmRowsParams p{};
+    p.W = W;
+    p.X = X;
+    p.Y = Y;
+    p.counters = static_cast<uint32_t *>(workspace);
+    p.partial = reinterpret_cast<float *>(static_cast<char *>(workspace) + kGrCounterBytes);
+    p.N = N;
+    p.K = K;
+    p.rows = rows;
+    p.ks = pl.ks;
+    p.slice = pl.slice;
+    p.accumulate = accumulate ? 1 : 0;
+    const int tb = (rows + 15) / 16;
+    const size_t lds = static_cast<size_t>(16 * tb) * (pl.slice + 4) * sizeof(float);
+    const dim3 grid(static_cast<unsigned>(pl.tiles * pl.ks));
+    switch (tb) {
+        case 1: hipLaunchKernelGGL((gemm_rows_kernel<1>), grid, dim3(256), lds, stream, p); break;
+        case 2: hipLaunchKernelGGL((gemm_rows_kernel<2>), grid, dim3(256), lds, stream, p); break;
+        case 3: hipLaunchKernelGGL((gemm_rows_kernel<3>), grid, dim3(256), lds, stream, p); break;
+        default: hipLaunchKernelGGL((gemm_rows_kernel<4>), grid, dim3(256), lds, stream, p); break;
+    }
+    QA_LAUNCH_CHECK("gemm_rows_kernel");
+    return QA_OK;
 }
 
 size_t argmax_workspace_bytes(int32_t rows) {
@@ -478,3 +745,13 @@ int cast_rows_launch(const float * src, void * dst, int32_t cache_type, int64_t 
 }
 
 }  // namespace qa
+
+extern "C" size_t qa_gemm_rows_workspace_bytes(int32_t out_dim, int32_t in_dim, int32_t rows) {
+    return qa::gemm_rows_workspace_bytes(out_dim, in_dim, rows);
+}
+
+extern "C" int qa_gemm_rows(const float * W, int32_t out_dim, int32_t in_dim, const float * x, int32_t rows, float * y,
+                            int32_t accumulate, void * workspace, size_t workspace_bytes, void * stream) {
+    return qa::gemm_rows_launch(W, out_dim, in_dim, x, rows, y, accumulate != 0, workspace, workspace_bytes,
+                                qa::as_stream(stream));
+}

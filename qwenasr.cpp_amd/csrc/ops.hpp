@@ -9,6 +9,10 @@ enum { kEpiStoreOp = 0, kEpiAccumOp = 1, kEpiSwigluOp = 2 };
 
 int gemv_launch(int epi, bool prenorm, const float * W, int32_t out_dim, int32_t in_dim, const float * x, float * y,
                 const float * norm_w, float eps, hipStream_t stream);
+// Y[rows][N] (+)= X[rows][K] W[N][K]^T for 1..64 rows (K a multiple of 32), f32 MFMA.
+size_t gemm_rows_workspace_bytes(int32_t N, int32_t K, int32_t rows);
+int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int32_t rows, float * Y, bool accumulate,
+                     void * workspace, size_t workspace_bytes, hipStream_t stream);
 size_t argmax_workspace_bytes(int32_t rows);
 int argmax_launch(const float * logits, int32_t rows, int32_t vocab, int32_t * ids, void * workspace,
                   hipStream_t stream);

@@ -119,6 +119,8 @@ SIGNATURES = {
     "qa_model_tensor": (fp, vp, C.c_char_p, C.POINTER(i64)),
     "qa_model_config": (C.c_int, vp, C.POINTER(TextConfig)),
     "qa_decoder_input_assemble": (C.c_int, vp, i32, i32, vp, i32, i32, vp, i32, vp),
+    "qa_gemm_rows_workspace_bytes": (sz, i32, i32, i32),
+    "qa_gemm_rows": (C.c_int, vp, i32, i32, vp, i32, vp, i32, vp, sz, vp),
     "qa_model_weights_view": (C.c_int, vp, C.POINTER(LayerWeights), i32, C.POINTER(ModelWeights)),
     "qa_decoder_create": (C.c_int, C.POINTER(TextConfig), C.POINTER(ModelWeights), i32, i32, i32, C.POINTER(vp)),
     "qa_decoder_destroy": (None, vp),

@@ -300,6 +300,58 @@ def test_gemv(qa, orc, in_dim, out_dim):
     np.testing.assert_allclose(d_y.numpy(), y0 + orc.linear(x, w), rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("out_dim,in_dim,rows", [(4096, 2048, 32), (2048, 2048, 5), (12288, 2048, 32),
+                                                  (2048, 6144, 32), (20000, 2048, 32), (100, 1024, 64),
+                                                  (2048, 6144, 1), (3000, 3072, 17), (4096, 1024, 49),
+                                                  (1024, 2048, 49), (6144, 1024, 49), (1024, 3072, 49)])
+def test_gemm_rows(qa, out_dim, in_dim, rows):
+    """Skinny f32 MFMA GEMM of the multi-stream decode step against float64, store and accumulate,
+    twice on one workspace (slice counters left at zero)."""
+    rng = np.random.default_rng(out_dim + in_dim + rows)
+    w = (rng.standard_normal((out_dim, in_dim)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((rows, in_dim)).astype(np.float32)
+    y0 = rng.standard_normal((rows, out_dim)).astype(np.float32)
+    d_w, d_x = dev(qa, w), dev(qa, x)
+    wsb = qa.lib.qa_gemm_rows_workspace_bytes(out_dim, in_dim, rows)
+    assert wsb > 0
+    ws = zeros(qa, wsb, np.uint8)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    print(f"gemm_rows {out_dim}x{in_dim} rows={rows}", flush=True)
+    for acc in (0, 1, 0):
+        d_y = dev(qa, y0)
+        qa.check(qa.lib.qa_gemm_rows(d_w.ptr, out_dim, in_dim, d_x.ptr, rows, d_y.ptr, acc, ws.ptr, wsb, NULL_STREAM))
+        qa.synchronize()
+        got = d_y.numpy()
+        expect = ref + (y0 if acc else 0.0)
+        np.testing.assert_allclose(got, expect, rtol=1e-4, atol=2e-4)
+
+
+def test_gemm_rows_shared_workspace(qa):
+    """One workspace, sized for the largest shape, serves a sequence of different shapes (as in a
+    decoder layer) with no clearing: counters and partials never overlap across shapes."""
+    rng = np.random.default_rng(11)
+    rows = 49
+    shapes = [(4096, 1024), (1024, 2048), (6144, 1024), (1024, 3072), (4096, 1024), (6144, 1024)]
+    wsb = max(qa.lib.qa_gemm_rows_workspace_bytes(n, k, rows) for n, k in shapes)
+    ws = zeros(qa, wsb, np.uint8)
+    for n, k in shapes:
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        x = rng.standard_normal((rows, k)).astype(np.float32)
+        d_w, d_x, d_y = dev(qa, w), dev(qa, x), zeros(qa, (rows, n))
+        print(f"gemm_rows shared {n}x{k}", flush=True)
+        qa.check(qa.lib.qa_gemm_rows(d_w.ptr, n, k, d_x.ptr, rows, d_y.ptr, 0, ws.ptr, wsb, NULL_STREAM))
+        qa.synchronize()
+        np.testing.assert_allclose(d_y.numpy(), x.astype(np.float64) @ w.astype(np.float64).T, rtol=1e-4, atol=2e-4)
+
+
+def test_gemm_rows_rejects_bad_shapes(qa):
+    assert qa.lib.qa_gemm_rows_workspace_bytes(100, 1000, 4) == 0       # in_dim not a multiple of 32
+    assert qa.lib.qa_gemm_rows_workspace_bytes(100, 1024, 65) == 0      # more than 64 rows
+    d = zeros(qa, 64)
+    rc = qa.lib.qa_gemm_rows(d.ptr, 100, 1024, d.ptr, 4, d.ptr, 0, d.ptr, 0, NULL_STREAM)
+    assert rc == qa.QA_ERR_INVALID and b"workspace" in qa.lib.qa_last_error()
+
+
 def test_rmsnorm_rows_bit_exact(qa, orc):
     rng = np.random.default_rng(3)
     x = (rng.standard_normal((7, 2048)) * 2).astype(np.float32)

@@ -148,18 +148,19 @@ def copy_calibration(reps: int = 10, mib: int = 256):
     print(json.dumps({"copy_calibration": {"bytes_per_copy": n, "copies": reps}}), flush=True)
 
 
-def multistream_roofline(qa, cfg, reps: int):
-    """Config-4 shapes: 32 streams, context lengths U[156, 3913] (the config's seeded lengths), one
-    decode-step attention launch pair per layer covering all streams, rotating over 28 layer caches
+def multistream_roofline(qa, cfg, reps: int, lens=None, label: str = "config 4 shapes"):
+    """Multi-stream decode-step attention: one launch pair per layer covering every stream, rotating over
+    28 layer caches (so no cache can serve them).  Default lengths: config 4's seeded U[156, 3913]
     (14.6 GB of f16 KV).  Cache contents do not change the bytes moved, so the cache stays zeroed."""
     import ctypes as C
 
     import numpy as np
     from qwenasr_amd import configs
 
-    w = configs.CONFIGS[4]
-    lens = configs.cfg4_lengths(w.streams).astype(np.int32)
-    S = w.streams
+    if lens is None:
+        lens = configs.cfg4_lengths(configs.CONFIGS[4].streams)
+    lens = np.asarray(lens).astype(np.int32)
+    S = len(lens)
     cap = int(lens.max()) + 2
     lay = qa.KvLayout(cfg.n_layers, S, cfg.n_kv_heads, cfg.head_dim, cap, qa.QA_CACHE_F16)
     cache = qa.DeviceArray(qa.lib.qa_kv_cache_bytes(C.byref(lay)), np.uint8)
@@ -198,7 +199,7 @@ def multistream_roofline(qa, cfg, reps: int):
     achieved = nbytes / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3),
-            "workload": f"config 4 shapes: {S} streams, contexts {int(lens.min()) + 1}..{int(lens.max()) + 1} "
+            "workload": f"{label}: {S} streams, contexts {int(lens.min()) + 1}..{int(lens.max()) + 1} "
                         f"(mean {float(lens.mean()) + 1:.0f}), one layer's decode-step attention per launch pair"}
 
 
@@ -390,6 +391,10 @@ def main():
     log(f"config-4 multi-stream attention: {roof4['avg_launch_us']:.1f} us per layer, {roof4['achieved']:.0f} GB/s "
         f"({100 * roof4['frac']:.1f}% of peak)")
 
+    roof4k = multistream_roofline(qa, model.cfg, max(2, args.roofline_reps // 4), lens=[4095] * 32,
+                                  label="32 streams at 4k context")
+    log(f"32 streams at 4k: {roof4k['avg_launch_us']:.1f} us per layer, {roof4k['achieved']:.0f} GB/s "
+        f"({100 * roof4k['frac']:.1f}% of peak)")
     ms4 = multistream_decode(qa, model, args.multistream_steps)
     log(f"config-4 decode, {ms4['streams']} streams: {ms4['ms_per_step']:.2f} ms per step, {ms4['tok_s']:.0f} tok/s")
 
@@ -420,6 +425,7 @@ def main():
                                "decode_values_kernel, launched back to back",
                      "bytes_per_launch": attn_bytes, "attended_positions": L, "avg_launch_us": round(attn_us, 3)},
         "roofline_multistream": roof4,
+        "roofline_multistream_4k": roof4k,
         "multistream_decode": ms4,
         "attn_us_per_layer": round(attn_us, 3),
         "prefill_ms": round(prefill_ms, 2),

@@ -406,8 +406,9 @@ GemmRowsPlan gemm_rows_plan(int32_t N, int32_t K, int32_t rows) {
     GemmRowsPlan pl{};
     pl.tiles = (N + kGrTile - 1) / kGrTile;
     const int rows_pad = (rows + 15) / 16 * 16;
-    // ~512 workgroups, and the X slice of every token (padded row stride) within the LDS budget
-    int ks = std::max(1, std::min((512 + pl.tiles - 1) / pl.tiles, K / 32));
+    // ~512 workgroups but at most 8 slices (the merge then takes one round of loads), and the X slice of
+    // every token (padded row stride) within the LDS budget
+    int ks = std::max(1, std::min(std::min((512 + pl.tiles - 1) / pl.tiles, 8), K / 32));
     for (;; ++ks) {
         pl.slice = ((K + ks - 1) / ks + 31) / 32 * 32;
         if (static_cast<size_t>(rows_pad) * (pl.slice + 4) * sizeof(float) <= kGrLdsBytes || pl.slice == 32) break;

@@ -300,6 +300,9 @@ def multistream_decode(qa, model, steps: int):
         for s_ in range(w.streams):
             dec.set_cur_len(s_, int(lens[s_]))
         ids = dec.decode_streams(first, 2)                  # warm
+        bad = [(k, s_, int(ids[k, s_])) for k in range(ids.shape[0]) for s_ in range(ids.shape[1])
+               if not 0 <= int(ids[k, s_]) < model.cfg.vocab]
+        assert not bad, f"config-4 warm-up produced invalid ids (step, stream, id): {bad[:8]}"
         qa.check(qa.lib.qa_device_synchronize())
         t0 = time.perf_counter()
         dec.decode_streams(ids[-1].astype(np.int32), steps)

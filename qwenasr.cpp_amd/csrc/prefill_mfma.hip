@@ -26,11 +26,10 @@
 // e of lane group j is mapped to key (e / 4) * 16 + j * 4 + e % 4 of the 32-key step, which is
 // exactly the set of keys that lane already holds; V^T is read from LDS with the same mapping.
 //
-// LDS: two buffers of the K tile (row-major, 136-half rows) and of V^T (dims x keys, 72-half rows):
-// one barrier per tile; the next tile's global loads are in registers while the current one is
-// computed.  Strides: 16 lanes of a 16-byte K read cover 64 distinct banks; the 8-byte V^T reads and
-// writes of 32 lanes cover 64 distinct banks (V^T is written as 4 keys x 1 dim per 8-byte store,
-// transposed in registers from 4 rows of 8 dims).
+// LDS: two buffers of the K tile (row-major, 144-half rows) and of V^T (dims x keys in PV order,
+// 80-half rows): one barrier per tile; the next tile's global loads are in registers while the current
+// one is computed.  Both operands are read as 16-byte rows at conflict-free strides.  V^T is written as
+// 4 keys x 1 dim per 8-byte store, transposed in registers from 4 rows of 8 dims.
 // Block mapping: blockIdx.x = (n_qt - 1 - tile) * n_kv + kv_head, so consecutive workgroups (dispatched
 // round-robin over the 8 XCDs) are the 8 KV heads of one tile: every tile of one KV head lands on the
 // same XCD, whose L2 then holds that head's K/V (2 MB at 3913 positions) for all of its tiles; the
@@ -49,8 +48,11 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBQ = 64;     // query tokens per workgroup
 constexpr int kBK = 64;     // keys per tile
-constexpr int kKS = 136;    // K tile row stride (halfs)
-constexpr int kVS = 72;     // V^T tile row stride (halfs)
+// Row strides: a 16-byte LDS read by 16 lanes of consecutive rows is conflict-free on gfx950 when the
+// stride in dwords is 8 mod 16 (measured: 80, 112, 144 halfs conflict-free; 72, 88, 96, 136 halfs
+// lose ~half the LDS cycles to bank conflicts).
+constexpr int kKS = 144;    // K tile row stride (halfs): 128 dims + 16
+constexpr int kVS = 80;     // V^T tile row stride (halfs): 64 keys + 16
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct MfmaParams {
@@ -103,13 +105,17 @@ __device__ inline void store_tile(const TileRegs & r, _Float16 * sK, _Float16 * 
     }
     if (!with_v) return;
     const int kq = t & 15, dg = t >> 4;
+    // V^T columns are keys in PV order: key j sits at column (j / 32) * 32 + ((j % 16) / 4) * 8 +
+    // ((j / 16) % 2) * 4 + j % 4, so the 8 keys one lane multiplies in a 32-key step (4 from each 16-key
+    // block) are 8 consecutive halfs: one 16-byte read.  Keys 4 kq .. 4 kq + 3 stay adjacent.
+    const int col = (kq >> 3) * 32 + (kq & 3) * 8 + ((kq >> 2) & 1) * 4;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
         // dims 2w and 2w + 1 of the slice, keys 4 kq .. 4 kq + 3
         const uint2 even = make_uint2(lo_pair(r.v[0][w], r.v[1][w]), lo_pair(r.v[2][w], r.v[3][w]));
         const uint2 odd = make_uint2(hi_pair(r.v[0][w], r.v[1][w]), hi_pair(r.v[2][w], r.v[3][w]));
-        *reinterpret_cast<uint2 *>(sV + (dg * 8 + 2 * w) * kVS + kq * 4) = even;
-        *reinterpret_cast<uint2 *>(sV + (dg * 8 + 2 * w + 1) * kVS + kq * 4) = odd;
+        *reinterpret_cast<uint2 *>(sV + (dg * 8 + 2 * w) * kVS + col) = even;
+        *reinterpret_cast<uint2 *>(sV + (dg * 8 + 2 * w + 1) * kVS + col) = odd;
     }
 }
 
@@ -190,10 +196,7 @@ __device__ inline void pv_tile(const f4 (&S)[4][2], const _Float16 * sV, const f
     for (int ksv = 0; ksv < 2; ++ksv) {
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
-            const _Float16 * vr = sV + (db * 16 + c16) * kVS + (2 * ksv) * 16 + g4 * 4;
-            const h4 lo = *reinterpret_cast<const h4 *>(vr);
-            const h4 hi = *reinterpret_cast<const h4 *>(vr + 16);
-            const h8 a = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            const h8 a = *reinterpret_cast<const h8 *>(sV + (db * 16 + c16) * kVS + ksv * 32 + g4 * 8);
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb) {
                 O[db][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pf[cb][ksv], O[db][cb], 0, 0, 0);

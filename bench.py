@@ -204,6 +204,19 @@ def multistream_roofline(qa, cfg, reps: int, lens=None, label: str = "config 4 s
 
 
 def kernel_only(which: str, reps: int):
+    """One hot-path kernel on synthetic inputs at the config-3 shape, for rocprofv3 passes (the counters
+    of every dispatch are then the kernel's alone).  append: the prefill K/V append of 3913 positions
+    (q/k norm + RoPE, f16 cache write); prefill: causal prefill attention over 3913 positions of one
+    layer (f16 cache, n_past 0); decode-attn: the decode-step attention of one layer at L = 4186,
+    rotating 28 layer caches; multistream: the config-4 decode step of 32 streams (end to end);
+    multistream-attn: the decode-step attention of 32 streams at L = 4096 (reps x 28 launch pairs)."""
+    if which == "multistream-attn":
+        import qwenasr_amd as qa
+
+        cfg = qa.QWEN3_ASR_1_7B.config()
+        r = multistream_roofline(qa, cfg, reps, lens=[4095] * 32, label="32 streams at 4k context")
+        print(json.dumps(dict(kernel=which, **r)), flush=True)
+        return
     if which == "multistream":
         import qwenasr_amd as qa
         from qwenasr_amd import configs
@@ -212,11 +225,6 @@ def kernel_only(which: str, reps: int):
         model = qa.Model(w.size, n_layers=w.n_layers)
         print(json.dumps(dict(kernel=which, **multistream_decode(qa, model, reps))), flush=True)
         return
-    """One hot-path kernel on synthetic inputs at the config-3 shape, for rocprofv3 passes (the counters
-    of every dispatch are then the kernel's alone).  append: the prefill K/V append of 3913 positions
-    (q/k norm + RoPE, f16 cache write); prefill: causal prefill attention over 3913 positions of one
-    layer (f16 cache, n_past 0); decode-attn: the decode-step attention of one layer at L = 4186,
-    rotating 28 layer caches; multistream: the config-4 decode step of 32 streams (end to end)."""
     import ctypes as C
 
     import numpy as np
@@ -305,11 +313,18 @@ def multistream_decode(qa, model, steps: int):
         assert not bad, f"config-4 warm-up produced invalid ids (step, stream, id): {bad[:8]}"
         qa.check(qa.lib.qa_device_synchronize())
         t0 = time.perf_counter()
-        dec.decode_streams(ids[-1].astype(np.int32), steps)
+        last = dec.decode_streams(ids[-1].astype(np.int32), steps)
         qa.check(qa.lib.qa_device_synchronize())
         dt = time.perf_counter() - t0
+        # where a step's device time goes (HIP events around each kernel family, outside the timed steps)
+        n_prof = 4
+        dec.profile(True)
+        dec.profile_reset()
+        dec.decode_streams(last[-1].astype(np.int32), n_prof)
+        fam = {f: round(dec.profile_read(f)[0] / n_prof, 3) for f in ("decode_attn", "projections", "logits")}
+        dec.profile(False)
     return {"streams": w.streams, "steps": steps, "ms_per_step": round(dt * 1e3 / steps, 3),
-            "tok_s": round(w.streams * steps / dt, 1),
+            "tok_s": round(w.streams * steps / dt, 1), "family_ms_per_step": fam,
             "workload": f"config 4: {w.streams} streams, contexts {int(lens.min())}..{int(lens.max())} + {steps + 2}, "
                         f"lock-step greedy decode, f16 cache, f32 weights"}
 
@@ -327,7 +342,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 10 times (reference for HBM traffic counters)")
-    ap.add_argument("--kernel", choices=["append", "prefill", "decode-attn", "multistream"],
+    ap.add_argument("--kernel", choices=["append", "prefill", "decode-attn", "multistream", "multistream-attn"],
                     help="only run one hot-path kernel on synthetic inputs (short program for rocprofv3 passes)")
     ap.add_argument("--kernel-reps", type=int, default=20)
     args = ap.parse_args()
@@ -399,7 +414,8 @@ def main():
     log(f"32 streams at 4k: {roof4k['avg_launch_us']:.1f} us per layer, {roof4k['achieved']:.0f} GB/s "
         f"({100 * roof4k['frac']:.1f}% of peak)")
     ms4 = multistream_decode(qa, model, args.multistream_steps)
-    log(f"config-4 decode, {ms4['streams']} streams: {ms4['ms_per_step']:.2f} ms per step, {ms4['tok_s']:.0f} tok/s")
+    log(f"config-4 decode, {ms4['streams']} streams: {ms4['ms_per_step']:.2f} ms per step, {ms4['tok_s']:.0f} tok/s "
+        f"(device ms per step by family: {ms4['family_ms_per_step']})")
 
     traffic, traffic_note = measured_traffic(attn_bytes)
     weight_bytes = int(4 * sum(model.tensor(n).size for n in (

@@ -116,7 +116,11 @@ Workspace workspace_layout(int32_t n_streams, int32_t n_kv, int32_t max_seq) {
 }
 
 // 8 consecutive elements of a cache row: raw bits are loaded first (all loads in flight), converted
-// to f32 when used.
+// to f32 when used.  Cache rows are read once per call, so they are loaded with the streaming
+// (nontemporal) policy: they do not evict the scores, statistics and partials that the kernels write,
+// which then stay in L2 until the end of the kernel instead of being written back between the reads
+// (a microbenchmark of 32 KB one-shot workgroups: 6.35 -> 6.79 TB/s reading, 5.82 -> 6.41 TB/s with a
+// 1 KB write per workgroup).
 template <typename CT>
 struct Slice;
 
@@ -124,7 +128,7 @@ template <>
 struct Slice<_Float16> {
     typedef _Float16 h8 __attribute__((ext_vector_type(8)));
     h8 x;
-    __device__ inline void load(const _Float16 * p) { x = *reinterpret_cast<const h8 *>(p); }
+    __device__ inline void load(const _Float16 * p) { x = __builtin_nontemporal_load(reinterpret_cast<const h8 *>(p)); }
     __device__ inline void zero() {
 #pragma unroll
         for (int i = 0; i < 8; ++i) x[i] = static_cast<_Float16>(0.0f);
@@ -137,8 +141,11 @@ template <>
 struct Slice<float> {
     float4 a, b;
     __device__ inline void load(const float * p) {
-        a = *reinterpret_cast<const float4 *>(p);
-        b = *reinterpret_cast<const float4 *>(p + 4);
+        typedef float f4v __attribute__((ext_vector_type(4)));
+        const f4v lo = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(p));
+        const f4v hi = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(p + 4));
+        a = make_float4(lo[0], lo[1], lo[2], lo[3]);
+        b = make_float4(hi[0], hi[1], hi[2], hi[3]);
     }
     __device__ inline void zero() {
         a = make_float4(0.f, 0.f, 0.f, 0.f);

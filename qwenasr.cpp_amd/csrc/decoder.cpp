@@ -170,7 +170,11 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
                                 : 0;
     if (rc == QA_OK && gr > 0) {
         rc = dmalloc(d->act_allocs, gr, &d->gr_ws);
-        if (rc == QA_OK && hipMemset(d->gr_ws, 0, gr) != hipSuccess) rc = fail(QA_ERR_DEVICE, "workspace clear failed");
+        // cleared on the decoder's stream (non-blocking: a null-stream memset would not be ordered before
+        // the kernels that use the counters)
+        if (rc == QA_OK && hipMemsetAsync(d->gr_ws, 0, gr, d->stream) != hipSuccess) {
+            rc = fail(QA_ERR_DEVICE, "workspace clear failed");
+        }
         if (rc == QA_OK) d->gr_ws_bytes = gr;
     }
     if (rc != QA_OK) {
@@ -485,8 +489,10 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
         d->h_ids = nullptr;
         return bail(fail(QA_ERR_ALLOC, "pinned host allocation failed"));
     }
-    if (hipMemset(d->d_lens, 0, sizeof(int32_t) * n_streams) != hipSuccess ||
-        hipMemset(d->attn_ws, 0, d->attn_ws_bytes) != hipSuccess || hipMemset(d->am_ws, 0, d->am_ws_bytes) != hipSuccess) {
+    // cleared on the decoder's own stream, ahead of every kernel that reads them
+    if (hipMemsetAsync(d->d_lens, 0, sizeof(int32_t) * n_streams, d->stream) != hipSuccess ||
+        hipMemsetAsync(d->attn_ws, 0, d->attn_ws_bytes, d->stream) != hipSuccess ||
+        hipMemsetAsync(d->am_ws, 0, d->am_ws_bytes, d->stream) != hipSuccess) {
         return bail(fail(QA_ERR_DEVICE, "workspace clear failed"));
     }
     rc = ensure_rows(d, n_streams);

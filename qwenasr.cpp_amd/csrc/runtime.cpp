@@ -97,7 +97,10 @@ extern "C" int qa_copy_device(void * dev_dst, const void * dev_src, size_t bytes
 
 extern "C" int qa_memset_device(void * dev_dst, int value, size_t bytes) {
     if (!dev_dst) return fail(QA_ERR_INVALID, "qa_memset_device: null pointer");
+    // hipMemset runs on the null stream, which work on a non-blocking stream does not wait for: finish
+    // it before returning so that every stream sees the cleared memory
     QA_HIP(hipMemset(dev_dst, value, bytes));
+    QA_HIP(hipDeviceSynchronize());
     return QA_OK;
 }
 
@@ -174,7 +177,10 @@ extern "C" int qa_kv_cache_alloc(const qa_kv_layout * l, void ** dev_cache) {
     const size_t bytes = qa_kv_cache_bytes(l);
     void * p = nullptr;
     if (hipMalloc(&p, bytes) != hipSuccess) return fail(QA_ERR_ALLOC, "failed to allocate text decoder KV-cache");
-    if (hipMemset(p, 0, bytes) != hipSuccess) {
+    // the clear runs on the null stream; decoders work on non-blocking streams that do not wait for it,
+    // so it is finished before the cache is handed out (a recycled allocation would otherwise expose
+    // stale bytes, possibly f16 NaN patterns, to the first attention calls)
+    if (hipMemset(p, 0, bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         (void)hipFree(p);
         return fail(QA_ERR_DEVICE, "failed to clear text decoder KV-cache");
     }

@@ -1,5 +1,6 @@
 """Decoder-level parity: configs 0-4 on the HIP path against the oracle's golden fixtures, greedy
 token ids identical, bookkeeping (cur_len, device lengths) bit-exact, reference error behaviour."""
+import ctypes
 import hashlib
 import json
 import os
@@ -158,6 +159,35 @@ def test_config4_ragged_streams_match_golden(qa):
             assert_greedy_match(ids[:, int(s)].tolist(), ref["ids"], ref["margins"], ref["runner_up"], f"stream {s}")
         assert dec.device_lens().tolist() == (lens + w.steps).tolist()
         assert [dec.cur_len(s) for s in range(w.streams)] == (lens + w.steps).tolist()
+
+
+def test_decoders_in_sequence_see_cleared_memory(qa):
+    """Decoders created one after another in one process, each over memory just released by a buffer
+    full of f16 NaN patterns (0xFF bytes), decode identical valid ids: the cache and workspace clears
+    complete before the decoder's own (non-blocking) stream runs its first kernel.  Lengths are set
+    without filling K/V, so every cache row read is one of the cleared zeros."""
+    from qwenasr_amd import configs
+
+    w = configs.CONFIGS[4]
+    lens = configs.cfg4_lengths(w.streams)
+    first = configs.cfg4_first_ids(w.streams).astype(np.int32)
+    model = qa.Model(w.size, n_layers=w.n_layers)
+    lay = qa.KvLayout(w.n_layers, w.streams, model.cfg.n_kv_heads, model.cfg.head_dim, w.max_seq, w.cache_type)
+    cache_bytes = int(qa.lib.qa_kv_cache_bytes(ctypes.byref(lay)))
+    runs = []
+    for rep in range(3):
+        junk = qa.DeviceArray(cache_bytes, np.uint8, zero=False)
+        qa.check(qa.lib.qa_memset_device(junk.ptr, 0xFF, junk.nbytes))
+        junk.free()
+        with qa.Decoder(model, w.streams, w.max_seq, w.cache_type) as dec:
+            for s in range(w.streams):
+                dec.set_cur_len(s, int(lens[s]))
+            ids = dec.decode_streams(first, 3)
+        assert ((ids >= 0) & (ids < model.cfg.vocab)).all(), (rep, ids[:, :8])
+        runs.append(ids)
+        print(f"decoder {rep}: ids valid", flush=True)
+    for ids in runs[1:]:
+        np.testing.assert_array_equal(ids, runs[0])
 
 
 def test_graph_replay_equals_eager(qa, monkeypatch):

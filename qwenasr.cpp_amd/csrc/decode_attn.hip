@@ -688,13 +688,13 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
     *out = s_acc[0][threadIdx.x] + s_acc[1][threadIdx.x];
 }
 
-// Positions per workgroup of each kernel.  The scores kernel has no merge, so it uses small chunks
-// (many workgroups in flight); the values kernel's chunks are the merge participants of one
-// (stream, KV head), so it uses chunks large enough to keep them at <= 16 per unit (every participant
-// increments the same counter).  The choice depends on the cache capacity only, never on a call's
-// length, so a captured decode step (grids sized by capacity) and an eager one (grids sized by the
-// longest stream) run the same tiling and produce the same bits.  QA_DECODE_CHUNK / QA_DECODE_VCHUNK
-// override the choice (tuning).
+// Positions per workgroup of each kernel.  The scores kernel has no merge; its chunk trades workgroup
+// count (dispatch and per-workgroup overhead) against the load size of one workgroup.  The values
+// kernel's chunks are the merge participants of one (stream, KV head), so it uses chunks large enough
+// to keep them at <= 16 per unit (every participant increments the same counter).  The choice
+// depends on the cache capacity only, never on a call's length, so a captured decode step (grids
+// sized by capacity) and an eager one (grids sized by the longest stream) run the same tiling and
+// produce the same bits.  QA_DECODE_CHUNK / QA_DECODE_VCHUNK override the choice (tuning).
 struct Chunks {
     int scores, values;
 };
@@ -709,8 +709,18 @@ Chunks pick_chunks(int32_t n_streams, int32_t n_kv, int32_t capacity) {
     static const int forced_s = env_chunk("QA_DECODE_CHUNK");
     static const int forced_v = env_chunk("QA_DECODE_VCHUNK");
     Chunks ch{};
-    const int64_t wg32 = static_cast<int64_t>(n_streams) * n_kv * ((capacity + 31) / 32);
-    ch.scores = forced_s && forced_s <= 128 ? forced_s : wg32 < 2048 ? 32 : wg32 < 16384 ? 64 : 128;
+    // scores: the smallest chunk that keeps the grid at about one workgroup per CU, else 128 (measured
+    // at batch 1: 32 is best up to ~1k positions, 64 at 2k, 128 from 4k on, 11.1 vs 12.2 us at 4186;
+    // 128 also for 32 streams)
+    const int64_t units = static_cast<int64_t>(n_streams) * n_kv;
+    ch.scores = 128;
+    for (int c = 32; c < 128; c *= 2) {
+        if (units * ((capacity + c - 1) / c) <= 320) {
+            ch.scores = c;
+            break;
+        }
+    }
+    if (forced_s && forced_s <= 128) ch.scores = forced_s;
     int v = 32;
     while (v < 256 && (capacity + v - 1) / v > 16) v *= 2;
     ch.values = forced_v ? forced_v : v;

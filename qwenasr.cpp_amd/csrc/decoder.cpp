@@ -67,6 +67,8 @@ struct qa_decoder {
     size_t am_ws_bytes = 0;
     void * gr_ws = nullptr;      // skinny-GEMM partials and tile counters (activation allocation)
     size_t gr_ws_bytes = 0;
+    void * pf_ws = nullptr;      // prefill attention: row statistics, split partials, merge counters
+    size_t pf_ws_bytes = 0;
     int32_t * d_ids = nullptr;
     int32_t * h_ids = nullptr;   // pinned
     float * staging = nullptr;
@@ -136,6 +138,8 @@ void free_acts(qa_decoder * d) {
     d->cap_rows = 0;
     d->gr_ws = nullptr;
     d->gr_ws_bytes = 0;
+    d->pf_ws = nullptr;
+    d->pf_ws_bytes = 0;
 }
 
 // Workspace of the skinny GEMM for the layer projections at up to `rows` token rows and the LM head at
@@ -176,6 +180,15 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
             rc = fail(QA_ERR_DEVICE, "workspace clear failed");
         }
         if (rc == QA_OK) d->gr_ws_bytes = gr;
+    }
+    // prefill attention over up to `rows` tokens (counters cleared once; every call leaves them zero)
+    const size_t pf = rows >= 2 ? qa_prefill_attn_workspace_bytes(rows, d->cfg.n_heads) : 0;
+    if (rc == QA_OK && pf > 0) {
+        rc = dmalloc(d->act_allocs, pf, &d->pf_ws);
+        if (rc == QA_OK && hipMemsetAsync(d->pf_ws, 0, pf, d->stream) != hipSuccess) {
+            rc = fail(QA_ERR_DEVICE, "workspace clear failed");
+        }
+        if (rc == QA_OK) d->pf_ws_bytes = pf;
     }
     if (rc != QA_OK) {
         free_acts(d);
@@ -257,7 +270,7 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
         }
         Prof pr(d, kFamPrefillAttn);
         rc = prefill_attn_launch(d->qrot, QD, d->cache, d->layout, l, 0, n_past, rows, c.n_heads, d->scale,
-                                 d->attn, nullptr, 0, s);
+                                 d->attn, d->pf_ws, d->pf_ws_bytes, s);
         if (rc != QA_OK) return rc;
     }
     Prof pr(d, kFamProj);

@@ -38,8 +38,10 @@ size_t decode_attn_workspace(int32_t n_streams, int32_t n_kv_heads, int32_t max_
 int prefill_attn_launch(const float * q, int32_t q_stride, const void * cache, const qa_kv_layout & layout,
                         int32_t layer, int32_t stream_idx, int32_t n_past, int32_t n_tokens, int32_t n_heads,
                         float scale, float * out, void * workspace, size_t workspace_bytes, hipStream_t stream);
+size_t prefill_mfma_workspace_bytes(int32_t n_tokens, int32_t n_kv);
 int prefill_mfma_launch(const float * q, int32_t q_stride, const void * k, const void * v, int64_t head_stride,
-                        int32_t n_past, int32_t n_tokens, int32_t n_kv, float scale, float * out, hipStream_t stream);
+                        int32_t n_past, int32_t n_tokens, int32_t n_kv, float scale, float * out, void * workspace,
+                        size_t workspace_bytes, hipStream_t stream);
 int causal_f32_launch(const float * q, int32_t q_stride, const float * k, const float * v, int64_t row_stride,
                       int32_t n_tokens, int32_t n_heads, int32_t n_kv_heads, float scale, float * out,
                       hipStream_t stream);

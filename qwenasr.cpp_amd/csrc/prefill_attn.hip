@@ -207,8 +207,6 @@ int launch_rows(const RowsParams & p, int n_kv_heads, hipStream_t stream) {
 int prefill_attn_launch(const float * q, int32_t q_stride, const void * cache, const qa_kv_layout & layout,
                         int32_t layer, int32_t stream_idx, int32_t n_past, int32_t n_tokens, int32_t n_heads,
                         float scale, float * out, void * workspace, size_t workspace_bytes, hipStream_t stream) {
-    (void)workspace;
-    (void)workspace_bytes;
     if (layout.head_dim != kHeadDim || n_heads != kRep * layout.n_kv_heads) {
         return fail(QA_ERR_INVALID, "prefill attention: only head_dim 128 with 2 query heads per KV head");
     }
@@ -224,7 +222,7 @@ int prefill_attn_launch(const float * q, int32_t q_stride, const void * cache, c
                                                     layout.max_seq);
     if (layout.cache_type == QA_CACHE_F16) {
         return prefill_mfma_launch(q, q_stride, k0, v0, static_cast<int64_t>(layout.max_seq) * kHeadDim, n_past,
-                                   n_tokens, layout.n_kv_heads, scale, out, stream);
+                                   n_tokens, layout.n_kv_heads, scale, out, workspace, workspace_bytes, stream);
     }
     if (n_past + n_tokens > kMaxRowsKeys) {
         return fail(QA_ERR_INVALID, "prefill attention: more than 8192 keys with an f32 cache");
@@ -246,9 +244,7 @@ int prefill_attn_launch(const float * q, int32_t q_stride, const void * cache, c
 }  // namespace qa
 
 extern "C" size_t qa_prefill_attn_workspace_bytes(int32_t n_tokens, int32_t n_heads) {
-    (void)n_tokens;
-    (void)n_heads;
-    return 256;
+    return qa::prefill_mfma_workspace_bytes(n_tokens, n_heads / qa::kRep);
 }
 
 extern "C" int qa_prefill_attn(const float * q, const void * cache, const qa_kv_layout * layout, int32_t layer,

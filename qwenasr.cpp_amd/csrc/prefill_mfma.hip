@@ -36,6 +36,7 @@
 // heaviest (last, causally longest) tiles start first.
 #include "ops.hpp"
 
+#include <algorithm>
 #include <cmath>
 
 namespace qa {
@@ -54,6 +55,20 @@ constexpr int kBK = 64;     // keys per tile
 constexpr int kKS = 144;    // K tile row stride (halfs): 128 dims + 16
 constexpr int kVS = 80;     // V^T tile row stride (halfs): 64 keys + 16
 constexpr float kLog2e = 1.4426950408889634f;
+// Split plan limits: a query tile is split in two only while the grid is small enough for the causal
+// imbalance to matter (n_qt * n_kv <= kPfMaxUnits, about twice the workgroups that fit at once); the
+// merge counters sit in a fixed region at the start of the workspace, 256 bytes apart.
+constexpr int kPfMaxUnits = 1024;
+constexpr int kPfCounterStride = 64;
+constexpr size_t kPfCounterBytes = static_cast<size_t>(kPfMaxUnits) * kPfCounterStride * sizeof(uint32_t);
+
+// Row statistics of one part of a query tile: max m (raw score units) and the double sum of
+// exp((s - m) * scale) over the part's keys.
+struct alignas(16) PrefillStat {
+    float m;
+    float pad;
+    double s;
+};
 
 struct MfmaParams {
     const float * q;          // [T][q_stride], token t of the call
@@ -63,8 +78,19 @@ struct MfmaParams {
     int64_t head_stride;      // elements between KV heads (max_seq * 128)
     int32_t q_stride;
     int32_t n_past, n_tokens, n_kv, n_qt;
+    int32_t split;            // key tiles of the first part of a split query tile; 0: no tile is split
+    int32_t qt_split;         // first split query tile (the tiles with more than `split` key tiles)
     float scale;
+    PrefillStat * stats;      // [n_kv][n_qt][2 parts][128 columns]
+    float * partial;          // [n_kv][n_qt - qt_split][2 parts][16][256 threads][4]
+    uint32_t * counters;      // [n_kv][n_qt - qt_split][kPfCounterStride]
 };
+
+__device__ inline uint64_t pack2(float a, float b) {
+    return static_cast<uint64_t>(__float_as_uint(a)) | (static_cast<uint64_t>(__float_as_uint(b)) << 32);
+}
+__device__ inline float lo_float(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
+__device__ inline float hi_float(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v >> 32)); }
 
 // Global -> register staging of one tile.  K: thread t loads 16-byte slices idx = it * 256 + t
 // (row idx / 16, slice idx % 16).  V: thread t loads slice dg = 4 * wave + lane / 16 of the 4 rows
@@ -205,13 +231,41 @@ __device__ inline void pv_tile(const f4 (&S)[4][2], const _Float16 * sV, const f
     }
 }
 
+// One work item: KV head g, query tile qt and key tiles [kt0, kt1).  Items 0 .. n_qt - 1 (times n_kv)
+// are the query tiles in descending order (the causally longest first) over their first part of the
+// keys; items n_qt .. are the second parts of the split query tiles (qt >= qt_split), also longest first.
+struct Item {
+    int g, qt, j, kt0, kt1, n_kt;
+    bool split;
+};
+
+__device__ inline Item item_of(const MfmaParams & p) {
+    Item it;
+    it.g = static_cast<int>(blockIdx.x) % p.n_kv;
+    const int i = static_cast<int>(blockIdx.x) / p.n_kv;
+    it.j = i < p.n_qt ? 0 : 1;
+    it.qt = p.n_qt - 1 - (i < p.n_qt ? i : i - p.n_qt);
+    const int t0 = it.qt * kBQ;
+    const int kend = min(p.n_past + p.n_tokens, p.n_past + min(t0 + kBQ, p.n_tokens));
+    it.n_kt = (kend + kBK - 1) / kBK;
+    it.split = p.split > 0 && it.qt >= p.qt_split;
+    it.kt0 = it.j == 0 ? 0 : p.split;
+    it.kt1 = it.split && it.j == 0 ? p.split : it.n_kt;
+    return it;
+}
+
+// PASS 1: the item's part of the row statistics (max and sum of exp) of its 128 query columns.
+// PASS 2: p over the item's keys with the statistics of every part of its query tile, and O^T += V^T P^T;
+// the two parts of a split tile are added by whichever finishes second.
+template <int PASS>
 __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaParams p) {
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][kBK * kKS];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[2][kHeadDim * kVS];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[PASS == 2 ? 2 : 1][PASS == 2 ? kHeadDim * kVS : 8];
+    constexpr bool kWithV = PASS == 2;
 
-    const int g = static_cast<int>(blockIdx.x) % p.n_kv;
-    const int qt = p.n_qt - 1 - static_cast<int>(blockIdx.x) / p.n_kv;
-    const int t0 = qt * kBQ;
+    const Item it = item_of(p);
+    const int g = it.g;
+    const int t0 = it.qt * kBQ;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x >> 6;
     const int hh = wave >> 1;
@@ -221,9 +275,8 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaParams p) {
     const int g4 = lane >> 4;
     const int L_total = p.n_past + p.n_tokens;
     const int kend = min(L_total, p.n_past + min(t0 + kBQ, p.n_tokens));
-    const int n_kt = (kend + kBK - 1) / kBK;
     // tiles below kt_full hold only keys <= n_past + t0, attended by every query of the workgroup
-    const int kt_full = min((p.n_past + t0 + 1) / kBK, n_kt);
+    const int kt_full = min((p.n_past + t0 + 1) / kBK, it.n_kt);
     const _Float16 * kh = p.k + g * p.head_stride;
     const _Float16 * vh = p.v + g * p.head_stride;
     const float c = p.scale * kLog2e;
@@ -235,6 +288,9 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaParams p) {
         tq[cb] = tw + cb * 16 + c16;
         lim[cb] = tq[cb] < p.n_tokens ? p.n_past + tq[cb] : -1;   // keys j <= lim are attended
     }
+    // statistics slot of query column cb of this lane: [g][qt][part][column]
+    const int col0 = hh * 64 + (wave & 1) * 32 + c16;
+    PrefillStat * st = p.stats + (static_cast<int64_t>(g) * p.n_qt + it.qt) * 2 * 128;
 
     // Q fragments, the B operand of S^T: lane holds query column c16 and 8 dims of each 32-dim step,
     // rounded to f16 (GGML's conversion of src1 for an f16 src0); absent tokens are zero
@@ -255,60 +311,113 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaParams p) {
         }
     }
 
-    // ---------------------------------------------------------------- pass 1: max and sum
-    float m[2] = {-INFINITY, -INFINITY};
-    double sum[2] = {0.0, 0.0};
-    TileRegs regs;
-    load_tile(kh, vh, 0, kend, false, regs);
-    store_tile(regs, sK[0], sV[0], false);
-    if (n_kt > 1) load_tile(kh, vh, 1, kend, false, regs);
-    __syncthreads();
-    for (int kt = 0; kt < n_kt; ++kt) {
-        f4 S[4][2];
-        scores_tile(sK[kt & 1], qf, c16, g4, S);
-        if (kt >= kt_full) mask_tile(S, lim, kt, g4);
-        stats_update(S, 0, c, m[0], sum[0]);
-        stats_update(S, 1, c, m[1], sum[1]);
-        if (kt + 1 < n_kt) {
-            store_tile(regs, sK[(kt + 1) & 1], sV[(kt + 1) & 1], false);
-            if (kt + 2 < n_kt) load_tile(kh, vh, kt + 2, kend, false, regs);
-        }
-        __syncthreads();
-    }
-    // combine the 4 lanes of each query column (lane bits 4, 5)
-    float mc[2], r[2];
+    float mc[2] = {0.f, 0.f}, r[2] = {0.f, 0.f};
+    if constexpr (PASS == 2) {
+        // row max M and sum S of every part: S = sum over parts of s_part * exp(m_part - M), in double
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-        float M = fmaxf(m[cb], __shfl_xor(m[cb], 16, kWave));
-        M = fmaxf(M, __shfl_xor(M, 32, kWave));
-        double s = M == -INFINITY ? 0.0 : sum[cb] * static_cast<double>(__builtin_amdgcn_exp2f((m[cb] - M) * c));
-        s += __shfl_xor(s, 16, kWave);
-        s += __shfl_xor(s, 32, kWave);
-        mc[cb] = M == -INFINITY ? 0.0f : M * c;
-        r[cb] = s > 0.0 ? static_cast<float>(1.0 / s) : 0.0f;
+        for (int cb = 0; cb < 2; ++cb) {
+            const int col = col0 + cb * 16;
+            const PrefillStat a = st[col];
+            float M = a.m;
+            PrefillStat b{-INFINITY, 0.f, 0.0};
+            if (it.split) {
+                b = st[128 + col];
+                M = fmaxf(M, b.m);
+            }
+            double S = 0.0;
+            if (M != -INFINITY) {
+                S = a.s * static_cast<double>(__builtin_amdgcn_exp2f((a.m - M) * c));
+                if (it.split) S += b.s * static_cast<double>(__builtin_amdgcn_exp2f((b.m - M) * c));
+            }
+            mc[cb] = M == -INFINITY ? 0.0f : M * c;
+            r[cb] = S > 0.0 ? static_cast<float>(1.0 / S) : 0.0f;
+        }
     }
 
-    // ---------------------------------------------------------------- pass 2: p and PV
+    float m[2] = {-INFINITY, -INFINITY};
+    double sum[2] = {0.0, 0.0};
     f4 O[8][2];
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) O[db][cb] = f4{0.f, 0.f, 0.f, 0.f};
     }
-    load_tile(kh, vh, 0, kend, true, regs);
-    store_tile(regs, sK[0], sV[0], true);
-    if (n_kt > 1) load_tile(kh, vh, 1, kend, true, regs);
+    TileRegs regs;
+    const int kt0 = it.kt0, kt1 = it.kt1;
+    load_tile(kh, vh, kt0, kend, kWithV, regs);
+    store_tile(regs, sK[0], sV[0], kWithV);
+    if (kt0 + 1 < kt1) load_tile(kh, vh, kt0 + 1, kend, kWithV, regs);
     __syncthreads();
-    for (int kt = 0; kt < n_kt; ++kt) {
+    for (int kt = kt0; kt < kt1; ++kt) {
+        const int b = (kt - kt0) & 1;
         f4 S[4][2];
-        scores_tile(sK[kt & 1], qf, c16, g4, S);
+        scores_tile(sK[b], qf, c16, g4, S);
         if (kt >= kt_full) mask_tile(S, lim, kt, g4);
-        pv_tile(S, sV[kt & 1], mc, r, c, c16, g4, O);
-        if (kt + 1 < n_kt) {
-            store_tile(regs, sK[(kt + 1) & 1], sV[(kt + 1) & 1], true);
-            if (kt + 2 < n_kt) load_tile(kh, vh, kt + 2, kend, true, regs);
+        if constexpr (PASS == 1) {
+            stats_update(S, 0, c, m[0], sum[0]);
+            stats_update(S, 1, c, m[1], sum[1]);
+        } else {
+            pv_tile(S, sV[b], mc, r, c, c16, g4, O);
+        }
+        if (kt + 1 < kt1) {
+            store_tile(regs, sK[b ^ 1], sV[PASS == 2 ? (b ^ 1) : 0], kWithV);
+            if (kt + 2 < kt1) load_tile(kh, vh, kt + 2, kend, kWithV, regs);
         }
         __syncthreads();
+    }
+
+    if constexpr (PASS == 1) {
+        // combine the 4 lanes of each query column (lane bits 4, 5) and store the part's statistics
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            float M = fmaxf(m[cb], __shfl_xor(m[cb], 16, kWave));
+            M = fmaxf(M, __shfl_xor(M, 32, kWave));
+            double s = M == -INFINITY ? 0.0 : sum[cb] * static_cast<double>(__builtin_amdgcn_exp2f((m[cb] - M) * c));
+            s += __shfl_xor(s, 16, kWave);
+            s += __shfl_xor(s, 32, kWave);
+            if (g4 == 0) st[it.j * 128 + col0 + cb * 16] = PrefillStat{M, 0.0f, s};
+        }
+        return;
+    }
+
+    if (it.split) {
+        // Publish this part's O (thread-major: element i of every thread is 256 consecutive float4), then
+        // count; the second part to arrive adds the first's O to its own.  With two addends the sum is the
+        // same whichever part arrives second.
+        const int64_t unit = static_cast<int64_t>(g) * (p.n_qt - p.qt_split) + (it.qt - p.qt_split);
+        uint64_t * mine = reinterpret_cast<uint64_t *>(p.partial) + (unit * 2 + it.j) * (16 * 256 * 2);
+        const uint64_t * other = reinterpret_cast<const uint64_t *>(p.partial) + (unit * 2 + (it.j ^ 1)) * (16 * 256 * 2);
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                const int e = ((db * 2 + cb) * 256 + static_cast<int>(threadIdx.x)) * 2;
+                const f4 o = O[db][cb];
+                __hip_atomic_store(mine + e, pack2(o[0], o[1]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(mine + e + 1, pack2(o[2], o[3]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        __shared__ int s_last;
+        if (threadIdx.x == 0) {
+            uint32_t * ctr = p.counters + unit * kPfCounterStride;
+            const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = prev == 1u;
+            if (s_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!s_last) return;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                const int e = ((db * 2 + cb) * 256 + static_cast<int>(threadIdx.x)) * 2;
+                const uint64_t lo = __hip_atomic_load(other + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t hi = __hip_atomic_load(other + e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                O[db][cb] += f4{lo_float(lo), hi_float(lo), lo_float(hi), hi_float(hi)};
+            }
+        }
     }
 
     // O^T: lane holds dims db * 16 + g4 * 4 + i of query column c16 of block cb
@@ -325,8 +434,19 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaParams p) {
 
 }  // namespace
 
+// Workspace: merge counters (fixed region), the statistics of two parts per (KV head, query tile), and
+// two partial O per (KV head, query tile) when the grid is small enough to be split.
+size_t prefill_mfma_workspace_bytes(int32_t n_tokens, int32_t n_kv) {
+    if (n_tokens <= 0 || n_kv <= 0) return 256;
+    const int64_t units = (static_cast<int64_t>(n_tokens) + kBQ - 1) / kBQ * n_kv;
+    const size_t stats = static_cast<size_t>(units) * 2 * 128 * sizeof(PrefillStat);
+    const size_t partials = units <= kPfMaxUnits ? static_cast<size_t>(units) * 2 * 16 * 256 * 4 * sizeof(float) : 0;
+    return kPfCounterBytes + stats + partials;
+}
+
 int prefill_mfma_launch(const float * q, int32_t q_stride, const void * k, const void * v, int64_t head_stride,
-                        int32_t n_past, int32_t n_tokens, int32_t n_kv, float scale, float * out, hipStream_t stream) {
+                        int32_t n_past, int32_t n_tokens, int32_t n_kv, float scale, float * out, void * workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
     MfmaParams p{};
     p.q = q;
     p.k = static_cast<const _Float16 *>(k);
@@ -339,10 +459,40 @@ int prefill_mfma_launch(const float * q, int32_t q_stride, const void * k, const
     p.n_kv = n_kv;
     p.n_qt = (n_tokens + kBQ - 1) / kBQ;
     p.scale = scale;
-    const int64_t blocks = static_cast<int64_t>(p.n_qt) * n_kv;
-    if (blocks <= 0) return QA_OK;
-    hipLaunchKernelGGL(prefill_mfma_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, p);
-    QA_LAUNCH_CHECK("prefill_mfma_kernel");
+    if (static_cast<int64_t>(p.n_qt) * n_kv <= 0) return QA_OK;
+    // Split plan.  The query tile qt attends key tiles [0, n_kt(qt)); the longest has n_kt_max.  With the
+    // whole grid resident at once, the kernel lasts as long as its longest tile, about twice the average:
+    // the tiles with more than ceil(n_kt_max / 2) key tiles are therefore split into two parts of at most
+    // that many, computed by separate workgroups.  The plan needs the workspace (statistics, partials,
+    // counters); without it, or for grids large enough to balance themselves, no tile is split.
+    const int n_kt_max = (n_past + n_tokens + kBK - 1) / kBK;
+    const int64_t units = static_cast<int64_t>(p.n_qt) * n_kv;
+    p.split = 0;
+    p.qt_split = p.n_qt;
+    if (units <= kPfMaxUnits && n_kt_max >= 2 && workspace &&
+        workspace_bytes >= prefill_mfma_workspace_bytes(n_tokens, n_kv)) {
+        p.split = (n_kt_max + 1) / 2;
+        int qt = 0;
+        while (qt < p.n_qt && (n_past + std::min((qt + 1) * kBQ, n_tokens) + kBK - 1) / kBK <= p.split) ++qt;
+        p.qt_split = qt;
+        char * base = static_cast<char *>(workspace);
+        p.counters = reinterpret_cast<uint32_t *>(base);
+        p.stats = reinterpret_cast<PrefillStat *>(base + kPfCounterBytes);
+        p.partial = reinterpret_cast<float *>(base + kPfCounterBytes + static_cast<size_t>(units) * 2 * 128 *
+                                                                           sizeof(PrefillStat));
+    } else {
+        // unsplit: the statistics still pass through memory between the two kernels
+        if (!workspace || workspace_bytes < kPfCounterBytes + static_cast<size_t>(units) * 2 * 128 * sizeof(PrefillStat)) {
+            return fail(QA_ERR_INVALID, "prefill attention: workspace too small (qa_prefill_attn_workspace_bytes)");
+        }
+        p.stats = reinterpret_cast<PrefillStat *>(static_cast<char *>(workspace) + kPfCounterBytes);
+    }
+    const int64_t items = p.n_qt + (p.n_qt - p.qt_split);
+    const dim3 grid(static_cast<unsigned>(items * n_kv));
+    hipLaunchKernelGGL(prefill_mfma_kernel<1>, grid, dim3(256), 0, stream, p);
+    QA_LAUNCH_CHECK("prefill_mfma_kernel<1>");
+    hipLaunchKernelGGL(prefill_mfma_kernel<2>, grid, dim3(256), 0, stream, p);
+    QA_LAUNCH_CHECK("prefill_mfma_kernel<2>");
     return QA_OK;
 }
 

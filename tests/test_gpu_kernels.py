@@ -274,6 +274,72 @@ def test_prefill_attention(qa, orc, f16, n_past, T):
     check_close(got[t], dec)
 
 
+def test_prefill_attention_long_split_rows(qa, orc):
+    """Config-3 prefill shape (T = 3913, f16 cache): the longest query tiles are split over two
+    workgroups and merged.  Sampled rows, in split and unsplit tiles, equal a decode over their prefix."""
+    T = 3913
+    lay = layout(qa, 1, 1, T + 3, True)
+    cache = Cache(qa, lay)
+    rng = np.random.default_rng(T)
+    k, v = cache.fill(rng, 0, [T])[0]
+    q = rng.standard_normal((T, 16, 128)).astype(np.float32)
+    d_q, d_out = dev(qa, q), zeros(qa, (T, 2048))
+    ws_bytes = qa.lib.qa_prefill_attn_workspace_bytes(T, 16)
+    ws = zeros(qa, ws_bytes, np.uint8)
+    print(f"prefill split T={T}", flush=True)
+    qa.check(qa.lib.qa_prefill_attn(d_q.ptr, cache.ptr, C.byref(lay), 0, 0, 0, T, 16, SCALE, d_out.ptr, ws.ptr,
+                                    ws_bytes, NULL_STREAM))
+    qa.synchronize()
+    got = d_out.numpy().reshape(T, 16, 128)
+    for t in (0, 63, 64, 1000, 1983, 1984, 2047, 2048, 3000, 3840, 3841, 3912):
+        ref = orc.cache_attention(k[:, :t + 1], v[:, :t + 1], q[t:t + 1], t, True)[0]
+        check_close(got[t], ref)
+
+
+@pytest.mark.parametrize("n_past,T", [(0, 700), (300, 500)])
+def test_prefill_split_and_unsplit_agree(qa, orc, n_past, T):
+    """The split plan (full workspace) and the unsplit one (a workspace with room for the statistics
+    only) both match the oracle; repeated calls sharing one workspace, with other shapes in between,
+    give identical bits (the merge counters return to zero)."""
+    L = n_past + T
+    lay = layout(qa, 1, 1, L + 3, True)
+    cache = Cache(qa, lay)
+    rng = np.random.default_rng(L + 7)
+    k, v = cache.fill(rng, 0, [L])[0]
+    q = rng.standard_normal((T, 16, 128)).astype(np.float32)
+    d_q = dev(qa, q)
+    full = qa.lib.qa_prefill_attn_workspace_bytes(T, 16)
+    n_units = (T + 63) // 64 * 8
+    small = 1024 * 256 + n_units * 2 * 128 * 16       # counters + statistics, no partials
+    assert small < full
+    ws = zeros(qa, full, np.uint8)
+    ref = orc.cache_attention(k, v, q, n_past, True)
+    outs = {}
+    for label, nbytes in (("split", full), ("unsplit", small), ("split again", full)):
+        d_out = zeros(qa, (T, 2048))
+        print(f"prefill {label} n_past={n_past} T={T}", flush=True)
+        qa.check(qa.lib.qa_prefill_attn(d_q.ptr, cache.ptr, C.byref(lay), 0, 0, n_past, T, 16, SCALE, d_out.ptr,
+                                        ws.ptr, nbytes, NULL_STREAM))
+        # another shape on the same workspace in between
+        d_o2 = zeros(qa, (37, 2048))
+        qa.check(qa.lib.qa_prefill_attn(d_q.ptr, cache.ptr, C.byref(lay), 0, 0, 5, 37, 16, SCALE, d_o2.ptr,
+                                        ws.ptr, full, NULL_STREAM))
+        qa.synchronize()
+        outs[label] = d_out.numpy().reshape(T, 16, 128)
+        check_close(outs[label], ref)
+    np.testing.assert_array_equal(outs["split"].view(np.uint32), outs["split again"].view(np.uint32))
+    assert not (ws.numpy()[:1024 * 256].view(np.uint32)).any(), "merge counters not reset"
+
+
+def test_prefill_rejects_missing_workspace(qa):
+    lay = layout(qa, 1, 1, 70, True)
+    cache = Cache(qa, lay)
+    d_q, d_out = zeros(qa, (64, 2048)), zeros(qa, (64, 2048))
+    rc = qa.lib.qa_prefill_attn(d_q.ptr, cache.ptr, C.byref(lay), 0, 0, 0, 64, 16, SCALE, d_out.ptr, None, 0,
+                                NULL_STREAM)
+    assert rc != 0
+
+
 @pytest.mark.parametrize("T", [1, 45, 300])
 def test_causal_attention_f32(qa, orc, T):
     rng = np.random.default_rng(T)

@@ -30,10 +30,9 @@
 // 80-half rows): one barrier per tile; the next tile's global loads are in registers while the current
 // one is computed.  Both operands are read as 16-byte rows at conflict-free strides.  V^T is written as
 // 4 keys x 1 dim per 8-byte store, transposed in registers from 4 rows of 8 dims.
-// Block mapping: blockIdx.x = (n_qt - 1 - tile) * n_kv + kv_head, so consecutive workgroups (dispatched
-// round-robin over the 8 XCDs) are the 8 KV heads of one tile: every tile of one KV head lands on the
-// same XCD, whose L2 then holds that head's K/V (2 MB at 3913 positions) for all of its tiles; the
-// heaviest (last, causally longest) tiles start first.
+// Work distribution: the two passes are separate kernels over the same work items (parts of the key
+// range of one query tile and KV head), pulled from a queue in descending order of query tile by a grid
+// that fits on the GPU at once; the 8 KV heads of one item are consecutive pulls.
 #include "ops.hpp"
 
 #include <algorithm>
@@ -55,15 +54,21 @@ constexpr int kBK = 64;     // keys per tile
 constexpr int kKS = 144;    // K tile row stride (halfs): 128 dims + 16
 constexpr int kVS = 80;     // V^T tile row stride (halfs): 64 keys + 16
 constexpr float kLog2e = 1.4426950408889634f;
-// Split plan limits: a query tile is split in two only while the grid is small enough for the causal
-// imbalance to matter (n_qt * n_kv <= kPfMaxUnits, about twice the workgroups that fit at once); the
-// merge counters sit in a fixed region at the start of the workspace, 256 bytes apart.
-constexpr int kPfMaxUnits = 1024;
-constexpr int kPfCounterStride = 64;
-constexpr size_t kPfCounterBytes = static_cast<size_t>(kPfMaxUnits) * kPfCounterStride * sizeof(uint32_t);
+// Work plan.  Query tile qt attends key tiles [0, n_kt(qt)).  A tile with more than cap =
+// ceil(n_kt_last / 2) key tiles is cut at key tile cap into two parts; every part (or uncut tile) is
+// one work item.  Items are pulled from a queue per KV head by a grid that fits on the GPU at once, in
+// about descending order of size (see item_of), so that every CU stays busy until the end: a grid of
+// one workgroup per query tile lasts as long as the longest tile, about twice the average.
+// Workspace: a fixed region (queue and merge counters) first, so that calls of any shape can share one
+// workspace, then the statistics of every item and the partial outputs of the cut tiles.
+constexpr int kPfCounterStride = 64;    // uint32 (256 bytes) per counter
+constexpr int kPfMaxHeads = 8;          // KV heads (one queue each per pass)
+constexpr int kPfMaxMerge = 8192;       // merge counters: one per (KV head, query tile)
+constexpr int kPfCutUnits = 2048;       // (KV head, query tile) units up to which long tiles are cut
+constexpr size_t kPfQueueBytes = 2 * kPfMaxHeads * kPfCounterStride * sizeof(uint32_t);
+constexpr size_t kPfFixedBytes = kPfQueueBytes + static_cast<size_t>(kPfMaxMerge) * kPfCounterStride * sizeof(uint32_t);
+constexpr size_t kPfPartialFloats = 16 * 256 * 4;   // one part's O: 16 float4 per thread
 
-// Row statistics of one part of a query tile: max m (raw score units) and the double sum of
-// exp((s - m) * scale) over the part's keys.
 struct alignas(16) PrefillStat {
     float m;
     float pad;
@@ -78,12 +83,14 @@ struct MfmaParams {
     int64_t head_stride;      // elements between KV heads (max_seq * 128)
     int32_t q_stride;
     int32_t n_past, n_tokens, n_kv, n_qt;
-    int32_t split;            // key tiles of the first part of a split query tile; 0: no tile is split
-    int32_t qt_split;         // first split query tile (the tiles with more than `split` key tiles)
+    int32_t cap;              // key tiles of the first part of a cut query tile
+    int32_t qt_cut;           // first cut query tile (n_kt > cap); n_qt when none is cut
+    int32_t n_items;          // work items per KV head: n_qt + (n_qt - qt_cut)
     float scale;
+    uint32_t * queue;         // pull counters of this pass, one per KV head (every call leaves them zero)
     PrefillStat * stats;      // [n_kv][n_qt][2 parts][128 columns]
-    float * partial;          // [n_kv][n_qt - qt_split][2 parts][16][256 threads][4]
-    uint32_t * counters;      // [n_kv][n_qt - qt_split][kPfCounterStride]
+    float * partial;          // [n_kv][n_qt - qt_cut][2 parts][kPfPartialFloats]
+    uint32_t * counters;      // [n_kv][n_qt - qt_cut][kPfCounterStride]
 };
 
 __device__ inline uint64_t pack2(float a, float b) {
@@ -231,39 +238,53 @@ __device__ inline void pv_tile(const f4 (&S)[4][2], const _Float16 * sV, const f
     }
 }
 
-// One work item: KV head g, query tile qt and key tiles [kt0, kt1).  Items 0 .. n_qt - 1 (times n_kv)
-// are the query tiles in descending order (the causally longest first) over their first part of the
-// keys; items n_qt .. are the second parts of the split query tiles (qt >= qt_split), also longest first.
+// One work item: KV head g, part j of query tile qt, key tiles [kt0, kt1); cut says whether qt has
+// two parts.  Item order per head (k = 0, 1, ...): first the first parts of the cut tiles (cap key
+// tiles each, longest query tile first), then the uncut tiles and the second parts alternately, both
+// in descending order of size: about the order a longest-first scheduler would pick.
 struct Item {
     int g, qt, j, kt0, kt1, n_kt;
-    bool split;
+    bool cut;
 };
 
-__device__ inline Item item_of(const MfmaParams & p) {
+__device__ inline Item item_of(const MfmaParams & p, int g, int k) {
     Item it;
-    it.g = static_cast<int>(blockIdx.x) % p.n_kv;
-    const int i = static_cast<int>(blockIdx.x) / p.n_kv;
-    it.j = i < p.n_qt ? 0 : 1;
-    it.qt = p.n_qt - 1 - (i < p.n_qt ? i : i - p.n_qt);
+    it.g = g;
+    const int n_cut = p.n_qt - p.qt_cut;          // cut tiles = second parts
+    const int n_whole = p.qt_cut;                  // uncut tiles
+    if (k < n_cut) {
+        it.qt = p.n_qt - 1 - k;
+        it.j = 0;
+    } else {
+        const int m = k - n_cut;
+        const int both = 2 * min(n_cut, n_whole);
+        int i;
+        bool second;
+        if (m < both) {
+            i = m >> 1;
+            second = (m & 1) != 0;
+        } else {
+            i = m - both + min(n_cut, n_whole);
+            second = n_cut > n_whole;
+        }
+        it.qt = second ? p.n_qt - 1 - i : p.qt_cut - 1 - i;
+        it.j = second ? 1 : 0;
+    }
     const int t0 = it.qt * kBQ;
-    const int kend = min(p.n_past + p.n_tokens, p.n_past + min(t0 + kBQ, p.n_tokens));
-    it.n_kt = (kend + kBK - 1) / kBK;
-    it.split = p.split > 0 && it.qt >= p.qt_split;
-    it.kt0 = it.j == 0 ? 0 : p.split;
-    it.kt1 = it.split && it.j == 0 ? p.split : it.n_kt;
+    it.n_kt = (min(p.n_past + p.n_tokens, p.n_past + min(t0 + kBQ, p.n_tokens)) + kBK - 1) / kBK;
+    it.cut = it.qt >= p.qt_cut;
+    it.kt0 = it.j == 0 ? 0 : p.cap;
+    it.kt1 = it.cut && it.j == 0 ? p.cap : it.n_kt;
     return it;
 }
 
-// PASS 1: the item's part of the row statistics (max and sum of exp) of its 128 query columns.
-// PASS 2: p over the item's keys with the statistics of every part of its query tile, and O^T += V^T P^T;
-// the two parts of a split tile are added by whichever finishes second.
+// One work item.  PASS 1: the part's row statistics (max and sum of exp) of its 128 query columns.
+// PASS 2: p over the part's keys with the statistics of both parts of its query tile, and
+// O^T += V^T P^T; the two parts of a cut tile are added by whichever finishes second.
 template <int PASS>
-__global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaParams p) {
-    __shared__ __attribute__((aligned(16))) _Float16 sK[2][kBK * kKS];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[PASS == 2 ? 2 : 1][PASS == 2 ? kHeadDim * kVS : 8];
+__device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 (*sK)[kBK * kKS],
+                                _Float16 (*sV)[kHeadDim * kVS]) {
     constexpr bool kWithV = PASS == 2;
-
-    const Item it = item_of(p);
     const int g = it.g;
     const int t0 = it.qt * kBQ;
     const int lane = threadIdx.x & (kWave - 1);
@@ -288,7 +309,7 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaParams p) {
         tq[cb] = tw + cb * 16 + c16;
         lim[cb] = tq[cb] < p.n_tokens ? p.n_past + tq[cb] : -1;   // keys j <= lim are attended
     }
-    // statistics slot of query column cb of this lane: [g][qt][part][column]
+    // statistics of part j of this query tile: [g][qt][j][column]
     const int col0 = hh * 64 + (wave & 1) * 32 + c16;
     PrefillStat * st = p.stats + (static_cast<int64_t>(g) * p.n_qt + it.qt) * 2 * 128;
 
@@ -313,21 +334,18 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaParams p) {
 
     float mc[2] = {0.f, 0.f}, r[2] = {0.f, 0.f};
     if constexpr (PASS == 2) {
-        // row max M and sum S of every part: S = sum over parts of s_part * exp(m_part - M), in double
+        // row max M and sum S over the parts: S = s_0 exp(m_0 - M) + s_1 exp(m_1 - M), in double
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
             const int col = col0 + cb * 16;
             const PrefillStat a = st[col];
-            float M = a.m;
             PrefillStat b{-INFINITY, 0.f, 0.0};
-            if (it.split) {
-                b = st[128 + col];
-                M = fmaxf(M, b.m);
-            }
+            if (it.cut) b = st[128 + col];
+            const float M = fmaxf(a.m, b.m);
             double S = 0.0;
             if (M != -INFINITY) {
                 S = a.s * static_cast<double>(__builtin_amdgcn_exp2f((a.m - M) * c));
-                if (it.split) S += b.s * static_cast<double>(__builtin_amdgcn_exp2f((b.m - M) * c));
+                if (it.cut) S += b.s * static_cast<double>(__builtin_amdgcn_exp2f((b.m - M) * c));
             }
             mc[cb] = M == -INFINITY ? 0.0f : M * c;
             r[cb] = S > 0.0 ? static_cast<float>(1.0 / S) : 0.0f;
@@ -372,21 +390,21 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaParams p) {
         for (int cb = 0; cb < 2; ++cb) {
             float M = fmaxf(m[cb], __shfl_xor(m[cb], 16, kWave));
             M = fmaxf(M, __shfl_xor(M, 32, kWave));
-            double s = M == -INFINITY ? 0.0 : sum[cb] * static_cast<double>(__builtin_amdgcn_exp2f((m[cb] - M) * c));
-            s += __shfl_xor(s, 16, kWave);
-            s += __shfl_xor(s, 32, kWave);
-            if (g4 == 0) st[it.j * 128 + col0 + cb * 16] = PrefillStat{M, 0.0f, s};
+            double sm = M == -INFINITY ? 0.0 : sum[cb] * static_cast<double>(__builtin_amdgcn_exp2f((m[cb] - M) * c));
+            sm += __shfl_xor(sm, 16, kWave);
+            sm += __shfl_xor(sm, 32, kWave);
+            if (g4 == 0) st[it.j * 128 + col0 + cb * 16] = PrefillStat{M, 0.0f, sm};
         }
         return;
     }
 
-    if (it.split) {
-        // Publish this part's O (thread-major: element i of every thread is 256 consecutive float4), then
-        // count; the second part to arrive adds the first's O to its own.  With two addends the sum is the
-        // same whichever part arrives second.
-        const int64_t unit = static_cast<int64_t>(g) * (p.n_qt - p.qt_split) + (it.qt - p.qt_split);
-        uint64_t * mine = reinterpret_cast<uint64_t *>(p.partial) + (unit * 2 + it.j) * (16 * 256 * 2);
-        const uint64_t * other = reinterpret_cast<const uint64_t *>(p.partial) + (unit * 2 + (it.j ^ 1)) * (16 * 256 * 2);
+    if (it.cut) {
+        // Publish this part's O (thread-major: element e of every thread is 256 consecutive float4), then
+        // count; the second part to arrive adds the first's O to its own.  With two addends the sum is
+        // the same whichever part arrives second.
+        const int64_t unit = static_cast<int64_t>(g) * (p.n_qt - p.qt_cut) + (it.qt - p.qt_cut);
+        uint64_t * mine = reinterpret_cast<uint64_t *>(p.partial + (unit * 2 + it.j) * kPfPartialFloats);
+        const uint64_t * other = reinterpret_cast<const uint64_t *>(p.partial + (unit * 2 + (it.j ^ 1)) * kPfPartialFloats);
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
 #pragma unroll
@@ -432,16 +450,60 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaParams p) {
     }
 }
 
+// A grid of at most the workgroups that fit on the GPU pulls items until the queues are empty.
+// Workgroup b serves KV head b % n_kv and pulls that head's items from the head's own queue: the
+// workgroups are dispatched round-robin over the 8 XCDs, so with 8 KV heads every XCD works on one
+// head, whose K/V (2 MB at 4k positions) then stays in that XCD's L2.  Each workgroup makes exactly one
+// pull past the end of its queue; the last of those resets the counter to zero for the next call.
+template <int PASS>
+__global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaParams p) {
+    __shared__ __attribute__((aligned(16))) _Float16 sK[2][kBK * kKS];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[PASS == 2 ? 2 : 1][PASS == 2 ? kHeadDim * kVS : 8];
+    __shared__ int s_pull;
+    const int g = static_cast<int>(blockIdx.x) % p.n_kv;
+    // workgroups serving head g, hence pulls past the end of its queue
+    const int n_wg = (static_cast<int>(gridDim.x) - g + p.n_kv - 1) / p.n_kv;
+    uint32_t * queue = p.queue + g * kPfCounterStride;
+    for (;;) {
+        if (threadIdx.x == 0) s_pull = static_cast<int>(__hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED,
+                                                                                 __HIP_MEMORY_SCOPE_AGENT));
+        __syncthreads();
+        const int k = s_pull;
+        __syncthreads();
+        if (k >= p.n_items) {
+            if (threadIdx.x == 0 && k == p.n_items + n_wg - 1) {
+                __hip_atomic_store(queue, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return;
+        }
+        run_item<PASS>(p, item_of(p, g, k), sK, reinterpret_cast<_Float16 (*)[kHeadDim * kVS]>(sV));
+    }
+}
+
 }  // namespace
 
-// Workspace: merge counters (fixed region), the statistics of two parts per (KV head, query tile), and
-// two partial O per (KV head, query tile) when the grid is small enough to be split.
+// Workgroups of one pass that fit on the device at once (the size of the pulling grid).
+template <int PASS>
+int resident_grid() {
+    static const int n = [] {
+        int dev = 0, cus = 0, per_cu = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, prefill_mfma_kernel<PASS>, 256, 0) != hipSuccess) {
+            return 512;
+        }
+        return std::max(1, cus * std::max(1, per_cu));
+    }();
+    return n;
+}
+
+// Workspace: the fixed region (queue and merge counters), then the statistics of two parts per
+// (KV head, query tile), then (grids of at most kPfCutUnits units) two partial outputs per unit.
 size_t prefill_mfma_workspace_bytes(int32_t n_tokens, int32_t n_kv) {
     if (n_tokens <= 0 || n_kv <= 0) return 256;
     const int64_t units = (static_cast<int64_t>(n_tokens) + kBQ - 1) / kBQ * n_kv;
-    const size_t stats = static_cast<size_t>(units) * 2 * 128 * sizeof(PrefillStat);
-    const size_t partials = units <= kPfMaxUnits ? static_cast<size_t>(units) * 2 * 16 * 256 * 4 * sizeof(float) : 0;
-    return kPfCounterBytes + stats + partials;
+    return kPfFixedBytes + static_cast<size_t>(units) * 2 * 128 * sizeof(PrefillStat) +
+           (units <= kPfCutUnits ? static_cast<size_t>(units) * 2 * kPfPartialFloats * sizeof(float) : 0);
 }
 
 int prefill_mfma_launch(const float * q, int32_t q_stride, const void * k, const void * v, int64_t head_stride,
@@ -460,38 +522,38 @@ int prefill_mfma_launch(const float * q, int32_t q_stride, const void * k, const
     p.n_qt = (n_tokens + kBQ - 1) / kBQ;
     p.scale = scale;
     if (static_cast<int64_t>(p.n_qt) * n_kv <= 0) return QA_OK;
-    // Split plan.  The query tile qt attends key tiles [0, n_kt(qt)); the longest has n_kt_max.  With the
-    // whole grid resident at once, the kernel lasts as long as its longest tile, about twice the average:
-    // the tiles with more than ceil(n_kt_max / 2) key tiles are therefore split into two parts of at most
-    // that many, computed by separate workgroups.  The plan needs the workspace (statistics, partials,
-    // counters); without it, or for grids large enough to balance themselves, no tile is split.
-    const int n_kt_max = (n_past + n_tokens + kBK - 1) / kBK;
+    if (n_kv > kPfMaxHeads) return fail(QA_ERR_INVALID, "prefill attention: more than 8 KV heads");
+    // Cut the tiles with more than ceil(n_kt_last / 2) key tiles in two when the grid is small enough for
+    // the longest tiles to set the duration (larger grids balance themselves through the queue) and the
+    // workspace holds the partial outputs; otherwise every tile is one item.
+    const int n_kt_last = (n_past + n_tokens + kBK - 1) / kBK;
     const int64_t units = static_cast<int64_t>(p.n_qt) * n_kv;
-    p.split = 0;
-    p.qt_split = p.n_qt;
-    if (units <= kPfMaxUnits && n_kt_max >= 2 && workspace &&
-        workspace_bytes >= prefill_mfma_workspace_bytes(n_tokens, n_kv)) {
-        p.split = (n_kt_max + 1) / 2;
-        int qt = 0;
-        while (qt < p.n_qt && (n_past + std::min((qt + 1) * kBQ, n_tokens) + kBK - 1) / kBK <= p.split) ++qt;
-        p.qt_split = qt;
-        char * base = static_cast<char *>(workspace);
-        p.counters = reinterpret_cast<uint32_t *>(base);
-        p.stats = reinterpret_cast<PrefillStat *>(base + kPfCounterBytes);
-        p.partial = reinterpret_cast<float *>(base + kPfCounterBytes + static_cast<size_t>(units) * 2 * 128 *
-                                                                           sizeof(PrefillStat));
-    } else {
-        // unsplit: the statistics still pass through memory between the two kernels
-        if (!workspace || workspace_bytes < kPfCounterBytes + static_cast<size_t>(units) * 2 * 128 * sizeof(PrefillStat)) {
-            return fail(QA_ERR_INVALID, "prefill attention: workspace too small (qa_prefill_attn_workspace_bytes)");
-        }
-        p.stats = reinterpret_cast<PrefillStat *>(static_cast<char *>(workspace) + kPfCounterBytes);
+    const size_t stats_bytes = static_cast<size_t>(units) * 2 * 128 * sizeof(PrefillStat);
+    if (!workspace || workspace_bytes < kPfFixedBytes + stats_bytes) {
+        return fail(QA_ERR_INVALID, "prefill attention: workspace too small (qa_prefill_attn_workspace_bytes)");
     }
-    const int64_t items = p.n_qt + (p.n_qt - p.qt_split);
-    const dim3 grid(static_cast<unsigned>(items * n_kv));
-    hipLaunchKernelGGL(prefill_mfma_kernel<1>, grid, dim3(256), 0, stream, p);
+    const bool can_cut = units <= kPfCutUnits && n_kt_last >= 2 &&
+                         workspace_bytes >= prefill_mfma_workspace_bytes(n_tokens, n_kv);
+    p.cap = can_cut ? (n_kt_last + 1) / 2 : n_kt_last;
+    int qt = 0;
+    while (qt < p.n_qt && (n_past + std::min((qt + 1) * kBQ, n_tokens) + kBK - 1) / kBK <= p.cap) ++qt;
+    p.qt_cut = qt;
+    p.n_items = p.n_qt + (p.n_qt - p.qt_cut);
+    char * base = static_cast<char *>(workspace);
+    p.counters = reinterpret_cast<uint32_t *>(base + kPfQueueBytes);
+    p.stats = reinterpret_cast<PrefillStat *>(base + kPfFixedBytes);
+    p.partial = reinterpret_cast<float *>(base + kPfFixedBytes + stats_bytes);
+    // grids: whole multiples of n_kv (every head gets as many workgroups), at most one per item
+    const int64_t total = static_cast<int64_t>(p.n_items) * n_kv;
+    auto grid_of = [&](int resident) {
+        const int64_t gsz = std::max<int64_t>(n_kv, resident / n_kv * n_kv);
+        return dim3(static_cast<unsigned>(std::min(total, gsz)));
+    };
+    p.queue = reinterpret_cast<uint32_t *>(base);
+    hipLaunchKernelGGL(prefill_mfma_kernel<1>, grid_of(resident_grid<1>()), dim3(256), 0, stream, p);
     QA_LAUNCH_CHECK("prefill_mfma_kernel<1>");
-    hipLaunchKernelGGL(prefill_mfma_kernel<2>, grid, dim3(256), 0, stream, p);
+    p.queue = reinterpret_cast<uint32_t *>(base) + kPfMaxHeads * kPfCounterStride;
+    hipLaunchKernelGGL(prefill_mfma_kernel<2>, grid_of(resident_grid<2>()), dim3(256), 0, stream, p);
     QA_LAUNCH_CHECK("prefill_mfma_kernel<2>");
     return QA_OK;
 }

@@ -296,11 +296,15 @@ def test_prefill_attention_long_split_rows(qa, orc):
         check_close(got[t], ref)
 
 
-@pytest.mark.parametrize("n_past,T", [(0, 700), (300, 500)])
+# fixed region of the prefill workspace: queue counters (4 KB) + 8192 merge counters of 256 bytes
+PF_FIXED = 4096 + 8192 * 256
+
+
+@pytest.mark.parametrize("n_past,T", [(0, 1500), (600, 1500)])
 def test_prefill_split_and_unsplit_agree(qa, orc, n_past, T):
-    """The split plan (full workspace) and the unsplit one (a workspace with room for the statistics
-    only) both match the oracle; repeated calls sharing one workspace, with other shapes in between,
-    give identical bits (the merge counters return to zero)."""
+    """The longest query tiles cut in two parts (full workspace) and one item per tile (a workspace
+    with room for the statistics only) both match the oracle; repeated calls sharing one workspace,
+    with other shapes in between, give identical bits (queue and merge counters return to zero)."""
     L = n_past + T
     lay = layout(qa, 1, 1, L + 3, True)
     cache = Cache(qa, lay)
@@ -310,7 +314,7 @@ def test_prefill_split_and_unsplit_agree(qa, orc, n_past, T):
     d_q = dev(qa, q)
     full = qa.lib.qa_prefill_attn_workspace_bytes(T, 16)
     n_units = (T + 63) // 64 * 8
-    small = 1024 * 256 + n_units * 2 * 128 * 16       # counters + statistics, no partials
+    small = PF_FIXED + n_units * 2 * 128 * 16         # counters + statistics, no partial outputs
     assert small < full
     ws = zeros(qa, full, np.uint8)
     ref = orc.cache_attention(k, v, q, n_past, True)
@@ -328,7 +332,7 @@ def test_prefill_split_and_unsplit_agree(qa, orc, n_past, T):
         outs[label] = d_out.numpy().reshape(T, 16, 128)
         check_close(outs[label], ref)
     np.testing.assert_array_equal(outs["split"].view(np.uint32), outs["split again"].view(np.uint32))
-    assert not (ws.numpy()[:1024 * 256].view(np.uint32)).any(), "merge counters not reset"
+    assert not (ws.numpy()[:PF_FIXED].view(np.uint32)).any(), "queue or merge counters not reset"
 
 
 def test_prefill_rejects_missing_workspace(qa):

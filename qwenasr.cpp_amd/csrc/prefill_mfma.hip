@@ -37,6 +37,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 namespace qa {
 namespace {
@@ -111,23 +112,40 @@ struct TileRegs {
 __device__ inline void load_tile(const _Float16 * kh, const _Float16 * vh, int kt, int kend, bool with_v,
                                  TileRegs & r) {
     const int t = threadIdx.x;
+    const int kq = t & 15, dg = t >> 4;
+    const int row0 = kt * kBK;
+    if (row0 + kBK <= kend) {
+        // whole tile: a uniform tile base and fixed per-thread offsets (scalar base + 32-bit vector
+        // offset addressing, no per-load address arithmetic)
+        const _Float16 * kb = kh + static_cast<int64_t>(row0) * kHeadDim;
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            r.k[it] = *reinterpret_cast<const u4 *>(kb + (it * 16 + (t >> 4)) * kHeadDim + (t & 15) * 8);
+        }
+        if (!with_v) return;
+        const _Float16 * vb = vh + static_cast<int64_t>(row0) * kHeadDim;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r.v[e] = *reinterpret_cast<const u4 *>(vb + (kq * 4 + e) * kHeadDim + dg * 8);
+        return;
+    }
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int idx = it * 256 + t;
-        const int row = min(kt * kBK + (idx >> 4), kend - 1);
+        const int row = min(row0 + (idx >> 4), kend - 1);
         r.k[it] = *reinterpret_cast<const u4 *>(kh + static_cast<int64_t>(row) * kHeadDim + (idx & 15) * 8);
     }
     if (!with_v) return;
-    const int kq = t & 15, dg = t >> 4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const int row = min(kt * kBK + kq * 4 + e, kend - 1);
+        const int row = min(row0 + kq * 4 + e, kend - 1);
         r.v[e] = *reinterpret_cast<const u4 *>(vh + static_cast<int64_t>(row) * kHeadDim + dg * 8);
     }
 }
 
-__device__ inline uint32_t lo_pair(uint32_t a, uint32_t b) { return (a & 0xffffu) | (b << 16); }
-__device__ inline uint32_t hi_pair(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xffff0000u); }
+// (a.lo, b.lo) and (a.hi, b.hi) half pairs: one v_perm_b32 each (selector bytes 0-3 pick from the
+// second operand, 4-7 from the first)
+__device__ inline uint32_t lo_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ inline uint32_t hi_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
 __device__ inline void store_tile(const TileRegs & r, _Float16 * sK, _Float16 * sV, bool with_v) {
     const int t = threadIdx.x;
@@ -210,8 +228,9 @@ __device__ inline void stats_update(const f4 (&S)[4][2], int cb, float c, float 
     m = mn;
 }
 
-__device__ inline void pv_tile(const f4 (&S)[4][2], const _Float16 * sV, const float (&mc)[2], const float (&r)[2],
-                               float c, int c16, int g4, f4 (&O)[8][2]) {
+// mc[cb] = (M scale - log2 S) log2 e per query column: p = exp2(s c - mc) = exp(s scale - M) / S.
+__device__ inline void pv_tile(const f4 (&S)[4][2], const _Float16 * sV, const float (&mc)[2], float c, int c16,
+                               int g4, f4 (&O)[8][2]) {
     // P^T fragments: pf[cb][ksv] element e <-> key (2 ksv + e / 4) * 16 + g4 * 4 + e % 4
     h8 pf[2][2];
 #pragma unroll
@@ -220,7 +239,7 @@ __device__ inline void pv_tile(const f4 (&S)[4][2], const _Float16 * sV, const f
         for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float pv = __builtin_amdgcn_exp2f(fmaf(S[kb][cb][i], c, -mc[cb])) * r[cb];
+                const float pv = __builtin_amdgcn_exp2f(fmaf(S[kb][cb][i], c, -mc[cb]));
                 pf[cb][kb >> 1][(kb & 1) * 4 + i] = static_cast<_Float16>(pv);
             }
         }
@@ -332,7 +351,7 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
         }
     }
 
-    float mc[2] = {0.f, 0.f}, r[2] = {0.f, 0.f};
+    float mc[2] = {0.f, 0.f};
     if constexpr (PASS == 2) {
         // row max M and sum S over the parts: S = s_0 exp(m_0 - M) + s_1 exp(m_1 - M), in double
 #pragma unroll
@@ -347,8 +366,10 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
                 S = a.s * static_cast<double>(__builtin_amdgcn_exp2f((a.m - M) * c));
                 if (it.cut) S += b.s * static_cast<double>(__builtin_amdgcn_exp2f((b.m - M) * c));
             }
-            mc[cb] = M == -INFINITY ? 0.0f : M * c;
-            r[cb] = S > 0.0 ? static_cast<float>(1.0 / S) : 0.0f;
+            // the normalisation 1 / S folded into the exponent: exp2(s c - M c - log2 S); a column
+            // without keys (padding) gets an exponent of -inf, so p = 0
+            mc[cb] = M == -INFINITY || !(S > 0.0) ? INFINITY
+                                                  : static_cast<float>(static_cast<double>(M * c) + std::log2(S));
         }
     }
 
@@ -366,23 +387,29 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
     store_tile(regs, sK[0], sV[0], kWithV);
     if (kt0 + 1 < kt1) load_tile(kh, vh, kt0 + 1, kend, kWithV, regs);
     __syncthreads();
-    for (int kt = kt0; kt < kt1; ++kt) {
+    // one key tile: scores, masking (diagonal tiles only), statistics or PV, then the next tile into
+    // the other LDS buffer and the one after into registers
+    auto step = [&](int kt, auto mask) {
         const int b = (kt - kt0) & 1;
         f4 S[4][2];
         scores_tile(sK[b], qf, c16, g4, S);
-        if (kt >= kt_full) mask_tile(S, lim, kt, g4);
+        if constexpr (decltype(mask)::value) mask_tile(S, lim, kt, g4);
         if constexpr (PASS == 1) {
             stats_update(S, 0, c, m[0], sum[0]);
             stats_update(S, 1, c, m[1], sum[1]);
         } else {
-            pv_tile(S, sV[b], mc, r, c, c16, g4, O);
+            pv_tile(S, sV[b], mc, c, c16, g4, O);
         }
         if (kt + 1 < kt1) {
             store_tile(regs, sK[b ^ 1], sV[PASS == 2 ? (b ^ 1) : 0], kWithV);
             if (kt + 2 < kt1) load_tile(kh, vh, kt + 2, kend, kWithV, regs);
         }
         __syncthreads();
-    }
+    };
+    // separate loops, so that the unmasked tiles carry no masking code at all
+    int kt = kt0;
+    for (; kt < min(kt1, kt_full); ++kt) step(kt, std::false_type{});
+    for (; kt < kt1; ++kt) step(kt, std::true_type{});
 
     if constexpr (PASS == 1) {
         // combine the 4 lanes of each query column (lane bits 4, 5) and store the part's statistics
@@ -456,7 +483,7 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
 // head, whose K/V (2 MB at 4k positions) then stays in that XCD's L2.  Each workgroup makes exactly one
 // pull past the end of its queue; the last of those resets the counter to zero for the next call.
 template <int PASS>
-__global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaParams p) {
+__global__ __launch_bounds__(256, PASS == 1 ? 3 : 2) void prefill_mfma_kernel(MfmaParams p) {
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][kBK * kKS];
     __shared__ __attribute__((aligned(16))) _Float16 sV[PASS == 2 ? 2 : 1][PASS == 2 ? kHeadDim * kVS : 8];
     __shared__ int s_pull;

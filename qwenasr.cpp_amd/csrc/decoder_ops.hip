@@ -199,8 +199,11 @@ int launch_gemv_in(const GemvParams & p, hipStream_t stream) {
 //   workgroups, and the number of slices is chosen so that ~512 workgroups cover the matrix;
 // - the X slice of every token (<= 64 KB) is staged once in LDS and read as the B operand;
 // - W streams straight from HBM into the A operand: lane l reads row l % 16 of its wave's block,
-//   8 consecutive k at 8 (l / 16), i.e. 128 contiguous bytes per row per wave instruction pair; the
-//   k order inside an MFMA step is a permutation shared by A and B, which the sum does not see;
+//   k 4 (l / 16) + 0..3 and 16 + 4 (l / 16) + 0..3 of each 32-k step, i.e. 64 contiguous bytes per
+//   row per wave instruction; the k order inside an MFMA step is a permutation shared by A and B,
+//   which the sum does not see.  The B operand reads X from LDS with the same two 16-byte offsets,
+//   whose 16 rows x 4 lane groups at +16 bytes are bank-conflict-free at a row stride of 8 mod 16
+//   dwords (8 consecutive k per lane, +32 bytes per lane group, conflicts at every stride);
 // - slices are merged by the last workgroup of each tile (agent-scope publish + counter on its own
 //   cache line), in slice order, so the result does not depend on scheduling.
 constexpr int kGrTile = 64;          // output rows per workgroup
@@ -220,6 +223,8 @@ struct GemmRowsParams {
     float * partial;          // [ks][rows][N] (ks > 1)
     uint32_t * counters;      // [tiles][kGrCounterStride]
     int32_t N, K, rows, ks, slice, accumulate;
+    uint32_t x_magic;         // ceil(2^32 / (slice / 4)): X staging index / vectors per token row
+    uint32_t x_magic_last;    // the same for the last slice (K - (ks - 1) slice)
 };
 
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -227,20 +232,23 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 template <int TB>
 __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
 #pragma clang fp contract(off)
-    extern __shared__ __attribute__((aligned(16))) float sX[];      // [16 TB][slice + 4]
+    extern __shared__ __attribute__((aligned(16))) float sX[];      // [16 TB][slice + 8]
     const int tile = static_cast<int>(blockIdx.x) / p.ks;
     const int sl = static_cast<int>(blockIdx.x) - tile * p.ks;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x >> 6;
     const int k_begin = sl * p.slice;
     const int k_len = min(p.slice, p.K - k_begin);                 // multiple of 32
-    const int xs = p.slice + 4;                                      // LDS row stride (floats)
+    const uint32_t x_magic = k_len == p.slice ? p.x_magic : p.x_magic_last;
+    // LDS row stride (floats): 16-byte reads of 16 consecutive rows are conflict-free on gfx950 when the
+    // stride in dwords is 8 mod 16 (slices are multiples of 32)
+    const int xs = p.slice + 8;
 
     // W rows of this lane: row n0 + lane % 16 (clamped; rows past N are not stored)
     const int n0 = tile * kGrTile + wave * 16;
     const int nrow = min(n0 + (lane & 15), p.N - 1);
     const int g = lane >> 4;
-    const float * wr = p.W + static_cast<int64_t>(nrow) * p.K + k_begin + 8 * g;
+    const float * wr = p.W + static_cast<int64_t>(nrow) * p.K + k_begin + 4 * g;
 
     // X slice first (at most 16 16-byte loads per thread; token rows past `rows` are zero), then the
     // first batch of W: vector loads complete in issue order, so staging X into LDS waits for X only
@@ -251,7 +259,10 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
 #pragma unroll
     for (int u = 0; u < kXPer; ++u) {
         const int i = min(static_cast<int>(threadIdx.x) + 256 * u, x_vecs - 1);
-        const int t = min(i / (k_len / 4), p.rows - 1), c = i - (i / (k_len / 4)) * (k_len / 4);
+        // i / cols by multiplication with ceil(2^32 / cols) (exact for i < 2^19 / cols)
+        const int cols = k_len / 4;
+        const int q = static_cast<int>(__umulhi(static_cast<uint32_t>(i), x_magic));
+        const int t = min(q, p.rows - 1), c = i - q * cols;
         xv[u] = *reinterpret_cast<const v4f *>(p.X + static_cast<int64_t>(t) * p.K + k_begin + 4 * c);
     }
     asm volatile("" ::: "memory");
@@ -262,13 +273,13 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
     for (int u = 0; u < kB; ++u) {
         const int st = min(u, n_steps - 1);
         wa[u][0] = *reinterpret_cast<const v4f *>(wr + 32 * st);
-        wa[u][1] = *reinterpret_cast<const v4f *>(wr + 32 * st + 4);
+        wa[u][1] = *reinterpret_cast<const v4f *>(wr + 32 * st + 16);
     }
 #pragma unroll
     for (int u = 0; u < kXPer; ++u) {
         const int i = static_cast<int>(threadIdx.x) + 256 * u;
         if (i < x_vecs) {
-            const int t = i / (k_len / 4), c = i - t * (k_len / 4);
+            const int t = static_cast<int>(__umulhi(static_cast<uint32_t>(i), x_magic)), c = i - t * (k_len / 4);
             *reinterpret_cast<v4f *>(sX + t * xs + 4 * c) = t < p.rows ? xv[u] : v4f{0.f, 0.f, 0.f, 0.f};
         }
     }
@@ -279,7 +290,7 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
     v4f acc[TB], acc2[TB];
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) { acc[tb] = v4f{0.f, 0.f, 0.f, 0.f}; acc2[tb] = acc[tb]; }
-    const float * xr = sX + (lane & 15) * xs + 8 * g;
+    const float * xr = sX + (lane & 15) * xs + 4 * g;
     for (int s0 = 0; s0 < n_steps; s0 += kB) {
 #pragma unroll
         for (int u = 0; u < kB; ++u) {
@@ -288,7 +299,7 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
 #pragma unroll
                 for (int tb = 0; tb < TB; ++tb) {
                     const v4f x0 = *reinterpret_cast<const v4f *>(xr + tb * 16 * xs + kk);
-                    const v4f x1 = *reinterpret_cast<const v4f *>(xr + tb * 16 * xs + kk + 4);
+                    const v4f x1 = *reinterpret_cast<const v4f *>(xr + tb * 16 * xs + kk + 16);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         acc[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[u][0][j], x0[j], acc[tb], 0, 0, 0);
@@ -303,7 +314,7 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
             for (int u = 0; u < kB; ++u) {
                 const int st = min(s0 + kB + u, n_steps - 1);
                 wa[u][0] = *reinterpret_cast<const v4f *>(wr + 32 * st);
-                wa[u][1] = *reinterpret_cast<const v4f *>(wr + 32 * st + 4);
+                wa[u][1] = *reinterpret_cast<const v4f *>(wr + 32 * st + 16);
             }
         }
     }
@@ -411,7 +422,7 @@ GemmRowsPlan gemm_rows_plan(int32_t N, int32_t K, int32_t rows) {
     int ks = std::max(1, std::min(std::min((512 + pl.tiles - 1) / pl.tiles, 8), K / 32));
     for (;; ++ks) {
         pl.slice = ((K + ks - 1) / ks + 31) / 32 * 32;
-        if (static_cast<size_t>(rows_pad) * (pl.slice + 4) * sizeof(float) <= kGrLdsBytes || pl.slice == 32) break;
+        if (static_cast<size_t>(rows_pad) * (pl.slice + 8) * sizeof(float) <= kGrLdsBytes || pl.slice == 32) break;
     }
     pl.ks = (K + pl.slice - 1) / pl.slice;
     return pl;
@@ -586,8 +597,14 @@ int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int
     p.ks = pl.ks;
     p.slice = pl.slice;
     p.accumulate = accumulate ? 1 : 0;
+    auto magic = [](int k_len) {
+        const uint64_t cols = static_cast<uint64_t>(k_len / 4);
+        return static_cast<uint32_t>(((uint64_t{1} << 32) + cols - 1) / cols);
+    };
+    p.x_magic = magic(pl.slice);
+    p.x_magic_last = magic(K - (pl.ks - 1) * pl.slice);
     const int tb = (rows + 15) / 16;
-    const size_t lds = static_cast<size_t>(16 * tb) * (pl.slice + 4) * sizeof(float);
+    const size_t lds = static_cast<size_t>(16 * tb) * (pl.slice + 8) * sizeof(float);
     const dim3 grid(static_cast<unsigned>(pl.tiles * pl.ks));
     switch (tb) {
         case 1: hipLaunchKernelGGL((gemm_rows_kernel<1>), grid, dim3(256), lds, stream, p); break;

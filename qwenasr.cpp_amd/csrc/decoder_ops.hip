@@ -208,7 +208,9 @@ int launch_gemv_in(const GemvParams & p, hipStream_t stream) {
 //   cache line), in slice order, so the result does not depend on scheduling.
 constexpr int kGrTile = 64;          // output rows per workgroup
 constexpr int kGrMaxRows = 64;       // token rows supported
-constexpr int kGrLdsBytes = 64 * 1024;
+constexpr int kGrLdsBytes = 52 * 1024;  // X slice budget: 3 workgroups per CU
+// X staging: every token row of the slice, 16-byte vectors over 256 threads, at most 13 per thread
+static_assert(kGrLdsBytes / 16 <= 13 * 256, "X staging registers per thread");
 constexpr int kGrCounterStride = 64; // uint32 per tile counter (256 bytes)
 // The workspace starts with a fixed counter region for kGrMaxTiles tiles, followed by the partials:
 // one layout for every shape, so calls of different shapes can share a workspace without one call's
@@ -253,7 +255,8 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
     // X slice first (at most 16 16-byte loads per thread; token rows past `rows` are zero), then the
     // first batch of W: vector loads complete in issue order, so staging X into LDS waits for X only
     // while W streams in
-    constexpr int kXPer = 16;
+    // 16 TB rows x slice / 4 vectors <= 13 per thread within the LDS budget (static_assert below)
+    constexpr int kXPer = 13;
     const int x_vecs = 16 * TB * (k_len / 4);
     v4f xv[kXPer];
 #pragma unroll
@@ -266,7 +269,7 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
         xv[u] = *reinterpret_cast<const v4f *>(p.X + static_cast<int64_t>(t) * p.K + k_begin + 4 * c);
     }
     asm volatile("" ::: "memory");
-    constexpr int kB = 16;                                           // 32-k steps per batch (slices <= 512: one)
+    constexpr int kB = 6;                                            // 32-k steps per batch
     const int n_steps = k_len / 32;
     v4f wa[kB][2];
 #pragma unroll

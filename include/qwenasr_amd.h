@@ -156,7 +156,14 @@ int qa_decode_step_attn(const float * qkv, const float * q_norm_w, const float *
 
 /* Causal prefill attention over the cache (row a7): the n_tokens queries of stream `stream_idx` at
  * positions n_past .. n_past + n_tokens - 1, query t attending keys [0, n_past + t].  Same
- * arithmetic as qa_decode_attn.  f16 caches run on CDNA4 f16 MFMA.                           */
+ * arithmetic as qa_decode_attn.  f16 caches run on CDNA4 f16 MFMA as two kernels (row statistics,
+ * then p and PV) over work items pulled from per-KV-head queues.
+ * workspace (f16 caches): qa_prefill_attn_workspace_bytes(n_tokens, n_heads) bytes, cleared once
+ * with qa_workspace_clear before the first call; it holds the queue and merge counters (every call
+ * leaves them zero, so one workspace serves any sequence of calls with at most n_tokens tokens),
+ * the statistics and the partial outputs of the longest query tiles.  A smaller workspace that
+ * still holds the counters and statistics runs without cutting tiles; a missing one is an error.
+ * Calls that share a workspace must be stream-ordered.  f32 caches use no workspace.            */
 size_t qa_prefill_attn_workspace_bytes(int32_t n_tokens, int32_t n_heads);
 int qa_prefill_attn(const float * q, const void * cache, const qa_kv_layout * layout, int32_t layer,
                     int32_t stream_idx, int32_t n_past, int32_t n_tokens, int32_t n_heads, float scale,

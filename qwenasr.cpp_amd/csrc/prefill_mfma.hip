@@ -49,6 +49,7 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBQ = 64;     // query tokens per workgroup
 constexpr int kBK = 64;     // keys per tile
+constexpr int kPfThreads = 512;   // 8 waves: wave w takes head 2g + w / 4 and query tokens 16 (w % 4) .. + 15
 // Row strides: a 16-byte LDS read by 16 lanes of consecutive rows is conflict-free on gfx950 when the
 // stride in dwords is 8 mod 16 (measured: 80, 112, 144 halfs conflict-free; 72, 88, 96, 136 halfs
 // lose ~half the LDS cycles to bank conflicts).
@@ -68,7 +69,7 @@ constexpr int kPfMaxMerge = 8192;       // merge counters: one per (KV head, que
 constexpr int kPfCutUnits = 2048;       // (KV head, query tile) units up to which long tiles are cut
 constexpr size_t kPfQueueBytes = 2 * kPfMaxHeads * kPfCounterStride * sizeof(uint32_t);
 constexpr size_t kPfFixedBytes = kPfQueueBytes + static_cast<size_t>(kPfMaxMerge) * kPfCounterStride * sizeof(uint32_t);
-constexpr size_t kPfPartialFloats = 16 * 256 * 4;   // one part's O: 16 float4 per thread
+constexpr size_t kPfPartialFloats = 8 * 512 * 4;    // one part's O: 8 float4 per thread
 
 struct alignas(16) PrefillStat {
     float m;
@@ -100,44 +101,44 @@ __device__ inline uint64_t pack2(float a, float b) {
 __device__ inline float lo_float(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
 __device__ inline float hi_float(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v >> 32)); }
 
-// Global -> register staging of one tile.  K: thread t loads 16-byte slices idx = it * 256 + t
-// (row idx / 16, slice idx % 16).  V: thread t loads slice dg = 4 * wave + lane / 16 of the 4 rows
-// 4 kq .. 4 kq + 3 with kq = lane % 16, which it writes transposed.  Rows past the end re-read the last
-// row (masked keys get p = 0; no branch splits the loads).
+// Global -> register staging of one tile by the 512 threads.  K: thread t loads 16-byte slices idx =
+// it * 512 + t (row idx / 16, slice idx % 16).  V: thread t loads dims 8 dg .. 8 dg + 7 (dg = t / 32) of
+// the key pair 2 kp, 2 kp + 1 (kp = t % 32), which it writes transposed.  Rows past the end re-read the
+// last row (masked keys get p = 0; no branch splits the loads).
 struct TileRegs {
-    u4 k[4];
-    u4 v[4];
+    u4 k[2];
+    u4 v[2];
 };
 
 __device__ inline void load_tile(const _Float16 * kh, const _Float16 * vh, int kt, int kend, bool with_v,
                                  TileRegs & r) {
     const int t = threadIdx.x;
-    const int kq = t & 15, dg = t >> 4;
+    const int kp = t & 31, dg = t >> 5;
     const int row0 = kt * kBK;
     if (row0 + kBK <= kend) {
         // whole tile: a uniform tile base and fixed per-thread offsets (scalar base + 32-bit vector
         // offset addressing, no per-load address arithmetic)
         const _Float16 * kb = kh + static_cast<int64_t>(row0) * kHeadDim;
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            r.k[it] = *reinterpret_cast<const u4 *>(kb + (it * 16 + (t >> 4)) * kHeadDim + (t & 15) * 8);
+        for (int it = 0; it < 2; ++it) {
+            r.k[it] = *reinterpret_cast<const u4 *>(kb + (it * 32 + (t >> 4)) * kHeadDim + (t & 15) * 8);
         }
         if (!with_v) return;
         const _Float16 * vb = vh + static_cast<int64_t>(row0) * kHeadDim;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r.v[e] = *reinterpret_cast<const u4 *>(vb + (kq * 4 + e) * kHeadDim + dg * 8);
+        for (int e = 0; e < 2; ++e) r.v[e] = *reinterpret_cast<const u4 *>(vb + (kp * 2 + e) * kHeadDim + dg * 8);
         return;
     }
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int idx = it * 256 + t;
+    for (int it = 0; it < 2; ++it) {
+        const int idx = it * kPfThreads + t;
         const int row = min(row0 + (idx >> 4), kend - 1);
         r.k[it] = *reinterpret_cast<const u4 *>(kh + static_cast<int64_t>(row) * kHeadDim + (idx & 15) * 8);
     }
     if (!with_v) return;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int row = min(row0 + kq * 4 + e, kend - 1);
+    for (int e = 0; e < 2; ++e) {
+        const int row = min(row0 + kp * 2 + e, kend - 1);
         r.v[e] = *reinterpret_cast<const u4 *>(vh + static_cast<int64_t>(row) * kHeadDim + dg * 8);
     }
 }
@@ -150,68 +151,58 @@ __device__ inline uint32_t hi_pair(uint32_t a, uint32_t b) { return __builtin_am
 __device__ inline void store_tile(const TileRegs & r, _Float16 * sK, _Float16 * sV, bool with_v) {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int idx = it * 256 + t;
+    for (int it = 0; it < 2; ++it) {
+        const int idx = it * kPfThreads + t;
         *reinterpret_cast<u4 *>(sK + (idx >> 4) * kKS + (idx & 15) * 8) = r.k[it];
     }
     if (!with_v) return;
-    const int kq = t & 15, dg = t >> 4;
+    const int kp = t & 31, dg = t >> 5;
     // V^T columns are keys in PV order: key j sits at column (j / 32) * 32 + ((j % 16) / 4) * 8 +
     // ((j / 16) % 2) * 4 + j % 4, so the 8 keys one lane multiplies in a 32-key step (4 from each 16-key
-    // block) are 8 consecutive halfs: one 16-byte read.  Keys 4 kq .. 4 kq + 3 stay adjacent.
-    const int col = (kq >> 3) * 32 + (kq & 3) * 8 + ((kq >> 2) & 1) * 4;
+    // block) are 8 consecutive halfs: one 16-byte read.  Keys 2 kp and 2 kp + 1 stay adjacent.
+    const int j = 2 * kp;
+    const int col = (j >> 5) * 32 + ((j & 15) >> 2) * 8 + ((j >> 4) & 1) * 4 + (j & 3);
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-        // dims 2w and 2w + 1 of the slice, keys 4 kq .. 4 kq + 3
-        const uint2 even = make_uint2(lo_pair(r.v[0][w], r.v[1][w]), lo_pair(r.v[2][w], r.v[3][w]));
-        const uint2 odd = make_uint2(hi_pair(r.v[0][w], r.v[1][w]), hi_pair(r.v[2][w], r.v[3][w]));
-        *reinterpret_cast<uint2 *>(sV + (dg * 8 + 2 * w) * kVS + col) = even;
-        *reinterpret_cast<uint2 *>(sV + (dg * 8 + 2 * w + 1) * kVS + col) = odd;
+        // dims 2w and 2w + 1 of the slice, keys 2 kp and 2 kp + 1
+        *reinterpret_cast<uint32_t *>(sV + (dg * 8 + 2 * w) * kVS + col) = lo_pair(r.v[0][w], r.v[1][w]);
+        *reinterpret_cast<uint32_t *>(sV + (dg * 8 + 2 * w + 1) * kVS + col) = hi_pair(r.v[0][w], r.v[1][w]);
     }
 }
 
-// S^T tile of this wave: S[kb][cb] = 16 keys (kb) x 16 queries (cb).
-__device__ inline void scores_tile(const _Float16 * sK, const h8 (&qf)[2][4], int c16, int g4, f4 (&S)[4][2]) {
+// S^T tile of this wave: S[kb] = 16 keys (kb) x the wave's 16 queries.
+__device__ inline void scores_tile(const _Float16 * sK, const h8 (&qf)[4], int c16, int g4, f4 (&S)[4]) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) S[kb][cb] = f4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int kb = 0; kb < 4; ++kb) S[kb] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
             const h8 a = *reinterpret_cast<const h8 *>(sK + (kb * 16 + c16) * kKS + ks * 32 + g4 * 8);
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                S[kb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[cb][ks], S[kb][cb], 0, 0, 0);
-            }
+            S[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ks], S[kb], 0, 0, 0);
         }
     }
 }
 
-// Masks the keys of a diagonal tile: key j of query column cb is attended iff j <= lim[cb].
-__device__ inline void mask_tile(f4 (&S)[4][2], const int (&lim)[2], int kt, int g4) {
+// Masks the keys of a diagonal tile: key j of this lane's query column is attended iff j <= lim.
+__device__ inline void mask_tile(f4 (&S)[4], int lim, int kt, int g4) {
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
+    for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int j = kt * kBK + kb * 16 + g4 * 4 + i;
-                if (j > lim[cb]) S[kb][cb][i] = -INFINITY;
-            }
+        for (int i = 0; i < 4; ++i) {
+            const int j = kt * kBK + kb * 16 + g4 * 4 + i;
+            if (j > lim) S[kb][i] = -INFINITY;
         }
     }
 }
 
 // Pass-1 update of one lane's running max m (raw score units) and double sum of exp(s - m).
-__device__ inline void stats_update(const f4 (&S)[4][2], int cb, float c, float & m, double & sum) {
+__device__ inline void stats_update(const f4 (&S)[4], float c, float & m, double & sum) {
     float tmax = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, S[kb][cb][i]);
+        for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, S[kb][i]);
     }
     const float mn = fmaxf(m, tmax);
     if (mn == -INFINITY) return;                 // every key so far masked for this lane
@@ -220,7 +211,7 @@ __device__ inline void stats_update(const f4 (&S)[4][2], int cb, float c, float 
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) part += __builtin_amdgcn_exp2f(fmaf(S[kb][cb][i], c, -mc));
+        for (int i = 0; i < 4; ++i) part += __builtin_amdgcn_exp2f(fmaf(S[kb][i], c, -mc));
     }
     // exp2(-inf) = 0 when the lane had nothing before this tile
     const float f = __builtin_amdgcn_exp2f(fmaf(m, c, -mc));
@@ -228,20 +219,16 @@ __device__ inline void stats_update(const f4 (&S)[4][2], int cb, float c, float 
     m = mn;
 }
 
-// mc[cb] = (M scale - log2 S) log2 e per query column: p = exp2(s c - mc) = exp(s scale - M) / S.
-__device__ inline void pv_tile(const f4 (&S)[4][2], const _Float16 * sV, const float (&mc)[2], float c, int c16,
-                               int g4, f4 (&O)[8][2]) {
-    // P^T fragments: pf[cb][ksv] element e <-> key (2 ksv + e / 4) * 16 + g4 * 4 + e % 4
-    h8 pf[2][2];
+// mc = (M scale - log2 S) log2 e for this lane's query column: p = exp2(s c - mc) = exp(s scale - M) / S.
+__device__ inline void pv_tile(const f4 (&S)[4], const _Float16 * sV, float mc, float c, int c16, int g4,
+                               f4 (&O)[8]) {
+    // P^T fragments: pf[ksv] element e <-> key (2 ksv + e / 4) * 16 + g4 * 4 + e % 4
+    h8 pf[2];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
+    for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float pv = __builtin_amdgcn_exp2f(fmaf(S[kb][cb][i], c, -mc[cb]));
-                pf[cb][kb >> 1][(kb & 1) * 4 + i] = static_cast<_Float16>(pv);
-            }
+        for (int i = 0; i < 4; ++i) {
+            pf[kb >> 1][(kb & 1) * 4 + i] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(S[kb][i], c, -mc)));
         }
     }
 #pragma unroll
@@ -249,10 +236,7 @@ __device__ inline void pv_tile(const f4 (&S)[4][2], const _Float16 * sV, const f
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
             const h8 a = *reinterpret_cast<const h8 *>(sV + (db * 16 + c16) * kVS + ksv * 32 + g4 * 8);
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                O[db][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pf[cb][ksv], O[db][cb], 0, 0, 0);
-            }
+            O[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pf[ksv], O[db], 0, 0, 0);
         }
     }
 }
@@ -308,9 +292,8 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
     const int t0 = it.qt * kBQ;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x >> 6;
-    const int hh = wave >> 1;
+    const int hh = wave >> 2;
     const int h = g * 2 + hh;
-    const int tw = t0 + (wave & 1) * 32;
     const int c16 = lane & 15;
     const int g4 = lane >> 4;
     const int L_total = p.n_past + p.n_tokens;
@@ -321,66 +304,53 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
     const _Float16 * vh = p.v + g * p.head_stride;
     const float c = p.scale * kLog2e;
 
-    // query columns of this lane and their causal key limits
-    int tq[2], lim[2];
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-        tq[cb] = tw + cb * 16 + c16;
-        lim[cb] = tq[cb] < p.n_tokens ? p.n_past + tq[cb] : -1;   // keys j <= lim are attended
-    }
+    // this lane's query column and its causal key limit (keys j <= lim are attended)
+    const int tq = t0 + (wave & 3) * 16 + c16;
+    const int lim = tq < p.n_tokens ? p.n_past + tq : -1;
     // statistics of part j of this query tile: [g][qt][j][column]
-    const int col0 = hh * 64 + (wave & 1) * 32 + c16;
+    const int col = hh * 64 + (wave & 3) * 16 + c16;
     PrefillStat * st = p.stats + (static_cast<int64_t>(g) * p.n_qt + it.qt) * 2 * 128;
 
     // Q fragments, the B operand of S^T: lane holds query column c16 and 8 dims of each 32-dim step,
     // rounded to f16 (GGML's conversion of src1 for an f16 src0); absent tokens are zero
-    h8 qf[2][4];
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-        const int tqc = min(tq[cb], p.n_tokens - 1);
+    h8 qf[4];
+    {
+        const int tqc = min(tq, p.n_tokens - 1);
+        const bool ok = tq < p.n_tokens;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const float * qp = p.q + static_cast<int64_t>(tqc) * p.q_stride + h * kHeadDim + ks * 32 + g4 * 8;
             const float4 a = *reinterpret_cast<const float4 *>(qp);
             const float4 b = *reinterpret_cast<const float4 *>(qp + 4);
-            const bool ok = tq[cb] < p.n_tokens;
-            qf[cb][ks] = h8{static_cast<_Float16>(ok ? a.x : 0.f), static_cast<_Float16>(ok ? a.y : 0.f),
-                            static_cast<_Float16>(ok ? a.z : 0.f), static_cast<_Float16>(ok ? a.w : 0.f),
-                            static_cast<_Float16>(ok ? b.x : 0.f), static_cast<_Float16>(ok ? b.y : 0.f),
-                            static_cast<_Float16>(ok ? b.z : 0.f), static_cast<_Float16>(ok ? b.w : 0.f)};
+            qf[ks] = h8{static_cast<_Float16>(ok ? a.x : 0.f), static_cast<_Float16>(ok ? a.y : 0.f),
+                        static_cast<_Float16>(ok ? a.z : 0.f), static_cast<_Float16>(ok ? a.w : 0.f),
+                        static_cast<_Float16>(ok ? b.x : 0.f), static_cast<_Float16>(ok ? b.y : 0.f),
+                        static_cast<_Float16>(ok ? b.z : 0.f), static_cast<_Float16>(ok ? b.w : 0.f)};
         }
     }
 
-    float mc[2] = {0.f, 0.f};
+    float mc = 0.f;
     if constexpr (PASS == 2) {
-        // row max M and sum S over the parts: S = s_0 exp(m_0 - M) + s_1 exp(m_1 - M), in double
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            const int col = col0 + cb * 16;
-            const PrefillStat a = st[col];
-            PrefillStat b{-INFINITY, 0.f, 0.0};
-            if (it.cut) b = st[128 + col];
-            const float M = fmaxf(a.m, b.m);
-            double S = 0.0;
-            if (M != -INFINITY) {
-                S = a.s * static_cast<double>(__builtin_amdgcn_exp2f((a.m - M) * c));
-                if (it.cut) S += b.s * static_cast<double>(__builtin_amdgcn_exp2f((b.m - M) * c));
-            }
-            // the normalisation 1 / S folded into the exponent: exp2(s c - M c - log2 S); a column
-            // without keys (padding) gets an exponent of -inf, so p = 0
-            mc[cb] = M == -INFINITY || !(S > 0.0) ? INFINITY
-                                                  : static_cast<float>(static_cast<double>(M * c) + std::log2(S));
+        // row max M and sum S over the parts: S = s_0 exp(m_0 - M) + s_1 exp(m_1 - M), in double; the
+        // normalisation 1 / S folded into the exponent: exp2(s c - M c - log2 S); a column without keys
+        // (padding) gets an exponent of -inf, so p = 0
+        const PrefillStat a = st[col];
+        PrefillStat b{-INFINITY, 0.f, 0.0};
+        if (it.cut) b = st[128 + col];
+        const float M = fmaxf(a.m, b.m);
+        double S = 0.0;
+        if (M != -INFINITY) {
+            S = a.s * static_cast<double>(__builtin_amdgcn_exp2f((a.m - M) * c));
+            if (it.cut) S += b.s * static_cast<double>(__builtin_amdgcn_exp2f((b.m - M) * c));
         }
+        mc = M == -INFINITY || !(S > 0.0) ? INFINITY : static_cast<float>(static_cast<double>(M * c) + std::log2(S));
     }
 
-    float m[2] = {-INFINITY, -INFINITY};
-    double sum[2] = {0.0, 0.0};
-    f4 O[8][2];
+    float m = -INFINITY;
+    double sum = 0.0;
+    f4 O[8];
 #pragma unroll
-    for (int db = 0; db < 8; ++db) {
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) O[db][cb] = f4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int db = 0; db < 8; ++db) O[db] = f4{0.f, 0.f, 0.f, 0.f};
     TileRegs regs;
     const int kt0 = it.kt0, kt1 = it.kt1;
     load_tile(kh, vh, kt0, kend, kWithV, regs);
@@ -391,12 +361,11 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
     // the other LDS buffer and the one after into registers
     auto step = [&](int kt, auto mask) {
         const int b = (kt - kt0) & 1;
-        f4 S[4][2];
+        f4 S[4];
         scores_tile(sK[b], qf, c16, g4, S);
         if constexpr (decltype(mask)::value) mask_tile(S, lim, kt, g4);
         if constexpr (PASS == 1) {
-            stats_update(S, 0, c, m[0], sum[0]);
-            stats_update(S, 1, c, m[1], sum[1]);
+            stats_update(S, c, m, sum);
         } else {
             pv_tile(S, sV[b], mc, c, c16, g4, O);
         }
@@ -412,21 +381,18 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
     for (; kt < kt1; ++kt) step(kt, std::true_type{});
 
     if constexpr (PASS == 1) {
-        // combine the 4 lanes of each query column (lane bits 4, 5) and store the part's statistics
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            float M = fmaxf(m[cb], __shfl_xor(m[cb], 16, kWave));
-            M = fmaxf(M, __shfl_xor(M, 32, kWave));
-            double sm = M == -INFINITY ? 0.0 : sum[cb] * static_cast<double>(__builtin_amdgcn_exp2f((m[cb] - M) * c));
-            sm += __shfl_xor(sm, 16, kWave);
-            sm += __shfl_xor(sm, 32, kWave);
-            if (g4 == 0) st[it.j * 128 + col0 + cb * 16] = PrefillStat{M, 0.0f, sm};
-        }
+        // combine the 4 lanes of the query column (lane bits 4, 5) and store the part's statistics
+        float M = fmaxf(m, __shfl_xor(m, 16, kWave));
+        M = fmaxf(M, __shfl_xor(M, 32, kWave));
+        double sm = M == -INFINITY ? 0.0 : sum * static_cast<double>(__builtin_amdgcn_exp2f((m - M) * c));
+        sm += __shfl_xor(sm, 16, kWave);
+        sm += __shfl_xor(sm, 32, kWave);
+        if (g4 == 0) st[it.j * 128 + col] = PrefillStat{M, 0.0f, sm};
         return;
     }
 
     if (it.cut) {
-        // Publish this part's O (thread-major: element e of every thread is 256 consecutive float4), then
+        // Publish this part's O (thread-major: element e of every thread is 512 consecutive float4), then
         // count; the second part to arrive adds the first's O to its own.  With two addends the sum is
         // the same whichever part arrives second.
         const int64_t unit = static_cast<int64_t>(g) * (p.n_qt - p.qt_cut) + (it.qt - p.qt_cut);
@@ -434,13 +400,9 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
         const uint64_t * other = reinterpret_cast<const uint64_t *>(p.partial + (unit * 2 + (it.j ^ 1)) * kPfPartialFloats);
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                const int e = ((db * 2 + cb) * 256 + static_cast<int>(threadIdx.x)) * 2;
-                const f4 o = O[db][cb];
-                __hip_atomic_store(mine + e, pack2(o[0], o[1]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(mine + e + 1, pack2(o[2], o[3]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+            const int e = (db * kPfThreads + static_cast<int>(threadIdx.x)) * 2;
+            __hip_atomic_store(mine + e, pack2(O[db][0], O[db][1]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(mine + e + 1, pack2(O[db][2], O[db][3]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
@@ -455,24 +417,19 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
         if (!s_last) return;
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                const int e = ((db * 2 + cb) * 256 + static_cast<int>(threadIdx.x)) * 2;
-                const uint64_t lo = __hip_atomic_load(other + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const uint64_t hi = __hip_atomic_load(other + e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                O[db][cb] += f4{lo_float(lo), hi_float(lo), lo_float(hi), hi_float(hi)};
-            }
+            const int e = (db * kPfThreads + static_cast<int>(threadIdx.x)) * 2;
+            const uint64_t lo = __hip_atomic_load(other + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint64_t hi = __hip_atomic_load(other + e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            O[db] += f4{lo_float(lo), hi_float(lo), lo_float(hi), hi_float(hi)};
         }
     }
 
-    // O^T: lane holds dims db * 16 + g4 * 4 + i of query column c16 of block cb
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-        if (tq[cb] >= p.n_tokens) continue;
-        float * op = p.out + static_cast<int64_t>(tq[cb]) * p.q_stride + h * kHeadDim + g4 * 4;
+    // O^T: lane holds dims db * 16 + g4 * 4 + i of its query column
+    if (tq < p.n_tokens) {
+        float * op = p.out + static_cast<int64_t>(tq) * p.q_stride + h * kHeadDim + g4 * 4;
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
-            *reinterpret_cast<float4 *>(op + db * 16) = make_float4(O[db][cb][0], O[db][cb][1], O[db][cb][2], O[db][cb][3]);
+            *reinterpret_cast<float4 *>(op + db * 16) = make_float4(O[db][0], O[db][1], O[db][2], O[db][3]);
         }
     }
 }
@@ -483,7 +440,7 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
 // head, whose K/V (2 MB at 4k positions) then stays in that XCD's L2.  Each workgroup makes exactly one
 // pull past the end of its queue; the last of those resets the counter to zero for the next call.
 template <int PASS>
-__global__ __launch_bounds__(256, PASS == 1 ? 3 : 2) void prefill_mfma_kernel(MfmaParams p) {
+__global__ __launch_bounds__(kPfThreads, 4) void prefill_mfma_kernel(MfmaParams p) {
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][kBK * kKS];
     __shared__ __attribute__((aligned(16))) _Float16 sV[PASS == 2 ? 2 : 1][PASS == 2 ? kHeadDim * kVS : 8];
     __shared__ int s_pull;
@@ -516,7 +473,7 @@ int resident_grid() {
         int dev = 0, cus = 0, per_cu = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, prefill_mfma_kernel<PASS>, 256, 0) != hipSuccess) {
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, prefill_mfma_kernel<PASS>, kPfThreads, 0) != hipSuccess) {
             return 512;
         }
         return std::max(1, cus * std::max(1, per_cu));
@@ -577,10 +534,10 @@ int prefill_mfma_launch(const float * q, int32_t q_stride, const void * k, const
         return dim3(static_cast<unsigned>(std::min(total, gsz)));
     };
     p.queue = reinterpret_cast<uint32_t *>(base);
-    hipLaunchKernelGGL(prefill_mfma_kernel<1>, grid_of(resident_grid<1>()), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(prefill_mfma_kernel<1>, grid_of(resident_grid<1>()), dim3(kPfThreads), 0, stream, p);
     QA_LAUNCH_CHECK("prefill_mfma_kernel<1>");
     p.queue = reinterpret_cast<uint32_t *>(base) + kPfMaxHeads * kPfCounterStride;
-    hipLaunchKernelGGL(prefill_mfma_kernel<2>, grid_of(resident_grid<2>()), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(prefill_mfma_kernel<2>, grid_of(resident_grid<2>()), dim3(kPfThreads), 0, stream, p);
     QA_LAUNCH_CHECK("prefill_mfma_kernel<2>");
     return QA_OK;
 }

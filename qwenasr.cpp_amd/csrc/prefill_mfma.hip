@@ -6,22 +6,25 @@
 // QK^T and the normalised probabilities to f16 before PV; both are exactly the f16 operands the MFMA
 // takes, with f32 accumulation.
 //
-// Tiling.  A workgroup (4 waves) owns 64 query tokens of one stream and both query heads of one KV
+// Tiling.  A workgroup (8 waves) owns 64 query tokens of one stream and both query heads of one KV
 // head: 128 query columns, every K/V byte of the head shared by both heads.  Wave w takes head
-// 2g + w/2 and tokens [32 (w & 1), +32).  Per 64-key tile a wave computes S^T = K Q^T (keys x queries,
-// 16x16 blocks, head dim in 4 steps of 32), so after the MFMA each lane holds 16 keys of 2 query
-// columns.
+// 2g + w/4 and tokens [16 (w & 3), +16).  Per 64-key tile a wave computes S^T = K Q^T (keys x queries,
+// 16x16 blocks, head dim in 4 steps of 32), so after the MFMA each lane holds 16 keys of one query
+// column.
 //
-// Exact GGML softmax needs the row max and sum before any PV, so the key tiles are walked twice:
+// Exact GGML softmax needs the row max and sum before any PV, so the key tiles are walked twice, by two
+// kernels over the same work items:
 //   pass 1  S^T, a running max per lane and the sum of exp(s - max): 16 terms in f32 per tile and
 //           lane, carried across tiles in double and rescaled when the lane's max grows; the 4 lanes
-//           of a query column are combined once at the end;
-//   pass 2  S^T again, p = f16(exp(s - M) * (float)(1 / sum)), O^T += V^T P^T.
-// exp(x * scale - m) is evaluated as exp2(x * (scale log2 e) - m (scale log2 e)): one FMA and one
-// v_exp_f32 per score.  Its rounding differs from a library expf by a few f32 ulps, far below the f16
-// resolution of p (the reference's own CPU softmax uses a vectorised exp approximation as well).
-// Only the diagonal tiles (keys past the first query of the workgroup) are masked; every other tile
-// takes an unmasked path.
+//           of a query column are combined at the end and the item's statistics stored;
+//   pass 2  the statistics of the query tile's parts combined into M and S, S^T again,
+//           p = f16(exp(s - M) / S), O^T += V^T P^T.
+// exp(x * scale - m) is evaluated as exp2(x * (scale log2 e) - m (scale log2 e)), with log2 S folded
+// into m in pass 2: one FMA and one v_exp_f32 per score.  Its rounding differs from the reference's
+// expf(x - M) * (1 / S) by about 1e-6 relative, far below the f16 resolution of p (the reference's own
+// CPU softmax uses a vectorised exp approximation as well).
+// Only the diagonal tiles (keys past the first query of the workgroup) are masked, in a loop of their
+// own; every other tile takes an unmasked path.
 // P^T goes from the accumulator registers straight into the B operand of the PV MFMA: the PV k-index
 // e of lane group j is mapped to key (e / 4) * 16 + j * 4 + e % 4 of the 32-key step, which is
 // exactly the set of keys that lane already holds; V^T is read from LDS with the same mapping.
@@ -29,10 +32,10 @@
 // LDS: two buffers of the K tile (row-major, 144-half rows) and of V^T (dims x keys in PV order,
 // 80-half rows): one barrier per tile; the next tile's global loads are in registers while the current
 // one is computed.  Both operands are read as 16-byte rows at conflict-free strides.  V^T is written as
-// 4 keys x 1 dim per 8-byte store, transposed in registers from 4 rows of 8 dims.
-// Work distribution: the two passes are separate kernels over the same work items (parts of the key
-// range of one query tile and KV head), pulled from a queue in descending order of query tile by a grid
-// that fits on the GPU at once; the 8 KV heads of one item are consecutive pulls.
+// 2 keys x 1 dim per 4-byte store, transposed in registers from 2 rows of 8 dims.
+// Work distribution: the longest query tiles are cut in two parts of the key range; every part (or
+// uncut tile) of one KV head is a work item, pulled from that head's queue by the workgroups serving
+// the head, longest first (see the work plan below).
 #include "ops.hpp"
 
 #include <algorithm>

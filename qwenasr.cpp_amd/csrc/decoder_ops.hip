@@ -230,6 +230,7 @@ struct GemmRowsParams {
 };
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 template <int TB>
 __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
@@ -412,12 +413,200 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
     }
 }
 
+// ---------------------------------------------------------------- skinny GEMM, up to 32 token rows
+// The multi-stream decode step (one token per stream, 32 streams) on v_mfma_f32_32x32x2_f32: a
+// workgroup owns 32 weight rows over one K slice; its 4 waves take the slice's 64-k blocks in turn
+// (wave w: blocks w, w + 4, ...) and are summed through LDS in wave order at the end.
+// Memory access is what sets the speed here.  The MFMA operand layout puts 32 different rows on the
+// lanes of one load, i.e. 32 B per weight row per instruction, and the memory system moves such
+// loads at ~3 TB/s even with no arithmetic at all; 4 rows x 256 contiguous bytes per instruction
+// reach ~5.4 TB/s.  So both W and X blocks (32 x 64 f32 = 8 KB each) are loaded 4 rows x 256 B per
+// instruction into registers, written to a per-wave LDS block and read back in operand layout (row
+// stride 68 floats: the 16-byte reads of 16 consecutive rows fall on distinct banks).  P blocks of
+// loads are in flight per wave while one block is computed.
+constexpr int kG32Rows = 32;         // weight rows per workgroup (one MFMA block)
+constexpr int kG32Blk = 64;          // k per block
+constexpr int kG32Ls = kG32Blk + 4;  // LDS row stride (floats)
+
+template <int P>
+__global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) float lw[4][kG32Rows * kG32Ls];
+    __shared__ __attribute__((aligned(16))) float lx[4][kG32Rows * kG32Ls];
+    __shared__ int s_last;
+    const int tile = static_cast<int>(blockIdx.x) / p.ks;
+    const int sl = static_cast<int>(blockIdx.x) - tile * p.ks;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int row0 = tile * kG32Rows;
+    const int k_begin = sl * p.slice;
+    const int k_len = min(p.slice, p.K - k_begin);                  // multiple of 64
+    const int n_blk = k_len / kG32Blk;
+    const int my = (n_blk - wave + 3) / 4;                          // this wave's blocks
+    const int last = max(my - 1, 0);
+    // load lanes: row 4 i + lane / 16 of a block (i = 0..7), k 4 (lane % 16) .. + 3; rows past N re-read
+    // the last row and tokens past `rows` the last token (neither is stored)
+    const int lr = lane >> 4, lc = 4 * (lane & 15);
+    const float * wbase = p.W + k_begin + kG32Blk * wave + lc;
+    const float * xbase = p.X + k_begin + kG32Blk * wave + lc;
+    int64_t wrow[8];
+    int xrow[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        wrow[i] = static_cast<int64_t>(min(row0 + 4 * i + lr, p.N - 1)) * p.K;
+        xrow[i] = min(4 * i + lr, p.rows - 1) * p.K;
+    }
+    v4f wr[P][8], xr[P][8];
+    auto load = [&](int u, int b) {
+        const int o = min(b, last) * 4 * kG32Blk;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xr[u][i] = *reinterpret_cast<const v4f *>(xbase + xrow[i] + o);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wr[u][i] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(wbase + wrow[i] + o));
+    };
+    float * myw = lw[wave];
+    float * myx = lx[wave];
+    const int r = lane & 31, h = lane >> 5;
+    v16f acc0 = {}, acc1 = {};
+    auto compute = [&](int u) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            *reinterpret_cast<v4f *>(myw + (4 * i + lr) * kG32Ls + lc) = wr[u][i];
+            *reinterpret_cast<v4f *>(myx + (4 * i + lr) * kG32Ls + lc) = xr[u][i];
+        }
+        // the block is read back by other lanes of this wave: LDS operations of a wave complete in order
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            // MFMA step s: k 16 s + 4 h + j (acc0) and 16 s + 8 + 4 h + j (acc1), j = 0..3 -- the same
+            // permutation of k for the W (A) and X (B) operands
+            const v4f a0 = *reinterpret_cast<const v4f *>(myw + r * kG32Ls + 16 * s + 4 * h);
+            const v4f a1 = *reinterpret_cast<const v4f *>(myw + r * kG32Ls + 16 * s + 8 + 4 * h);
+            const v4f b0 = *reinterpret_cast<const v4f *>(myx + r * kG32Ls + 16 * s + 4 * h);
+            const v4f b1 = *reinterpret_cast<const v4f *>(myx + r * kG32Ls + 16 * s + 8 + 4 * h);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], b0[j], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], b1[j], acc1, 0, 0, 0);
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    };
+    if (my > 0) {
+        const int full = my / P * P;
+#pragma unroll
+        for (int u = 0; u < P; ++u) load(u, u);
+        for (int b0 = 0; b0 < full; b0 += P) {
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                compute(u);
+                load(u, b0 + P + u);
+                // keep the loads of block b + P right behind the arithmetic of block b
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        const int rem = my - full;
+#pragma unroll
+        for (int u = 0; u < P - 1; ++u) {
+            if (u < rem) compute(u);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // sum the 4 waves (wave order) through LDS: wave w then owns accumulator entries 4 w .. 4 w + 3,
+    // i.e. rows 8 w + 4 h + 0..3 of token r (32x32 MFMA output layout)
+    __syncthreads();
+    float * red = &lw[0][0];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) red[(wave * 16 + i) * kWave + lane] = acc0[i] + acc1[i];
+    __syncthreads();
+    v4f s;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float a = red[(4 * wave + j) * kWave + lane];
+#pragma unroll
+        for (int v = 1; v < 4; ++v) a += red[(v * 16 + 4 * wave + j) * kWave + lane];
+        s[j] = a;
+    }
+    const int t = r;
+    const int nr = row0 + 8 * wave + 4 * h;
+    const bool live = t < p.rows && nr < p.N;
+    auto store = [&](v4f v) {
+        float * y = p.Y + static_cast<int64_t>(t) * p.N + nr;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (nr + i < p.N) y[i] = p.accumulate ? y[i] + v[i] : v[i];
+        }
+    };
+    if (p.ks == 1) {
+        if (live) store(s);
+        return;
+    }
+    // publish (partial rows padded to whole 4-row groups), then the last slice of the tile merges in
+    // slice order -- the same protocol as gemm_rows_kernel
+    const int np = (p.N + 3) / 4 * 4;
+    if (live) {
+        uint64_t * q = reinterpret_cast<uint64_t *>(p.partial + (static_cast<int64_t>(sl) * p.rows + t) * np + nr);
+        const uint64_t lo = static_cast<uint64_t>(__float_as_uint(s[0])) | (static_cast<uint64_t>(__float_as_uint(s[1])) << 32);
+        const uint64_t hi = static_cast<uint64_t>(__float_as_uint(s[2])) | (static_cast<uint64_t>(__float_as_uint(s[3])) << 32);
+        __hip_atomic_store(q, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(q + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t * ctr = p.counters + static_cast<int64_t>(tile) * kGrCounterStride;
+        const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == static_cast<uint32_t>(p.ks - 1);
+        if (s_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    const int tt = min(t, p.rows - 1);
+    const int nn = min(nr, np - 4);
+    float sum[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < p.ks; k0 += 8) {
+        uint64_t v[8][2];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int k = min(k0 + u, p.ks - 1);
+            const uint64_t * q = reinterpret_cast<const uint64_t *>(p.partial + (static_cast<int64_t>(k) * p.rows + tt) * np + nn);
+            v[u][0] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            v[u][1] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (k0 + u >= p.ks) break;
+            sum[0] += __uint_as_float(static_cast<uint32_t>(v[u][0]));
+            sum[1] += __uint_as_float(static_cast<uint32_t>(v[u][0] >> 32));
+            sum[2] += __uint_as_float(static_cast<uint32_t>(v[u][1]));
+            sum[3] += __uint_as_float(static_cast<uint32_t>(v[u][1] >> 32));
+        }
+    }
+    if (live) store(v4f{sum[0], sum[1], sum[2], sum[3]});
+}
+
 struct GemmRowsPlan {
     int ks, slice, tiles;
+    bool rows32;     // gemm_rows32_kernel (else gemm_rows_kernel)
+    int depth;       // blocks in flight per wave (gemm_rows32_kernel)
 };
 
 GemmRowsPlan gemm_rows_plan(int32_t N, int32_t K, int32_t rows) {
     GemmRowsPlan pl{};
+    if (rows <= kG32Rows && K % kG32Blk == 0) {
+        // ~256 workgroups at least (one per CU); a K slice keeps >= 4 blocks (one per wave) and at most
+        // 8 slices are merged.  Measured at 32 rows (1.7B shapes): q|k|v 2 slices, o and down 4, gate|up
+        // and the LM head 1.  Two blocks in flight per wave when the grid is one workgroup per CU (the
+        // register file then holds 2 waves per SIMD either way), one when there are more workgroups.
+        pl.rows32 = true;
+        pl.tiles = (N + kG32Rows - 1) / kG32Rows;
+        int ks = std::max(1, std::min({(256 + pl.tiles / 2) / pl.tiles, 8, K / (4 * kG32Blk)}));
+        if (pl.tiles > kGrMaxTiles) ks = 1;                        // counters exist for kGrMaxTiles tiles
+        pl.slice = ((K + ks - 1) / ks + kG32Blk - 1) / kG32Blk * kG32Blk;
+        pl.ks = (K + pl.slice - 1) / pl.slice;
+        pl.depth = pl.tiles * pl.ks <= 256 ? 2 : 1;
+        return pl;
+    }
     pl.tiles = (N + kGrTile - 1) / kGrTile;
     const int rows_pad = (rows + 15) / 16 * 16;
     // ~512 workgroups but at most 8 slices (the merge then takes one round of loads), and the X slice of
@@ -604,6 +793,13 @@ int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int
         const uint64_t cols = static_cast<uint64_t>(k_len / 4);
         return static_cast<uint32_t>(((uint64_t{1} << 32) + cols - 1) / cols);
     };
+    if (pl.rows32) {
+        const dim3 grid(static_cast<unsigned>(pl.tiles * pl.ks));
+        if (pl.depth == 2) hipLaunchKernelGGL((gemm_rows32_kernel<2>), grid, dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((gemm_rows32_kernel<1>), grid, dim3(256), 0, stream, p);
+        QA_LAUNCH_CHECK("gemm_rows32_kernel");
+        return QA_OK;
+    }
     p.x_magic = magic(pl.slice);
     p.x_magic_last = magic(K - (pl.ks - 1) * pl.slice);
     const int tb = (rows + 15) / 16;

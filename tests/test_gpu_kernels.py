@@ -373,7 +373,8 @@ def test_gemv(qa, orc, in_dim, out_dim):
 @pytest.mark.parametrize("out_dim,in_dim,rows", [(4096, 2048, 32), (2048, 2048, 5), (12288, 2048, 32),
                                                   (2048, 6144, 32), (20000, 2048, 32), (100, 1024, 64),
                                                   (2048, 6144, 1), (3000, 3072, 17), (4096, 1024, 49),
-                                                  (1024, 2048, 49), (6144, 1024, 49), (1024, 3072, 49)])
+                                                  (1024, 2048, 49), (6144, 1024, 49), (1024, 3072, 49),
+                                                  (1001, 2048, 32), (512, 192, 7), (151936, 256, 32)])
 def test_gemm_rows(qa, out_dim, in_dim, rows):
     """Skinny f32 MFMA GEMM of the multi-stream decode step against float64, store and accumulate,
     twice on one workspace (slice counters left at zero)."""

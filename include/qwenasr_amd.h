@@ -192,6 +192,20 @@ int qa_qk_prep(float * qkv, int32_t n_tokens, int32_t n_heads, int32_t n_kv_head
 size_t qa_gemm_rows_workspace_bytes(int32_t out_dim, int32_t in_dim, int32_t rows);
 int qa_gemm_rows(const float * W, int32_t out_dim, int32_t in_dim, const float * x, int32_t rows, float * y,
                  int32_t accumulate, void * workspace, size_t workspace_bytes, void * stream);
+/* qa_gemm_rows with the decode step's neighbouring ops fused (rows <= 32, in_dim % 64 == 0), replacing  *
+ * the rms_norm * w before q/k/v and gate/up and the silu * up after gate/up (text-decoder.cpp:92-98,   *
+ * 365-373, 602) and the separate RMSNorm/SwiGLU passes:                                               *
+ *  - norm_w != NULL: x is replaced by RMSNorm(x) * norm_w (eps).  stats_in = [n_stats_in][32] doubles, *
+ *    partial sums of squares of each x row (row r at [k][r]), added in order k = 0, 8, 16, .. then     *
+ *    1, 9, .. (8 interleaved parts), 1 <= n_stats_in <= 128;                                           *
+ *  - stats_out != NULL: [ceil(out_dim / 32)][32] partial sums of squares of each stored y row (after   *
+ *    accumulation), the stats_in of a following normalised GEMM;                                      *
+ *  - swiglu != 0: W = [gate rows; up rows] (out_dim = 2 I, I % 16 == 0), y[rows][I] = silu(g) * u;     *
+ *    needs accumulate == 0 and stats_out == NULL.                                                     */
+int qa_gemm_rows_fused(const float * W, int32_t out_dim, int32_t in_dim, const float * x, int32_t rows,
+                       float * y, int32_t accumulate, const float * norm_w, const double * stats_in,
+                       int32_t n_stats_in, float eps, double * stats_out, int32_t swiglu,
+                       void * workspace, size_t workspace_bytes, void * stream);
 
 /* y[r][o] = sum_i W[o][i] * x[r][i]  (+ y[r][o] when accumulate != 0); rows small (decode).     */
 int qa_gemv(const float * W, int32_t out_dim, int32_t in_dim, const float * x, int32_t rows,

@@ -69,6 +69,7 @@ struct qa_decoder {
     size_t gr_ws_bytes = 0;
     void * pf_ws = nullptr;      // prefill attention: row statistics, split partials, merge counters
     size_t pf_ws_bytes = 0;
+    double * xstats = nullptr;   // [hidden / 32][32] partial sums of squares of the rows of x (fused steps)
     int32_t * d_ids = nullptr;
     int32_t * h_ids = nullptr;   // pinned
     float * staging = nullptr;
@@ -140,6 +141,7 @@ void free_acts(qa_decoder * d) {
     d->gr_ws_bytes = 0;
     d->pf_ws = nullptr;
     d->pf_ws_bytes = 0;
+    d->xstats = nullptr;
 }
 
 // Workspace of the skinny GEMM for the layer projections at up to `rows` token rows and the LM head at
@@ -181,6 +183,10 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
         }
         if (rc == QA_OK) d->gr_ws_bytes = gr;
     }
+    if (rc == QA_OK && rows >= 2) {
+        const size_t n = static_cast<size_t>((H + 31) / 32) * 32;
+        rc = dmalloc(d->act_allocs, n * sizeof(double), reinterpret_cast<void **>(&d->xstats));
+    }
     // prefill attention over up to `rows` tokens (counters cleared once; every call leaves them zero)
     const size_t pf = rows >= 2 ? qa_prefill_attn_workspace_bytes(rows, d->cfg.n_heads) : 0;
     if (rc == QA_OK && pf > 0) {
@@ -216,6 +222,37 @@ int sgemm(qa_decoder * d, const float * W, int32_t out_dim, int32_t in_dim, cons
     return QA_OK;
 }
 
+// The multi-stream decode step (2..32 streams) runs its projections on the 32-row skinny GEMM with the
+// RMSNorms and the SwiGLU fused in: the residual GEMMs (o, down) and the embedding gather leave the
+// per-row sums of squares of x in d->xstats, the normalised GEMMs (q|k|v, gate|up, LM head) read them.
+bool fused_rows(const qa_decoder * d, int32_t rows) {
+    const qa_text_config & c = d->cfg;
+    const int32_t H = c.hidden, QD = c.n_heads * kHeadDim, KD = c.n_kv_heads * kHeadDim, I = c.intermediate;
+    return rows >= 2 && d->xstats && (H + 31) / 32 <= 128 && (2 * I) % 32 == 0 &&
+           gemm_rows_fusable(QD + 2 * KD, H, rows) && gemm_rows_fusable(H, QD, rows) &&
+           gemm_rows_fusable(2 * I, H, rows) && gemm_rows_fusable(H, I, rows) && gemm_rows_fusable(c.vocab, H, rows);
+}
+
+int fused_gemm(qa_decoder * d, const float * W, int32_t N, int32_t K, const float * X, int32_t rows, float * Y,
+               bool accumulate, const GemmRowsFusion & f) {
+    return gemm_rows_launch(W, N, K, X, rows, Y, accumulate, d->gr_ws, d->gr_ws_bytes, d->stream, &f);
+}
+
+GemmRowsFusion norm_in(const qa_decoder * d, const float * norm_w) {
+    GemmRowsFusion f;
+    f.norm_w = norm_w;
+    f.stats_in = d->xstats;
+    f.n_stats_in = (d->cfg.hidden + 31) / 32;
+    f.eps = d->cfg.rms_norm_eps;
+    return f;
+}
+
+GemmRowsFusion stats_out(const qa_decoder * d) {
+    GemmRowsFusion f;
+    f.stats_out = d->xstats;
+    return f;
+}
+
 int32_t host_max_len(const qa_decoder * d, int32_t n, int32_t add) {
     int32_t m = 0;
     for (int32_t s = 0; s < n; ++s) m = std::max(m, d->cur_len[s] + add);
@@ -226,7 +263,8 @@ int32_t host_max_len(const qa_decoder * d, int32_t n, int32_t add) {
 //   kDecode : rows = number of streams (one token each), positions d_lens[s], keys [0, d_lens[s] + 1)
 //   kPrefill: rows = T tokens of stream 0 at positions n_past.., keys [0, n_past + t]
 //   kNoCache: rows = T tokens, positions 0..T-1, f32 K/V never stored
-int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past, int32_t max_len = 0) {
+int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past, int32_t max_len = 0,
+              bool fused = false) {
     const qa_text_config & c = d->cfg;
     const DevLayer & L = d->layers[l];
     const int32_t H = c.hidden, QD = c.n_heads * kHeadDim, KD = c.n_kv_heads * kHeadDim, I = c.intermediate;
@@ -237,6 +275,8 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
         Prof pr(d, kFamProj);
         if (rows == 1) {
             rc = gemv_launch(kEpiStoreOp, true, L.qkv, W3, H, d->x, d->qkv, L.attn_norm, c.rms_norm_eps, s);
+        } else if (fused) {
+            rc = fused_gemm(d, L.qkv, W3, H, d->x, rows, d->qkv, false, norm_in(d, L.attn_norm));
         } else {
             rc = rmsnorm_rows_launch(d->x, L.attn_norm, rows, H, c.rms_norm_eps, d->xn, s);
             if (rc == QA_OK) rc = sgemm(d, L.qkv, W3, H, d->xn, rows, d->qkv, 0.0f);
@@ -278,6 +318,12 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
         rc = gemv_launch(kEpiAccumOp, false, L.o, H, QD, d->attn, d->x, nullptr, 0.0f, s);
         if (rc == QA_OK) rc = gemv_launch(kEpiSwigluOp, true, L.gu, I, H, d->x, d->act, L.ffn_norm, c.rms_norm_eps, s);
         if (rc == QA_OK) rc = gemv_launch(kEpiAccumOp, false, L.down, H, I, d->act, d->x, nullptr, 0.0f, s);
+    } else if (fused) {
+        GemmRowsFusion gu = norm_in(d, L.ffn_norm);
+        gu.swiglu = true;
+        rc = fused_gemm(d, L.o, H, QD, d->attn, rows, d->x, true, stats_out(d));
+        if (rc == QA_OK) rc = fused_gemm(d, L.gu, 2 * I, H, d->x, rows, d->act, false, gu);
+        if (rc == QA_OK) rc = fused_gemm(d, L.down, H, I, d->act, rows, d->x, true, stats_out(d));
     } else {
         rc = sgemm(d, L.o, H, QD, d->attn, rows, d->x, 1.0f);
         if (rc == QA_OK) rc = rmsnorm_rows_launch(d->x, L.ffn_norm, rows, H, c.rms_norm_eps, d->xn, s);
@@ -289,7 +335,7 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
 }
 
 // Logits of `rows` rows starting at row `first` of d->x into d->logits[0..rows), then greedy ids.
-int logits_and_pick(qa_decoder * d, int32_t first, int32_t rows, bool pick) {
+int logits_and_pick(qa_decoder * d, int32_t first, int32_t rows, bool pick, bool fused = false) {
     const qa_text_config & c = d->cfg;
     if (!d->out_w || !d->out_norm) return fail(QA_ERR_INVALID, "decoder has no output weights");
     int rc;
@@ -299,6 +345,8 @@ int logits_and_pick(qa_decoder * d, int32_t first, int32_t rows, bool pick) {
         if (rows == 1) {
             rc = gemv_launch(kEpiStoreOp, true, d->out_w, c.vocab, c.hidden, xr, d->logits, d->out_norm,
                              c.rms_norm_eps, d->stream);
+        } else if (fused && first == 0) {
+            rc = fused_gemm(d, d->out_w, c.vocab, c.hidden, xr, rows, d->logits, false, norm_in(d, d->out_norm));
         } else {
             rc = rmsnorm_rows_launch(xr, d->out_norm, rows, c.hidden, c.rms_norm_eps, d->xn, d->stream);
             if (rc == QA_OK) rc = sgemm(d, d->out_w, c.vocab, c.hidden, d->xn, rows, d->logits, 0.0f);
@@ -338,9 +386,13 @@ int forward_device(qa_decoder * d, int32_t n_tokens, int32_t n_past, bool pick) 
 // layer (fused append + attention at position d_lens[s]), LM head, greedy pick into d_ids, and
 // d_lens[s] += 1.  Only device memory is read for lengths and ids, so the sequence is capturable.
 int decode_step_ops(qa_decoder * d, int32_t rows, int32_t max_len) {
-    int rc = embed_rows_launch(d->embd, d->cfg.vocab, d->cfg.hidden, d->d_ids, rows, d->x, d->stream);
-    for (int32_t l = 0; l < d->cfg.n_layers && rc == QA_OK; ++l) rc = run_layer(d, l, rows, kDecode, 0, max_len);
-    if (rc == QA_OK) rc = logits_and_pick(d, 0, rows, true);
+    const bool fused = fused_rows(d, rows);
+    int rc = embed_rows_launch(d->embd, d->cfg.vocab, d->cfg.hidden, d->d_ids, rows, d->x, d->stream,
+                               fused ? d->xstats : nullptr);
+    for (int32_t l = 0; l < d->cfg.n_layers && rc == QA_OK; ++l) {
+        rc = run_layer(d, l, rows, kDecode, 0, max_len, fused);
+    }
+    if (rc == QA_OK) rc = logits_and_pick(d, 0, rows, true, fused);
     if (rc == QA_OK) rc = advance_lens_launch(d->d_lens, rows, 1, d->stream);
     return rc;
 }

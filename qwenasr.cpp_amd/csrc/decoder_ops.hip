@@ -227,6 +227,12 @@ struct GemmRowsParams {
     int32_t N, K, rows, ks, slice, accumulate;
     uint32_t x_magic;         // ceil(2^32 / (slice / 4)): X staging index / vectors per token row
     uint32_t x_magic_last;    // the same for the last slice (K - (ks - 1) slice)
+    // fusions of gemm_rows32_kernel (null / 0: none)
+    const float * norm_w;     // X is RMSNorm(X) * norm_w, with the row sums of squares in stats_in
+    const double * stats_in;  // [n_stats_in][32]: partial sums of squares of each X row (summed in order)
+    double * stats_out;       // [tiles][32]: sums of squares of each stored Y row over the tile's 32 columns
+    int32_t n_stats_in, swiglu;
+    float eps;
 };
 
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -433,6 +439,8 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
 #pragma clang fp contract(off)
     __shared__ __attribute__((aligned(16))) float lw[4][kG32Rows * kG32Ls];
     __shared__ __attribute__((aligned(16))) float lx[4][kG32Rows * kG32Ls];
+    __shared__ double s_part[8][32];
+    __shared__ float s_scale[32];
     __shared__ int s_last;
     const int tile = static_cast<int>(blockIdx.x) / p.ks;
     const int sl = static_cast<int>(blockIdx.x) - tile * p.ks;
@@ -444,26 +452,69 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
     const int n_blk = k_len / kG32Blk;
     const int my = (n_blk - wave + 3) / 4;                          // this wave's blocks
     const int last = max(my - 1, 0);
+    const bool prenorm = p.norm_w != nullptr;
+    // RMSNorm input: thread (token tid % 32, part tid / 32) loads the partial sums of squares k = part,
+    // part + 8, ... (at most 16: K <= 4096 with 32-column partials) before any weight load
+    double sq[16];
+    if (prenorm) {
+        const int tk = threadIdx.x & 31, part = threadIdx.x >> 5;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int k = min(part + 8 * j, p.n_stats_in - 1);
+            sq[j] = p.stats_in[32 * k + tk];
+        }
+    }
     // load lanes: row 4 i + lane / 16 of a block (i = 0..7), k 4 (lane % 16) .. + 3; rows past N re-read
-    // the last row and tokens past `rows` the last token (neither is stored)
+    // the last row and tokens past `rows` the last token (neither is stored).  SwiGLU tiles hold 16
+    // gate rows and the 16 matching up rows (W = [gate rows; up rows], N = 2 I).
     const int lr = lane >> 4, lc = 4 * (lane & 15);
     const float * wbase = p.W + k_begin + kG32Blk * wave + lc;
     const float * xbase = p.X + k_begin + kG32Blk * wave + lc;
+    const float * nbase = prenorm ? p.norm_w + k_begin + kG32Blk * wave + lc : nullptr;
     int64_t wrow[8];
     int xrow[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        wrow[i] = static_cast<int64_t>(min(row0 + 4 * i + lr, p.N - 1)) * p.K;
-        xrow[i] = min(4 * i + lr, p.rows - 1) * p.K;
+        const int line = 4 * i + lr;
+        const int wr_row = p.swiglu ? (line < 16 ? 16 * tile + line : (p.N >> 1) + 16 * tile + line - 16) : row0 + line;
+        wrow[i] = static_cast<int64_t>(min(wr_row, p.N - 1)) * p.K;
+        xrow[i] = min(line, p.rows - 1) * p.K;
     }
-    v4f wr[P][8], xr[P][8];
+    v4f wr[P][8], xr[P][8], nw[P];
     auto load = [&](int u, int b) {
         const int o = min(b, last) * 4 * kG32Blk;
 #pragma unroll
         for (int i = 0; i < 8; ++i) xr[u][i] = *reinterpret_cast<const v4f *>(xbase + xrow[i] + o);
+        if (prenorm) nw[u] = *reinterpret_cast<const v4f *>(nbase + o);
 #pragma unroll
         for (int i = 0; i < 8; ++i) wr[u][i] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(wbase + wrow[i] + o));
     };
+    if (my > 0) {
+#pragma unroll
+        for (int u = 0; u < P; ++u) load(u, u);
+    }
+    float sc[8];
+    if (prenorm) {
+        // rms_norm_row (text-decoder.cpp:542-557): sum of squares in double, float scale, (x * scale) * w;
+        // partial sums are added in a fixed order (k = part + 8 j by j, then the 8 parts in order)
+        const int tk = threadIdx.x & 31, part = threadIdx.x >> 5;
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            if (part + 8 * j < p.n_stats_in) ss += sq[j];
+        }
+        s_part[part][tk] = ss;
+        __syncthreads();
+        if (threadIdx.x < 32) {
+            double tot = 0.0;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) tot += s_part[q][threadIdx.x];
+            s_scale[threadIdx.x] = 1.0f / sqrtf(static_cast<float>(tot / static_cast<double>(p.K)) + p.eps);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sc[i] = s_scale[min(4 * i + lr, p.rows - 1)];
+    }
     float * myw = lw[wave];
     float * myx = lx[wave];
     const int r = lane & 31, h = lane >> 5;
@@ -471,8 +522,13 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
     auto compute = [&](int u) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
+            v4f xv = xr[u][i];
+            if (prenorm) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xv[e] = xv[e] * sc[i] * nw[u][e];
+            }
             *reinterpret_cast<v4f *>(myw + (4 * i + lr) * kG32Ls + lc) = wr[u][i];
-            *reinterpret_cast<v4f *>(myx + (4 * i + lr) * kG32Ls + lc) = xr[u][i];
+            *reinterpret_cast<v4f *>(myx + (4 * i + lr) * kG32Ls + lc) = xv;
         }
         // the block is read back by other lanes of this wave: LDS operations of a wave complete in order
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -494,8 +550,6 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
     };
     if (my > 0) {
         const int full = my / P * P;
-#pragma unroll
-        for (int u = 0; u < P; ++u) load(u, u);
         for (int b0 = 0; b0 < full; b0 += P) {
 #pragma unroll
             for (int u = 0; u < P; ++u) {
@@ -512,33 +566,70 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    // sum the 4 waves (wave order) through LDS: wave w then owns accumulator entries 4 w .. 4 w + 3,
-    // i.e. rows 8 w + 4 h + 0..3 of token r (32x32 MFMA output layout)
+    // sum the 4 waves (wave order) through LDS: accumulator entry i of lane (r, h) is row
+    // 8 (i / 4) + 4 h + i % 4 of token r (32x32 MFMA output layout)
     __syncthreads();
     float * red = &lw[0][0];
 #pragma unroll
     for (int i = 0; i < 16; ++i) red[(wave * 16 + i) * kWave + lane] = acc0[i] + acc1[i];
     __syncthreads();
+    auto entry = [&](int i) {
+        float a = red[i * kWave + lane];
+#pragma unroll
+        for (int v = 1; v < 4; ++v) a += red[(v * 16 + i) * kWave + lane];
+        return a;
+    };
+    const int t = r;
+    if (p.swiglu) {
+        // one slice (ks = 1): waves 0 and 1 own gate rows 8 w + 4 h + 0..3 (entries 4 w + j) and their up
+        // rows 16 + 8 w + 4 h + 0..3 (entries 4 w + 8 + j); silu(gate) * up as text-decoder.cpp:602
+        if (wave < 2 && t < p.rows) {
+            const int I = p.N >> 1;
+            const int c = 16 * tile + 8 * wave + 4 * h;
+            float * y = p.Y + static_cast<int64_t>(t) * I + c;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float g = entry(4 * wave + j), u = entry(4 * wave + 8 + j);
+                if (c + j < I) y[j] = (g / (1.0f + expf(-g))) * u;
+            }
+        }
+        return;
+    }
+    // wave w owns entries 4 w .. 4 w + 3: rows 8 w + 4 h + 0..3 of token r
     v4f s;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        float a = red[(4 * wave + j) * kWave + lane];
-#pragma unroll
-        for (int v = 1; v < 4; ++v) a += red[(v * 16 + 4 * wave + j) * kWave + lane];
-        s[j] = a;
-    }
-    const int t = r;
+    for (int j = 0; j < 4; ++j) s[j] = entry(4 * wave + j);
     const int nr = row0 + 8 * wave + 4 * h;
     const bool live = t < p.rows && nr < p.N;
-    auto store = [&](v4f v) {
-        float * y = p.Y + static_cast<int64_t>(t) * p.N + nr;
+    // store (or accumulate) the final values; with stats_out also the tile's per-token sum of squares of
+    // the stored values (a workgroup-uniform step: every thread of the workgroup calls it)
+    auto finish = [&](v4f v) {
+        double ss = 0.0;
+        if (live) {
+            float * y = p.Y + static_cast<int64_t>(t) * p.N + nr;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (nr + i < p.N) y[i] = p.accumulate ? y[i] + v[i] : v[i];
+            for (int i = 0; i < 4; ++i) {
+                if (nr + i < p.N) {
+                    const float o = p.accumulate ? y[i] + v[i] : v[i];
+                    y[i] = o;
+                    ss += static_cast<double>(o) * o;
+                }
+            }
+        }
+        if (p.stats_out) {
+            double * sst = &s_part[0][0];                           // [4 waves][2 halves][32 tokens]
+            sst[(2 * wave + h) * 32 + t] = ss;
+            __syncthreads();
+            if (threadIdx.x < 32) {
+                double tot = 0.0;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) tot += sst[q * 32 + threadIdx.x];
+                p.stats_out[32 * tile + threadIdx.x] = tot;
+            }
         }
     };
     if (p.ks == 1) {
-        if (live) store(s);
+        finish(s);
         return;
     }
     // publish (partial rows padded to whole 4-row groups), then the last slice of the tile merges in
@@ -582,7 +673,7 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
             sum[3] += __uint_as_float(static_cast<uint32_t>(v[u][1] >> 32));
         }
     }
-    if (live) store(v4f{sum[0], sum[1], sum[2], sum[3]});
+    finish(v4f{sum[0], sum[1], sum[2], sum[3]});
 }
 
 struct GemmRowsPlan {
@@ -591,7 +682,7 @@ struct GemmRowsPlan {
     int depth;       // blocks in flight per wave (gemm_rows32_kernel)
 };
 
-GemmRowsPlan gemm_rows_plan(int32_t N, int32_t K, int32_t rows) {
+GemmRowsPlan gemm_rows_plan(int32_t N, int32_t K, int32_t rows, bool one_slice = false) {
     GemmRowsPlan pl{};
     if (rows <= kG32Rows && K % kG32Blk == 0) {
         // ~256 workgroups at least (one per CU); a K slice keeps >= 4 blocks (one per wave) and at most
@@ -601,7 +692,7 @@ GemmRowsPlan gemm_rows_plan(int32_t N, int32_t K, int32_t rows) {
         pl.rows32 = true;
         pl.tiles = (N + kG32Rows - 1) / kG32Rows;
         int ks = std::max(1, std::min({(256 + pl.tiles / 2) / pl.tiles, 8, K / (4 * kG32Blk)}));
-        if (pl.tiles > kGrMaxTiles) ks = 1;                        // counters exist for kGrMaxTiles tiles
+        if (pl.tiles > kGrMaxTiles || one_slice) ks = 1;           // counters exist for kGrMaxTiles tiles
         pl.slice = ((K + ks - 1) / ks + kG32Blk - 1) / kG32Blk * kG32Blk;
         pl.ks = (K + pl.slice - 1) / pl.slice;
         pl.depth = pl.tiles * pl.ks <= 256 ? 2 : 1;
@@ -658,16 +749,26 @@ __global__ void add_inplace_kernel(float * y, const float * x, size_t n) {
     }
 }
 
-__global__ void embed_rows_kernel(const float * table, int n_rows, int dim, const int32_t * ids, float * out) {
+// stats (optional): stats[k][r] = sum of squares of columns 32 k .. 32 k + 31 of row r (the partial
+// layout gemm_rows32_kernel takes for its RMSNorm input; r < 32)
+__global__ void embed_rows_kernel(const float * table, int n_rows, int dim, const int32_t * ids, float * out,
+                                  double * stats) {
     const int r = blockIdx.x;
     const int id = ids[r];
     float * o = out + static_cast<int64_t>(r) * dim;
-    if (id < 0 || id >= n_rows) {
-        for (int i = threadIdx.x; i < dim; i += blockDim.x) o[i] = 0.0f;
-        return;
+    const bool valid = id >= 0 && id < n_rows;
+    const float * t = table + static_cast<int64_t>(valid ? id : 0) * dim;
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) o[i] = valid ? t[i] : 0.0f;
+    if (stats) {
+        for (int k = threadIdx.x; 32 * k < dim; k += blockDim.x) {
+            double ss = 0.0;
+            for (int i = 32 * k; i < min(32 * k + 32, dim); ++i) {
+                const float v = valid ? t[i] : 0.0f;
+                ss += static_cast<double>(v) * v;
+            }
+            stats[32 * k + r] = ss;
+        }
     }
-    const float * t = table + static_cast<int64_t>(id) * dim;
-    for (int i = threadIdx.x; i < dim; i += blockDim.x) o[i] = t[i];
 }
 
 __global__ void advance_lens_kernel(int32_t * lens, int n, int delta) {
@@ -768,13 +869,27 @@ size_t gemm_rows_workspace_bytes(int32_t N, int32_t K, int32_t rows) {
     return kGrCounterBytes + partial;
 }
 
+bool gemm_rows_fusable(int32_t N, int32_t K, int32_t rows) {
+    return N > 0 && N <= kGrMaxTiles * kGrTile && rows >= 1 && rows <= kG32Rows && K > 0 && K % kG32Blk == 0;
+}
+
 int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int32_t rows, float * Y, bool accumulate,
-                     void * workspace, size_t workspace_bytes, hipStream_t stream) {
+                     void * workspace, size_t workspace_bytes, hipStream_t stream, const GemmRowsFusion * fusion) {
     if (!W || !X || !Y || N <= 0 || N > kGrMaxTiles * kGrTile || K <= 0 || K % 32 != 0 || rows < 1 ||
         rows > kGrMaxRows) {
         return fail(QA_ERR_INVALID, "gemm_rows: invalid shape");
     }
-    const GemmRowsPlan pl = gemm_rows_plan(N, K, rows);
+    const bool fused = fusion && (fusion->norm_w || fusion->stats_out || fusion->swiglu);
+    if (fused) {
+        if (!gemm_rows_fusable(N, K, rows)) return fail(QA_ERR_INVALID, "gemm_rows: fusions need <= 32 rows, K % 64 == 0");
+        if (fusion->norm_w && (!fusion->stats_in || fusion->n_stats_in < 1 || fusion->n_stats_in > 128)) {
+            return fail(QA_ERR_INVALID, "gemm_rows: RMSNorm input needs 1..128 partial sums per row");
+        }
+        if (fusion->swiglu && (N % 32 != 0 || accumulate || fusion->stats_out)) {
+            return fail(QA_ERR_INVALID, "gemm_rows: SwiGLU needs N = 2 I with I % 16 == 0 and a plain store");
+        }
+    }
+    const GemmRowsPlan pl = gemm_rows_plan(N, K, rows, fused && fusion->swiglu);
     const size_t need = gemm_rows_workspace_bytes(N, K, rows);
     if (!workspace || workspace_bytes < need) return fail(QA_ERR_INVALID, "gemm_rows: workspace too small");
     GemmRowsParams p{};
@@ -793,6 +908,14 @@ int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int
         const uint64_t cols = static_cast<uint64_t>(k_len / 4);
         return static_cast<uint32_t>(((uint64_t{1} << 32) + cols - 1) / cols);
     };
+    if (fused) {
+        p.norm_w = fusion->norm_w;
+        p.stats_in = fusion->stats_in;
+        p.n_stats_in = fusion->n_stats_in;
+        p.eps = fusion->eps;
+        p.stats_out = fusion->stats_out;
+        p.swiglu = fusion->swiglu ? 1 : 0;
+    }
     if (pl.rows32) {
         const dim3 grid(static_cast<unsigned>(pl.tiles * pl.ks));
         if (pl.depth == 2) hipLaunchKernelGGL((gemm_rows32_kernel<2>), grid, dim3(256), 0, stream, p);
@@ -850,10 +973,11 @@ int swiglu_rows_launch(const float * gu, int32_t rows, int32_t dim, float * a, h
 }
 
 int embed_rows_launch(const float * table, int32_t n_rows, int32_t dim, const int32_t * ids, int32_t rows,
-                      float * out, hipStream_t stream) {
+                      float * out, hipStream_t stream, double * stats) {
     if (rows <= 0) return QA_OK;
+    if (stats && rows > 32) return fail(QA_ERR_INVALID, "embed_rows: row statistics cover at most 32 rows");
     hipLaunchKernelGGL(embed_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, table, n_rows,
-                       dim, ids, out);
+                       dim, ids, out, stats);
     QA_LAUNCH_CHECK("embed_rows_kernel");
     return QA_OK;
 }
@@ -971,4 +1095,19 @@ extern "C" int qa_gemm_rows(const float * W, int32_t out_dim, int32_t in_dim, co
                             int32_t accumulate, void * workspace, size_t workspace_bytes, void * stream) {
     return qa::gemm_rows_launch(W, out_dim, in_dim, x, rows, y, accumulate != 0, workspace, workspace_bytes,
                                 qa::as_stream(stream));
+}
+
+extern "C" int qa_gemm_rows_fused(const float * W, int32_t out_dim, int32_t in_dim, const float * x, int32_t rows,
+                                  float * y, int32_t accumulate, const float * norm_w, const double * stats_in,
+                                  int32_t n_stats_in, float eps, double * stats_out, int32_t swiglu,
+                                  void * workspace, size_t workspace_bytes, void * stream) {
+    qa::GemmRowsFusion f;
+    f.norm_w = norm_w;
+    f.stats_in = stats_in;
+    f.n_stats_in = n_stats_in;
+    f.eps = eps;
+    f.stats_out = stats_out;
+    f.swiglu = swiglu != 0;
+    return qa::gemm_rows_launch(W, out_dim, in_dim, x, rows, y, accumulate != 0, workspace, workspace_bytes,
+                                qa::as_stream(stream), &f);
 }

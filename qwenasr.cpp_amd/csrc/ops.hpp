@@ -11,16 +11,32 @@ int gemv_launch(int epi, bool prenorm, const float * W, int32_t out_dim, int32_t
                 const float * norm_w, float eps, hipStream_t stream);
 // Y[rows][N] (+)= X[rows][K] W[N][K]^T for 1..64 rows (K a multiple of 32), f32 MFMA.
 size_t gemm_rows_workspace_bytes(int32_t N, int32_t K, int32_t rows);
+// Fusions of the <= 32-row kernel (gemm_rows_fusable):
+//  - norm_w: X is replaced by RMSNorm(X) * norm_w; the per-row sums of squares come as n_stats_in
+//    partials [n_stats_in][32] (double), e.g. the stats_out of the GEMM that produced X;
+//  - stats_out: [ceil(N / 32)][32] partial sums of squares of the stored rows of Y (after accumulation);
+//  - swiglu: W = [gate rows; up rows] (N = 2 I, I % 16 == 0), Y = silu(gate) * up, [rows][I].
+struct GemmRowsFusion {
+    const float * norm_w = nullptr;
+    const double * stats_in = nullptr;
+    int32_t n_stats_in = 0;
+    float eps = 0.0f;
+    double * stats_out = nullptr;
+    bool swiglu = false;
+};
+bool gemm_rows_fusable(int32_t N, int32_t K, int32_t rows);
 int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int32_t rows, float * Y, bool accumulate,
-                     void * workspace, size_t workspace_bytes, hipStream_t stream);
+                     void * workspace, size_t workspace_bytes, hipStream_t stream,
+                     const GemmRowsFusion * fusion = nullptr);
 size_t argmax_workspace_bytes(int32_t rows);
 int argmax_launch(const float * logits, int32_t rows, int32_t vocab, int32_t * ids, void * workspace,
                   hipStream_t stream);
 int rmsnorm_rows_launch(const float * x, const float * w, int32_t rows, int32_t dim, float eps, float * y,
                         hipStream_t stream);
 int swiglu_rows_launch(const float * gu, int32_t rows, int32_t dim, float * a, hipStream_t stream);
+// stats (optional, rows <= 32): [ceil(dim / 32)][32] partial sums of squares of each gathered row
 int embed_rows_launch(const float * table, int32_t n_rows, int32_t dim, const int32_t * ids, int32_t rows,
-                      float * out, hipStream_t stream);
+                      float * out, hipStream_t stream, double * stats = nullptr);
 int advance_lens_launch(int32_t * lens, int32_t n, int32_t delta, hipStream_t stream);
 int set_values_launch(int32_t * dst, int32_t n, int32_t value, hipStream_t stream);
 int cast_rows_launch(const float * src, void * dst, int32_t cache_type, int64_t n, hipStream_t stream);

@@ -397,6 +397,72 @@ def test_gemm_rows(qa, out_dim, in_dim, rows):
         np.testing.assert_allclose(got, expect, rtol=1e-4, atol=2e-4)
 
 
+def _row_stats(y, n_out):
+    """[ceil(n_out / 32)][32] float64 partial sums of squares of each row over 32-column groups."""
+    rows = y.shape[0]
+    st = np.zeros(((n_out + 31) // 32, 32))
+    for k in range(st.shape[0]):
+        st[k, :rows] = np.sum(y[:, 32 * k:32 * k + 32].astype(np.float64) ** 2, axis=1)
+    return st
+
+
+@pytest.mark.parametrize("out_dim,in_dim,rows", [(4096, 2048, 32), (2048, 2048, 7), (12288, 2048, 32),
+                                                  (2048, 6144, 32), (1056, 1024, 5)])
+def test_gemm_rows_fused(qa, out_dim, in_dim, rows):
+    """Fused skinny GEMM against float64: RMSNorm input from partial sums of squares (the normalised
+    row computed in f32 as the RMSNorm kernel does), accumulate + sums of squares of the stored rows,
+    and the SwiGLU epilogue over [gate rows; up rows]."""
+    rng = np.random.default_rng(out_dim * 3 + in_dim + rows)
+    eps = np.float32(1e-6)
+    w = (rng.standard_normal((out_dim, in_dim)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((rows, in_dim)).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(in_dim)).astype(np.float32)
+    y0 = rng.standard_normal((rows, out_dim)).astype(np.float32)
+    st_in = _row_stats(x, in_dim)
+    # reference normalisation: scale = 1 / sqrtf(float(ss / K) + eps), xn = (x * scale) * w in f32
+    ss = np.sum(x.astype(np.float64) ** 2, axis=1)
+    scale = (np.float32(1.0) / np.sqrt((ss / in_dim).astype(np.float32) + eps)).astype(np.float32)
+    xn = ((x * scale[:, None]).astype(np.float32) * nw[None, :]).astype(np.float32)
+    d_w, d_x, d_nw, d_st = dev(qa, w), dev(qa, x), dev(qa, nw), dev(qa, st_in)
+    if st_in.shape[0] > 128:        # the RMSNorm input takes at most 128 partials (in_dim <= 4096)
+        xn, d_nw, d_st = x, None, None
+    wsb = qa.lib.qa_gemm_rows_workspace_bytes(out_dim, in_dim, rows)
+    ws = zeros(qa, wsb, np.uint8)
+    d_so = zeros(qa, ((out_dim + 31) // 32, 32), np.float64)
+    print(f"gemm_rows_fused {out_dim}x{in_dim} rows={rows}", flush=True)
+    # RMSNorm input, accumulate, statistics out
+    d_y = dev(qa, y0)
+    ptr = lambda a: a.ptr if a is not None else None
+    qa.check(qa.lib.qa_gemm_rows_fused(d_w.ptr, out_dim, in_dim, d_x.ptr, rows, d_y.ptr, 1, ptr(d_nw), ptr(d_st),
+                                       st_in.shape[0], eps, d_so.ptr, 0, ws.ptr, wsb, NULL_STREAM))
+    qa.synchronize()
+    got = d_y.numpy()
+    np.testing.assert_allclose(got, y0 + xn.astype(np.float64) @ w.astype(np.float64).T, rtol=1e-4, atol=2e-4)
+    np.testing.assert_allclose(d_so.numpy()[:, :rows], _row_stats(got, out_dim)[:, :rows], rtol=1e-12, atol=0)
+    # SwiGLU epilogue: W = [gate; up]
+    if out_dim % 32 == 0:
+        half = out_dim // 2
+        d_a = zeros(qa, (rows, half))
+        qa.check(qa.lib.qa_gemm_rows_fused(d_w.ptr, out_dim, in_dim, d_x.ptr, rows, d_a.ptr, 0, ptr(d_nw),
+                                           ptr(d_st), st_in.shape[0], eps, None, 1, ws.ptr, wsb, NULL_STREAM))
+        qa.synchronize()
+        gu = xn.astype(np.float64) @ w.astype(np.float64).T
+        g, u = gu[:, :half], gu[:, half:]
+        np.testing.assert_allclose(d_a.numpy(), g / (1.0 + np.exp(-g)) * u, rtol=1e-4, atol=2e-4)
+
+
+def test_gemm_rows_fused_rejects_bad_arguments(qa):
+    d = zeros(qa, 1 << 16)
+    ws = zeros(qa, qa.lib.qa_gemm_rows_workspace_bytes(64, 1024, 40), np.uint8)
+    # more than 32 rows, or an odd SwiGLU split, or no statistics for the RMSNorm input
+    assert qa.lib.qa_gemm_rows_fused(d.ptr, 64, 1024, d.ptr, 40, d.ptr, 0, d.ptr, d.ptr, 32, 1e-6, None, 0,
+                                     ws.ptr, ws.nbytes, NULL_STREAM) == qa.QA_ERR_INVALID
+    assert qa.lib.qa_gemm_rows_fused(d.ptr, 48, 1024, d.ptr, 4, d.ptr, 0, None, None, 0, 0.0, None, 1,
+                                     ws.ptr, ws.nbytes, NULL_STREAM) == qa.QA_ERR_INVALID
+    assert qa.lib.qa_gemm_rows_fused(d.ptr, 64, 1024, d.ptr, 4, d.ptr, 0, d.ptr, None, 0, 1e-6, None, 0,
+                                     ws.ptr, ws.nbytes, NULL_STREAM) == qa.QA_ERR_INVALID
+
+
 def test_gemm_rows_shared_workspace(qa):
     """One workspace, sized for the largest shape, serves a sequence of different shapes (as in a
     decoder layer) with no clearing: counters and partials never overlap across shapes."""

@@ -161,6 +161,35 @@ def test_config4_ragged_streams_match_golden(qa):
         assert [dec.cur_len(s) for s in range(w.streams)] == (lens + w.steps).tolist()
 
 
+@pytest.mark.parametrize("n_streams", [2, 5, 32])
+def test_few_streams_match_oracle(qa, orc, n_streams):
+    """The multi-stream decode step at 2..32 streams (fused RMSNorm / SwiGLU skinny GEMMs, per-stream
+    lengths) against the oracle decoding each stream alone: 0.6B shapes, 2 layers, f16 cache, ragged
+    contexts, 4 greedy steps; ids identical up to an oracle near-tie."""
+    from qwenasr_amd import configs
+
+    model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=2)
+    om = orc.OracleModel.from_product_model(model)
+    rng = np.random.default_rng(n_streams)
+    lens = rng.integers(20, 180, n_streams)
+    first = rng.integers(0, model.cfg.vocab, n_streams).astype(np.int32)
+    steps, cap = 4, 200
+    with qa.Decoder(model, n_streams, cap, qa.QA_CACHE_F16) as dec:
+        refs = []
+        for s in range(n_streams):
+            k, v = configs.cfg4_stream_kv(1000 + s, int(lens[s]), n_layers=2)
+            dec.fill_cache(s, k, v, int(lens[s]))
+            cache = om.cache(cap, True)
+            cache.fill(k, v, int(lens[s]))
+            ids, margins, runner = om.decode_steps(cache, int(first[s]), steps)
+            refs.append((list(ids), list(margins), list(runner)))
+        print(f"{n_streams} streams: oracle done", flush=True)
+        got = dec.decode_streams(first, steps)
+        for s in range(n_streams):
+            assert_greedy_match(got[:, s].tolist(), *refs[s], f"stream {s}")
+        assert dec.device_lens().tolist() == (lens + steps).tolist()
+
+
 def test_decoders_in_sequence_see_cleared_memory(qa):
     """Decoders created one after another in one process, each over memory just released by a buffer
     full of f16 NaN patterns (0xFF bytes), decode identical valid ids: the cache and workspace clears

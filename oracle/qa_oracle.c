@@ -73,8 +73,15 @@ void orc_f32_to_f16_array(const float * x, uint16_t * h, size_t n) {
     for (size_t i = 0; i < n; ++i) h[i] = orc_f32_to_f16(x[i]);
 }
 
+/* Every f16 bit pattern's f32 value (the conversion is exact), filled once at load time. */
+static float f16_table[65536];
+
+__attribute__((constructor)) static void fill_f16_table(void) {
+    for (uint32_t b = 0; b < 65536u; ++b) f16_table[b] = orc_f16_to_f32((uint16_t)b);
+}
+
 void orc_f16_to_f32_array(const uint16_t * h, float * x, size_t n) {
-    for (size_t i = 0; i < n; ++i) x[i] = orc_f16_to_f32(h[i]);
+    for (size_t i = 0; i < n; ++i) x[i] = f16_table[h[i]];
 }
 
 static inline float round_f16(float x) { return orc_f16_to_f32(orc_f32_to_f16(x)); }
@@ -326,11 +333,18 @@ static float dot_fixed(const float * a, const float * b, int32_t n) {
     return ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
 }
 
+/* ORC_PLANT is a test hook for the negative controls of tests/test_oracle.py, which build copies of
+ * this file with a planted mistake and check that the attention pin rejects them: 1 rounds p to f16
+ * before the normalisation, 2 leaves q unrounded.  The library itself is always built with 0. */
+#ifndef ORC_PLANT
+#define ORC_PLANT 0
+#endif
+
 static void attend_row(const float * q, const float * kf, const float * vf, size_t row_stride,
                        int32_t n_keys, int32_t head_dim, float scale, int round16, float * scores,
                        float * out) {
     float qq[512];
-    for (int32_t d = 0; d < head_dim; ++d) qq[d] = round16 ? round_f16(q[d]) : q[d];
+    for (int32_t d = 0; d < head_dim; ++d) qq[d] = (round16 && ORC_PLANT != 2) ? round_f16(q[d]) : q[d];
     float mx = -INFINITY;
     for (int32_t j = 0; j < n_keys; ++j) {
         const float s = dot_fixed(qq, kf + (size_t)j * row_stride, head_dim) * scale;
@@ -347,7 +361,7 @@ static void attend_row(const float * q, const float * kf, const float * vf, size
     for (int32_t d = 0; d < head_dim; ++d) out[d] = 0.0f;
     for (int32_t j = 0; j < n_keys; ++j) {
         float p = scores[j] * r;
-        if (round16) p = round_f16(p);
+        if (round16) p = ORC_PLANT == 1 ? round_f16(scores[j]) * r : round_f16(p);
         const float * vr = vf + (size_t)j * row_stride;
         for (int32_t d = 0; d < head_dim; ++d) out[d] = fmaf(p, vr[d], out[d]);
     }
@@ -363,15 +377,21 @@ void orc_cache_attention(const orc_cache * cache, int32_t layer, const float * q
     /* f32 copies of rows [0, full) of every head: [head][pos][d] */
     float * kf = (float *)malloc(sizeof(float) * (size_t)n_kv * full * d);
     float * vf = (float *)malloc(sizeof(float) * (size_t)n_kv * full * d);
+    /* exact widening of the stored rows, in parallel blocks of 64 positions per head */
+    const int32_t n_blk = (full + 63) / 64;
+#pragma omp parallel for collapse(2) schedule(static)
     for (int32_t h = 0; h < n_kv; ++h) {
-        const size_t src = base + (size_t)orc_slot_index(h, 0, 0, cache->max_seq, d);
-        const size_t dst = (size_t)h * full * d;
-        if (cache->dtype == 1) {
-            orc_f16_to_f32_array((const uint16_t *)cache->k + src, kf + dst, (size_t)full * d);
-            orc_f16_to_f32_array((const uint16_t *)cache->v + src, vf + dst, (size_t)full * d);
-        } else {
-            memcpy(kf + dst, (const float *)cache->k + src, sizeof(float) * (size_t)full * d);
-            memcpy(vf + dst, (const float *)cache->v + src, sizeof(float) * (size_t)full * d);
+        for (int32_t b = 0; b < n_blk; ++b) {
+            const int32_t p0 = b * 64, np = full - p0 < 64 ? full - p0 : 64;
+            const size_t src = base + (size_t)orc_slot_index(h, p0, 0, cache->max_seq, d);
+            const size_t dst = ((size_t)h * full + p0) * d;
+            if (cache->dtype == 1) {
+                orc_f16_to_f32_array((const uint16_t *)cache->k + src, kf + dst, (size_t)np * d);
+                orc_f16_to_f32_array((const uint16_t *)cache->v + src, vf + dst, (size_t)np * d);
+            } else {
+                memcpy(kf + dst, (const float *)cache->k + src, sizeof(float) * (size_t)np * d);
+                memcpy(vf + dst, (const float *)cache->v + src, sizeof(float) * (size_t)np * d);
+            }
         }
     }
     const int round16 = cache->dtype == 1;

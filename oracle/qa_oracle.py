@@ -265,9 +265,10 @@ class OracleModel:
         return ids.tolist(), marg.tolist(), second.tolist()
 
 
-def cache_attention(k: np.ndarray, v: np.ndarray, q: np.ndarray, n_past: int, f16: bool) -> np.ndarray:
+def cache_attention(k: np.ndarray, v: np.ndarray, q: np.ndarray, n_past: int, f16: bool, library=None) -> np.ndarray:
     """Attention of T queries q [T][H][d] (positions n_past..) over one layer's cache rows.
-    k, v: f32 values [n_kv][L][d] with L = n_past + T (rounded to f16 first when f16)."""
+    k, v: f32 values [n_kv][L][d] with L = n_past + T (rounded to f16 first when f16).
+    `library` runs another build of qa_oracle.c (the planted-mistake builds of the oracle's tests)."""
     n_kv, L, d = k.shape
     T, H, _ = q.shape
     assert L == n_past + T
@@ -275,8 +276,18 @@ def cache_attention(k: np.ndarray, v: np.ndarray, q: np.ndarray, n_past: int, f1
     cache.fill(k[None], v[None], L)
     out = np.empty((T, H, d), dtype=np.float32)
     q = np.ascontiguousarray(q, dtype=np.float32)
-    lib.orc_cache_attention(C.byref(cache.c), 0, fptr(q), n_past, T, H, 1.0 / np.sqrt(np.float32(d)), fptr(out))
+    (library or lib).orc_cache_attention(C.byref(cache.c), 0, fptr(q), n_past, T, H, 1.0 / np.sqrt(np.float32(d)),
+                                         fptr(out))
     return out
+
+
+def load_build(path: str):
+    """ctypes handle of another build of qa_oracle.c with the attention entry point typed."""
+    other = C.CDLL(path)
+    f = other.orc_cache_attention
+    f.restype = None
+    f.argtypes = [C.POINTER(Cache), i32, fp, i32, i32, i32, f32, fp]
+    return other
 
 
 def causal_attention_f32(q: np.ndarray, k: np.ndarray, v: np.ndarray) -> np.ndarray:

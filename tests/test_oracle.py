@@ -8,6 +8,7 @@ matmul), a closed form written from the mathematics, or an invariant that a plau
 off-by-one position).
 """
 import math
+import os
 
 import numpy as np
 import pytest
@@ -171,6 +172,105 @@ def test_cache_attention_f16_semantics(orc):
     assert np.abs(got - plain).max() > 0   # q -> f16 and p -> f16 change the result
 
 
+# The f16-cache attention semantics, pinned at their rounding points.  GGML's f16 mul_mat converts
+# src1 to f16 (q before QK^T, p before PV) and soft_max_ext normalises in f32 before that conversion
+# (text-decoder.cpp:454-461 [ggml-sem]).  The inputs below make every q.K dot product exact in f32, so
+# a float64 statement with f32 rounding applied exactly where those ops round matches the oracle to
+# f32 accumulation error, and misplaced roundings are far outside that bar.
+PIN_REL = 1e-6
+
+
+def _exact_f16_values(rng, shape):
+    """a * 2^-4 with integer |a| in [1, 64]: exact in f16; a product of two is a multiple of 2^-8 below 16,
+    so any 128-term dot product of them is exact in f32, in any summation order."""
+    a = rng.integers(1, 65, shape) * rng.choice([-1, 1], shape)
+    return (a * 2.0 ** -4).astype(np.float32)
+
+
+def _f16_attention_statement(q, k16, v16, n_past, round_q=True, p_round="normalised"):
+    """float64 statement: q -> f16; s = f32(f32(q16 . K16) * f32(1/sqrt(d))); M = max s;
+    e = f32(exp(s - M)); S = double sum of e; p = f16(f32(e * f32(1/S))); o = sum_j p_j V16_j.
+    round_q=False and p_round="unnormalised" (p = f16(e) * f32(1/S)) state the two misplaced roundings."""
+    T, H, d = q.shape
+    scale = np.float32(1.0) / np.sqrt(np.float32(d))
+    qq = q.astype(np.float16).astype(np.float64) if round_q else q.astype(np.float64)
+    out = np.zeros((T, H, d))
+    for t in range(T):
+        n = n_past + t + 1
+        for h in range(H):
+            K, V = k16[h // 2, :n].astype(np.float64), v16[h // 2, :n].astype(np.float64)
+            s = (K @ qq[t, h]).astype(np.float32) * scale
+            e = np.exp((s - s.max()).astype(np.float64)).astype(np.float32)
+            r = np.float32(1.0 / float(np.sum(e.astype(np.float64))))
+            if p_round == "normalised":
+                p = (e * r).astype(np.float16)
+            else:
+                p = e.astype(np.float16).astype(np.float32) * r
+            out[t, h] = p.astype(np.float64) @ V
+    return out
+
+
+def _pin_inputs(n_past, T, seed):
+    rng = np.random.default_rng(seed)
+    L = n_past + T
+    q16 = _exact_f16_values(rng, (T, 16, 128))
+    # q carries bits below half an f16 ulp of q16: rounding q to f16 gives q16 back
+    ulp = 2.0 ** (np.floor(np.log2(np.abs(q16))) - 11)   # the smaller of the ulps either side of q16
+    q = (q16 + 0.45 * ulp * rng.uniform(-1, 1, q16.shape)).astype(np.float32)
+    assert (q.astype(np.float16).astype(np.float32) == q16).all()
+    k = _exact_f16_values(rng, (8, L, 128))
+    v = rng.standard_normal((8, L, 128)).astype(np.float32)
+    return q, k, v.astype(np.float16).astype(np.float32)
+
+
+def _rel(a, b):
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+@pytest.mark.parametrize("n_past,T", [(0, 1), (157, 1), (300, 3), (1000, 1)])
+def test_cache_attention_f16_rounding_points_pinned(orc, n_past, T):
+    q, k, v16 = _pin_inputs(n_past, T, 60 + n_past + T)
+    got = orc.cache_attention(k, v16, q, n_past, f16=True)
+    want = _f16_attention_statement(q, k, v16, n_past)
+    assert _rel(got, want) <= PIN_REL, _rel(got, want)
+    # the misplaced roundings are far outside the bar: the pin tells them apart from the oracle
+    if n_past > 0:
+        for kw in (dict(round_q=False), dict(p_round="unnormalised")):
+            assert _rel(_f16_attention_statement(q, k, v16, n_past, **kw), want) > 20 * PIN_REL, kw
+
+
+@pytest.fixture(scope="module")
+def planted_builds(tmp_path_factory, orc):
+    """Copies of the oracle built with a planted mistake (ORC_PLANT in qa_oracle.c): 1 rounds p before the
+    normalisation, 2 leaves q unrounded."""
+    import shutil
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc is needed to build the planted-mistake oracles")
+    out = {}
+    src = os.path.join(orc.ORACLE_DIR, "qa_oracle.c")
+    for plant in (1, 2):
+        so = str(tmp_path_factory.mktemp(f"plant{plant}") / "libqa_oracle_plant.so")
+        subprocess.run(["gcc", "-O3", "-std=c11", "-fPIC", "-fopenmp", "-ffp-contract=off", "-march=x86-64-v3",
+                        f"-DORC_PLANT={plant}", "-shared", "-o", so, src, "-lm"], check=True, capture_output=True)
+        out[plant] = orc.load_build(so)
+    return out
+
+
+@pytest.mark.parametrize("plant", [1, 2])
+def test_attention_pin_rejects_planted_mistakes(orc, planted_builds, plant):
+    """Negative controls: an oracle with p rounded before the normalisation (1) or q left unrounded (2)
+    fails the pin above, and matches the statement of its own mistake instead."""
+    n_past, T = 300, 3
+    q, k, v16 = _pin_inputs(n_past, T, 60 + n_past + T)
+    bad = orc.cache_attention(k, v16, q, n_past, f16=True, library=planted_builds[plant])
+    want = _f16_attention_statement(q, k, v16, n_past)
+    assert _rel(bad, want) > 20 * PIN_REL, _rel(bad, want)
+    if plant == 1:
+        assert _rel(bad, _f16_attention_statement(q, k, v16, n_past, p_round="unnormalised")) <= PIN_REL
+
+
 def test_attention_special_cases(orc):
     rng = np.random.default_rng(7)
     q = rng.standard_normal((1, 16, 128)).astype(np.float32)
@@ -237,7 +337,10 @@ def _tiny_model(orc, cfg, seed=11):
                            o=n(H, QD), q_norm=1 + n(128, s=0.1), k_norm=1 + n(128, s=0.1), gate=n(I, H), up=n(I, H),
                            down=n(H, I)))
     embd = n(cfg["vocab"], H, s=1.0)
-    return orc.OracleModel(cfg, layers, embd, 1 + n(H, s=0.1), embd), layers, embd
+    out_norm = 1 + n(H, s=0.1)
+    model = orc.OracleModel(cfg, layers, embd, out_norm, embd)
+    model.output_norm_w = out_norm
+    return model, layers, embd
 
 
 def _torch_layer(x, lw, cfg, pos0=0):
@@ -325,6 +428,93 @@ def test_generate_cached_equals_recompute_greedy(orc):
     assert stop["stopped"] and stop["ids"] == out["ids"][:first + 1] and stop["total_tokens"] == 6 + first + 1
     assert m.generate(x, 0, [], m.cache(6, f16=False))["ids"] == []
     assert m.generate(x, N, [], m.cache(6 + N - 1, f16=False))["rc"] == 2      # exceeds KV-cache capacity
+
+
+def test_decode_steps_continue_generate(orc):
+    """orc_decode_steps (the per-stream statement of config 4) continued from the cache a prefill left
+    gives exactly what orc_generate_cached gives after its first pick: same ids, margins, runner-ups and
+    cur_len (1 prefill + N - 1 decode forwards, text-decoder.cpp:2209-2311)."""
+    cfg = _tiny_cfg(layers=2)
+    m, _, _ = _tiny_model(orc, cfg)
+    x = np.random.default_rng(16).standard_normal((6, cfg["hidden"])).astype(np.float32)
+    N = 7
+    for f16 in (False, True):
+        gen = m.generate(x, N, [], m.cache(6 + N, f16))
+        cache = m.cache(6 + N, f16)
+        m.forward_cached(x, 0, cache)
+        assert cache.cur_len == 6
+        ids, marg, second = m.decode_steps(cache, gen["ids"][0], N - 1)
+        assert ids == gen["ids"][1:] and marg == gen["margins"][1:] and second == gen["runner_up"][1:], f16
+        assert cache.cur_len == gen["cur_len"] == 6 + N - 1
+
+
+def _torch_decode(layers, embd, out_norm, cfg, k0, v0, first, n_steps):
+    """Greedy decode from token `first` over a cache pre-filled with rows k0, v0 [layer][kv head][L0][d]
+    (K held after k_norm and RoPE, as the reference stores it), Qwen3 layers from their definition in
+    float64: step i embeds the token, appends its k/v at position L0 + i and attends over 0..L0 + i."""
+    d = torch.float64
+    eps = cfg["rms_norm_eps"]
+    W = [{k: torch.from_numpy(v).to(d) for k, v in lw.items()} for lw in layers]
+    E, ON = torch.from_numpy(embd).to(d), torch.from_numpy(out_norm).to(d)
+    Kc = [torch.from_numpy(k0[l]).to(d) for l in range(len(layers))]
+    Vc = [torch.from_numpy(v0[l]).to(d) for l in range(len(layers))]
+    inv = cfg["rope_theta"] ** (-torch.arange(0, 128, 2, dtype=d) / 128)
+
+    def rms(a, w):
+        return a / torch.sqrt(a.pow(2).mean(-1, keepdim=True) + eps) * w
+
+    tok, ids, margins = first, [], []
+    L0 = k0.shape[2]
+    for step in range(n_steps):
+        ang = (L0 + step) * inv
+        c, s = ang.cos(), ang.sin()
+
+        def rope(a):
+            return torch.cat([a[..., :64] * c - a[..., 64:] * s, a[..., 64:] * c + a[..., :64] * s], dim=-1)
+
+        X = E[tok][None]
+        for l, w in enumerate(W):
+            h = rms(X, w["attn_norm"])
+            q = rope(rms((h @ w["q"].T).view(16, 128), w["q_norm"]))
+            k = rope(rms((h @ w["k"].T).view(8, 128), w["k_norm"]))
+            v = (h @ w["v"].T).view(8, 128)
+            Kc[l] = torch.cat([Kc[l], k[:, None]], dim=1)
+            Vc[l] = torch.cat([Vc[l], v[:, None]], dim=1)
+            Kh, Vh = Kc[l].repeat_interleave(2, dim=0), Vc[l].repeat_interleave(2, dim=0)
+            p = torch.softmax((Kh @ q[:, :, None])[..., 0] / math.sqrt(128), dim=-1)
+            att = (p[:, None, :] @ Vh)[:, 0]
+            X = X + att.reshape(1, -1) @ w["o"].T
+            h = rms(X, w["ffn_norm"])
+            X = X + (torch.nn.functional.silu(h @ w["gate"].T) * (h @ w["up"].T)) @ w["down"].T
+        logits = (rms(X, ON) @ E.T)[0]
+        top = torch.topk(logits, 2)
+        tok = int(top.indices[0])
+        ids.append(tok)
+        margins.append(float(top.values[0] - top.values[1]))
+    return ids, margins, [k.numpy() for k in Kc], [v.numpy() for v in Vc]
+
+
+def test_decode_steps_match_textbook_decode_over_prefilled_cache(orc):
+    """orc_decode_steps from a cache pre-filled with random rows (config 4's setting) against the float64
+    textbook decode: identical greedy ids (every float64 top-2 margin here is far above f32 error), the
+    appended K/V rows at positions L0.., and cur_len = L0 + steps."""
+    cfg = _tiny_cfg(layers=2)
+    m, layers, embd = _tiny_model(orc, cfg)
+    rng = np.random.default_rng(17)
+    L0, steps = 40, 6
+    k0 = rng.standard_normal((2, 8, L0, 128)).astype(np.float32)
+    v0 = rng.standard_normal((2, 8, L0, 128)).astype(np.float32)
+    ids_ref, marg_ref, K, V = _torch_decode(layers, embd, m.output_norm_w, cfg, k0, v0, 5, steps)
+    assert min(marg_ref) > 1e-3, marg_ref
+    cache = m.cache(L0 + steps, f16=False)
+    cache.fill(k0, v0, L0)
+    ids, marg, _ = m.decode_steps(cache, 5, steps)
+    assert ids == ids_ref
+    np.testing.assert_allclose(marg, marg_ref, rtol=1e-3, atol=1e-4)
+    assert cache.cur_len == L0 + steps
+    np.testing.assert_allclose(cache.k[:, :, L0:L0 + steps], np.stack(K)[:, :, L0:L0 + steps], rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(cache.v[:, :, L0:L0 + steps], np.stack(V)[:, :, L0:L0 + steps], rtol=1e-4, atol=1e-5)
+    np.testing.assert_array_equal(cache.k[:, :, :L0], k0)          # the prefilled rows are never rewritten
 
 
 # ---------------------------------------------------------------------------------------------- bookkeeping

@@ -8,10 +8,59 @@ for p in (os.path.join(ROOT, "qwenasr.cpp_amd"), os.path.join(ROOT, "oracle"), R
     if p not in sys.path:
         sys.path.insert(0, p)
 
+# Logits of two f32 evaluations of the 28-layer decoder that differ only in summation order agree to
+# LOGIT_ATOL (asserted by test_teacher_forced_logits_within_tolerance on the long-context config).
+# A greedy pick can then differ only where the two top logits are closer than 2 * LOGIT_ATOL.
+LOGIT_ATOL = 2e-3
+TIE_EPS = 2 * LOGIT_ATOL
+
+_GREEDY = pytest.StashKey[list]()
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP path through the C ABI)")
     config.addinivalue_line("markers", "slow: long CPU oracle runs")
+    config.stash[_GREEDY] = []
+
+
+class GreedyRecorder:
+    """Greedy-id comparisons of the session.  Ids must be identical; the one accepted difference is a
+    first divergence at an oracle near-tie (top-2 margin < TIE_EPS) where the HIP path picked the oracle's
+    runner-up.  After it the two sequences feed different tokens and are not compared further.  Every
+    comparison is recorded and the terminal summary lists each accepted divergence by name, so a run
+    record (pytest -q tail) shows which configs and streams, if any, used the exception."""
+
+    def __init__(self, records: list):
+        self.records = records
+
+    def match(self, got, ref, margins, runner_up, what):
+        for i, (a, b) in enumerate(zip(got, ref)):
+            if a != b:
+                assert margins[i] < TIE_EPS and a == runner_up[i], (what, i, a, b, margins[i], runner_up[i])
+                self.records.append((what, len(ref), i, float(margins[i]), int(a), int(b)))
+                return i
+        assert len(got) == len(ref), (what, len(got), len(ref))
+        self.records.append((what, len(ref), None, None, None, None))
+        return None
+
+
+@pytest.fixture
+def greedy(request):
+    return GreedyRecorder(request.config.stash[_GREEDY])
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    recs = config.stash.get(_GREEDY, [])
+    if not recs:
+        return
+    div = [r for r in recs if r[2] is not None]
+    ids = sum(r[1] for r in recs)
+    terminalreporter.write_line(
+        f"greedy ids: {len(recs)} sequences ({ids} ids) compared, {len(recs) - len(div)} identical, "
+        f"{len(div)} accepted near-tie divergence(s) (oracle top-2 margin < {TIE_EPS:g}, runner-up taken)")
+    for what, n, i, m, a, b in div:
+        terminalreporter.write_line(f"  near-tie: {what}: step {i} of {n}, oracle margin {m:.2e}, "
+                                    f"HIP id {a} = oracle runner-up, oracle id {b}")
 
 
 @pytest.fixture(scope="session")

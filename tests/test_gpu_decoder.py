@@ -8,6 +8,7 @@ import subprocess
 
 import numpy as np
 import pytest
+from conftest import LOGIT_ATOL
 
 pytestmark = pytest.mark.gpu
 
@@ -25,27 +26,6 @@ def digest(*arrays) -> str:
 def golden(index):
     with open(os.path.join(GOLDEN, f"cfg{index}.json")) as f:
         return json.load(f)
-
-
-# Logits of two f32 evaluations of the 28-layer decoder that differ only in summation order agree to
-# LOGIT_ATOL (asserted by test_teacher_forced_logits_within_tolerance on the long-context config).
-# A greedy pick can then differ only where the two top logits are closer than 2 * LOGIT_ATOL.
-LOGIT_ATOL = 2e-3
-TIE_EPS = 2 * LOGIT_ATOL
-
-
-def assert_greedy_match(got, ref, margins, runner_up, what):
-    """Greedy ids identical.  The one accepted difference is a first divergence at an oracle near-tie
-    (top-2 margin < TIE_EPS) where the GPU picked the oracle's runner-up; after it the two sequences
-    feed different tokens and are not compared further.  Returns the divergence index or None."""
-    for i, (a, b) in enumerate(zip(got, ref)):
-        if a != b:
-            assert margins[i] < TIE_EPS and a == runner_up[i], (what, i, a, b, margins[i], runner_up[i])
-            print(f"{what}: near-tie divergence at step {i} (oracle margin {margins[i]:.2e}, GPU took the "
-                  f"runner-up {a})", flush=True)
-            return i
-    assert len(got) == len(ref), (what, len(got), len(ref))
-    return None
 
 
 def close(got, ref, atol=2e-3, rtol_l2=1e-3):
@@ -84,7 +64,7 @@ def test_cfg0_single_layer_decode(qa):
 
 
 @pytest.mark.parametrize("f16", [True, False])
-def test_small_model_greedy_matches_oracle(qa, orc, f16):
+def test_small_model_greedy_matches_oracle(qa, orc, greedy, f16):
     """0.6B shapes, 3 layers: greedy ids, stop handling and bookkeeping against an in-test oracle run."""
     model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=3)
     om = orc.OracleModel.from_product_model(model)
@@ -93,7 +73,8 @@ def test_small_model_greedy_matches_oracle(qa, orc, f16):
     ref = om.generate(x, N, qa.STOP_IDS, om.cache(49 + N, f16))
     with qa.Decoder(model, 1, 49 + N, qa.QA_CACHE_F16 if f16 else qa.QA_CACHE_F32) as dec:
         out = dec.generate(x, N, margins=True)
-        assert assert_greedy_match(out["ids"], ref["ids"], ref["margins"], ref["runner_up"], "small") is None
+        assert greedy.match(out["ids"], ref["ids"], ref["margins"], ref["runner_up"],
+                            f"small model ({'f16' if f16 else 'f32'} cache)") is None
         assert out["total_tokens"] == ref["total_tokens"] and out["stopped"] == ref["stopped"]
         assert dec.cur_len(0) == ref["cur_len"] == 49 + N - 1
         assert dec.device_lens().tolist() == [ref["cur_len"]]
@@ -118,7 +99,7 @@ def test_small_model_greedy_matches_oracle(qa, orc, f16):
 
 
 @pytest.mark.parametrize("index", [1, 2, 3])
-def test_config_greedy_matches_golden(qa, index):
+def test_config_greedy_matches_golden(qa, greedy, index):
     from qwenasr_amd import configs
 
     g = golden(index)
@@ -129,7 +110,7 @@ def test_config_greedy_matches_golden(qa, index):
     print(f"config {index}: prompt {w.prompt}, {w.new_tokens} tokens", flush=True)
     with qa.Decoder(model, 1, w.max_seq, w.cache_type) as dec:
         out = dec.generate(x, w.new_tokens, margins=True)
-        div = assert_greedy_match(out["ids"], g["ids"], g["margins"], g["runner_up"], f"config {index}")
+        div = greedy.match(out["ids"], g["ids"], g["margins"], g["runner_up"], f"config {index}")
         if div is None:
             assert out["stopped"] == g["stopped"] and out["total_tokens"] == g["total_tokens"]
             assert dec.cur_len(0) == g["cur_len"]
@@ -138,7 +119,7 @@ def test_config_greedy_matches_golden(qa, index):
         assert dec.device_lens().tolist() == [dec.cur_len(0)]
 
 
-def test_config4_ragged_streams_match_golden(qa):
+def test_config4_ragged_streams_match_golden(qa, greedy):
     from qwenasr_amd import configs
 
     g = golden(4)
@@ -155,14 +136,15 @@ def test_config4_ragged_streams_match_golden(qa):
         print("config 4 caches filled", flush=True)
         ids = dec.decode_streams(first, w.steps)
         assert ids.shape == (w.steps, w.streams)
+        assert sorted(int(s) for s in g["streams"]) == list(range(w.streams))   # every stream has a golden
         for s, ref in g["streams"].items():
-            assert_greedy_match(ids[:, int(s)].tolist(), ref["ids"], ref["margins"], ref["runner_up"], f"stream {s}")
+            greedy.match(ids[:, int(s)].tolist(), ref["ids"], ref["margins"], ref["runner_up"], f"config 4 stream {s}")
         assert dec.device_lens().tolist() == (lens + w.steps).tolist()
         assert [dec.cur_len(s) for s in range(w.streams)] == (lens + w.steps).tolist()
 
 
 @pytest.mark.parametrize("n_streams", [2, 5, 32])
-def test_few_streams_match_oracle(qa, orc, n_streams):
+def test_few_streams_match_oracle(qa, orc, greedy, n_streams):
     """The multi-stream decode step at 2..32 streams (fused RMSNorm / SwiGLU skinny GEMMs, per-stream
     lengths) against the oracle decoding each stream alone: 0.6B shapes, 2 layers, f16 cache, ragged
     contexts, 4 greedy steps; ids identical up to an oracle near-tie."""
@@ -186,7 +168,7 @@ def test_few_streams_match_oracle(qa, orc, n_streams):
         print(f"{n_streams} streams: oracle done", flush=True)
         got = dec.decode_streams(first, steps)
         for s in range(n_streams):
-            assert_greedy_match(got[:, s].tolist(), *refs[s], f"stream {s}")
+            greedy.match(got[:, s].tolist(), *refs[s], f"{n_streams}-stream step, stream {s}")
         assert dec.device_lens().tolist() == (lens + steps).tolist()
 
 
@@ -219,29 +201,10 @@ def test_decoders_in_sequence_see_cleared_memory(qa):
         np.testing.assert_array_equal(ids, runs[0])
 
 
-def test_graph_replay_equals_eager(qa, monkeypatch):
-    """The captured decode step (HIP graph, replayed every token) and the eager launch sequence give
-    bit-identical ids and logit margins, over repeated generate calls with eager prefills in between
-    (each call re-runs the prefill eagerly and replays the same graph)."""
-    model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=4)
-    x = qa.prompt_input(model, 30, 7)
-    runs = {}
-    for mode in ("1", "0"):
-        monkeypatch.setenv("QA_DECODE_GRAPH", mode)
-        with qa.Decoder(model, 1, 37 + 20, qa.QA_CACHE_F16) as dec:
-            outs = [dec.generate(x, 20, stop_ids=[], margins=True) for _ in range(3)]
-            logits = dec.forward(x, 0)
-        for o in outs[1:]:
-            assert o == outs[0]
-        runs[mode] = (outs[0], logits)
-    assert runs["1"][0] == runs["0"][0]
-    np.testing.assert_array_equal(runs["1"][1].view(np.uint32), runs["0"][1].view(np.uint32))
-
-
 def test_teacher_forced_logits_within_tolerance(qa, orc):
     """Config-4 stream 11 (context 3648, the stream with the smallest oracle margin): GPU and oracle
     decode the same tokens (the oracle's picks) step by step from bit-identical caches; every logit of
-    every step agrees to LOGIT_ATOL.  This is the bound the near-tie rule of assert_greedy_match uses."""
+    every step agrees to LOGIT_ATOL.  This is the bound the near-tie rule of conftest.GreedyRecorder uses."""
     from qwenasr_amd import configs
 
     w = configs.CONFIGS[4]

@@ -75,12 +75,6 @@ struct qa_decoder {
     float * staging = nullptr;
     size_t staging_bytes = 0;
     float scale = 0.0f;
-    // captured decode step (one token per stream, grids sized by capacity), replayed every step
-    hipGraphExec_t step_exec = nullptr;
-    int32_t step_rows = 0;
-    uint64_t act_gen = 1;       // bumped whenever the activation buffers are reallocated
-    uint64_t step_gen = 0;
-    bool use_graph = false;     // QA_DECODE_GRAPH=1: replay the captured step (measured no faster here)
     // profiling
     bool prof = false;
     struct Rec { int fam; hipEvent_t a, b; };
@@ -201,7 +195,6 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
         return rc;
     }
     d->cap_rows = rows;
-    ++d->act_gen;
     return QA_OK;
 }
 
@@ -397,45 +390,12 @@ int decode_step_ops(qa_decoder * d, int32_t rows, int32_t max_len) {
     return rc;
 }
 
-void drop_step_graph(qa_decoder * d) {
-    if (d->step_exec) (void)hipGraphExecDestroy(d->step_exec);
-    d->step_exec = nullptr;
-    d->step_rows = 0;
-}
-
-// With QA_DECODE_GRAPH=1, single-stream steps replay a captured graph (every kernel of the step is
-// this library's; the multi-stream projections go through rocBLAS and stay eager).  On MI355X the
-// replay measured the same per-token time as eager launches (the step's kernels are large enough that
-// dispatch latency is hidden), so eager is the default.  The capture sizes the attention grids
-// by the cache capacity; workgroups past a stream's length exit at once, and the tiling depends on
-// the capacity only, so replay and eager execution give the same bits.
+// One decode step launched eagerly.  The step reads lengths and ids from device memory only, so the
+// host does no per-token bookkeeping beyond the launches (the reference rebuilds its graph and uploads
+// a dense mask every token, text-decoder.cpp:1658-1739).
 int decode_step(qa_decoder * d, int32_t rows) {
-    if (!d->use_graph || d->prof || rows != 1) {
-        const int rc = decode_step_ops(d, rows, host_max_len(d, rows, 1));
-        if (rc != QA_OK) return rc;
-    } else {
-        if (!d->step_exec || d->step_rows != rows || d->step_gen != d->act_gen) {
-            drop_step_graph(d);
-            QA_HIP(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
-            const int rc = decode_step_ops(d, rows, d->max_seq);
-            hipGraph_t graph = nullptr;
-            const hipError_t end = hipStreamEndCapture(d->stream, &graph);
-            if (rc != QA_OK) {
-                if (graph) (void)hipGraphDestroy(graph);
-                return rc;
-            }
-            if (end != hipSuccess) return hip_fail(end, "hipStreamEndCapture (decode step)");
-            const hipError_t inst = hipGraphInstantiate(&d->step_exec, graph, nullptr, nullptr, 0);
-            (void)hipGraphDestroy(graph);
-            if (inst != hipSuccess) {
-                d->step_exec = nullptr;
-                return hip_fail(inst, "hipGraphInstantiate (decode step)");
-            }
-            d->step_rows = rows;
-            d->step_gen = d->act_gen;
-        }
-        QA_HIP(hipGraphLaunch(d->step_exec, d->stream));
-    }
+    const int rc = decode_step_ops(d, rows, host_max_len(d, rows, 1));
+    if (rc != QA_OK) return rc;
     for (int32_t s = 0; s < rows; ++s) d->cur_len[s] += 1;
     return QA_OK;
 }
@@ -474,7 +434,6 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
     d->cache_type = cache_type;
     d->scale = 1.0f / std::sqrt(static_cast<float>(cfg->head_dim));
     d->cur_len.assign(static_cast<size_t>(n_streams), 0);
-    if (const char * e = std::getenv("QA_DECODE_GRAPH")) d->use_graph = std::strcmp(e, "1") == 0;
     auto bail = [&](int rc) {
         qa_decoder_destroy(d);
         return rc;
@@ -569,7 +528,6 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
 extern "C" void qa_decoder_destroy(qa_decoder * d) {
     if (!d) return;
     if (d->stream) (void)hipStreamSynchronize(d->stream);
-    drop_step_graph(d);
     for (auto & r : d->recs) {
         if (r.a) (void)hipEventDestroy(r.a);
         if (r.b) (void)hipEventDestroy(r.b);

@@ -292,6 +292,43 @@ int qa_decoder_input_assemble(const float * token_embd, int32_t vocab, int32_t h
 int qa_model_weights_view(const qa_model * model, qa_layer_weights * layers, int32_t n_layers,
                           qa_model_weights * weights);
 
+/* Special-token ids of Qwen3-ASR (convert.py:334-354 defaults; native-model.cpp:411-434). */
+enum {
+    QA_TOKEN_ENDOFTEXT = 151643,
+    QA_TOKEN_IM_START = 151644,
+    QA_TOKEN_IM_END = 151645,
+    QA_TOKEN_AUDIO_START = 151669,
+    QA_TOKEN_AUDIO_END = 151670,
+    QA_TOKEN_AUDIO_PAD = 151676,
+    QA_TOKEN_ASR_TEXT = 151704
+};
+
+/* Writes `model` as a GGUF v3 checkpoint that the reference's loader accepts: the metadata keys of
+ * qwenasr_load_gguf_metadata (native-model.cpp:188-218), a placeholder tokenizer vocabulary with the
+ * special tokens at their ids (the reference's fixture layout, native-model.cpp:407-431; a vocabulary
+ * smaller than Qwen3-ASR's holds them at its last seven ids, in the order of the enum above) and every
+ * text tensor in f32 with GGML ne order (load_text_layer_tensors, text-decoder.cpp:191-228).  Replaces
+ * the checkpoint side of convert.py:357-397 for synthetic models.                                 */
+int qa_gguf_write_model(const qa_model * model, const char * path);
+
+/* The ASR prompt of qwenasr_build_asr_prompt (tokenizer.cpp:529-549): system turn with system_text,
+ * user turn holding audio_tokens <|audio_pad|> placeholders between <|audio_start|> and <|audio_end|>
+ * (a negative count counts as 0), the assistant turn, and "language NAME<asr_text>" when language is
+ * non-empty.  Writes at most cap bytes including the terminating NUL; *len (may be NULL) receives the
+ * full length without the NUL.  QA_ERR_RANGE when cap is too small (nothing is written then).     */
+int qa_build_asr_prompt(int32_t audio_tokens, const char * system_text, const char * language, char * out,
+                        size_t cap, size_t * len);
+
+/* Audio-encoder output length for `input_frames` mel frames (qwenasr_audio_output_length,
+ * audio-features.cpp:14-19): 13 tokens per 100 frames plus the tail's two stride-2 stages.      */
+int32_t qa_audio_output_length(int32_t input_frames);
+
+/* Header of a WAV file as the reference's reader sees it (qwenasr_read_wav_16k_mono,
+ * audio-features.cpp:120-200): the sample-frame count of the data chunk and the sample rate.
+ * QA_ERR_INVALID with the reference's messages for a missing file, a rate other than 16 kHz, no
+ * data, or an encoding other than PCM16, PCM24 or f32.                                           */
+int qa_wav_info(const char * path, int64_t * n_samples, int32_t * sample_rate);
+
 /* ---------------------------------------------------------------- runtime layer */
 typedef struct qa_decoder qa_decoder;
 

@@ -35,6 +35,7 @@ struct gguf_context {
     std::map<std::string, uint64_t> u64s;
     std::map<std::string, double> f64s;
     std::map<std::string, std::string> strs;
+    std::map<std::string, uint64_t> array_lens;
 };
 
 namespace {
@@ -95,6 +96,7 @@ bool read_value(Reader & r, uint32_t type, const std::string & key, gguf_context
         const uint32_t et = r.get<uint32_t>();
         const uint64_t n = r.get<uint64_t>();
         if (!r.ok) return false;
+        ctx->array_lens[key] = n;
         if (et == 8) {
             for (uint64_t i = 0; i < n && r.ok; ++i) (void)r.str();
             return r.ok;
@@ -368,5 +370,21 @@ bool qwenasr_gguf_model_get_f32(const QwenAsrGgufModel & model, const char * key
     auto it = model.gguf->f64s.find(key);
     if (it == model.gguf->f64s.end()) return false;
     *out = static_cast<float>(it->second);
+    return true;
+}
+
+bool qwenasr_gguf_model_get_str(const QwenAsrGgufModel & model, const char * key, std::string * out) {
+    if (!model.gguf || !key || !out) return false;
+    auto it = model.gguf->strs.find(key);
+    if (it == model.gguf->strs.end()) return false;
+    *out = it->second;
+    return true;
+}
+
+bool qwenasr_gguf_model_get_array_len(const QwenAsrGgufModel & model, const char * key, uint64_t * out) {
+    if (!model.gguf || !key || !out) return false;
+    auto it = model.gguf->array_lens.find(key);
+    if (it == model.gguf->array_lens.end()) return false;
+    *out = it->second;
     return true;
 }

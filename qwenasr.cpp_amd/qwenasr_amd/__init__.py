@@ -119,6 +119,10 @@ SIGNATURES = {
     "qa_model_tensor": (fp, vp, C.c_char_p, C.POINTER(i64)),
     "qa_model_config": (C.c_int, vp, C.POINTER(TextConfig)),
     "qa_decoder_input_assemble": (C.c_int, vp, i32, i32, vp, i32, i32, vp, i32, vp),
+    "qa_gguf_write_model": (C.c_int, vp, C.c_char_p),
+    "qa_build_asr_prompt": (C.c_int, i32, C.c_char_p, C.c_char_p, C.c_char_p, sz, C.POINTER(sz)),
+    "qa_audio_output_length": (i32, i32),
+    "qa_wav_info": (C.c_int, C.c_char_p, C.POINTER(i64), C.POINTER(i32)),
     "qa_gemm_rows_workspace_bytes": (sz, i32, i32, i32),
     "qa_gemm_rows": (C.c_int, vp, i32, i32, vp, i32, vp, i32, vp, sz, vp),
     "qa_gemm_rows_fused": (C.c_int, vp, i32, i32, vp, i32, vp, i32, vp, vp, i32, f32, vp, i32, vp, sz, vp),
@@ -281,6 +285,10 @@ class Model:
         check(lib.qa_model_weights_view(self.handle, layers, self.cfg.n_layers, C.byref(w)))
         return layers, w
 
+    def write_gguf(self, path: str):
+        """Writes this model as a GGUF v3 checkpoint (qa_gguf_write_model)."""
+        check(lib.qa_gguf_write_model(self.handle, os.fsencode(path)))
+
     def embed(self, ids) -> np.ndarray:
         e = self.tensor("text.token_embd.weight").reshape(self.cfg.vocab, self.cfg.hidden)
         return np.ascontiguousarray(e[np.asarray(ids, dtype=np.int64)])
@@ -295,6 +303,22 @@ class Model:
             self.close()
         except Exception:
             pass
+
+
+def build_asr_prompt(audio_tokens: int, system_text: str = "", language: str = "") -> str:
+    """qwenasr_build_asr_prompt (tokenizer.cpp:529-549) through the C ABI."""
+    n = sz()
+    lib.qa_build_asr_prompt(audio_tokens, system_text.encode(), language.encode(), None, 0, C.byref(n))
+    buf = C.create_string_buffer(n.value + 1)
+    check(lib.qa_build_asr_prompt(audio_tokens, system_text.encode(), language.encode(), buf, n.value + 1, None))
+    return buf.value.decode()
+
+
+def wav_info(path: str) -> tuple[int, int]:
+    """(sample frames, sample rate) of a WAV file as the reference's reader counts them."""
+    n, rate = i64(), i32()
+    check(lib.qa_wav_info(os.fsencode(path), C.byref(n), C.byref(rate)))
+    return n.value, rate.value
 
 
 def prompt_input(model: Model, audio_tokens: int, prompt_tokens: int) -> np.ndarray:

@@ -34,7 +34,8 @@ def test_c_abi_exports_every_declared_symbol(qa):
     assert set(names) == set(qa.SIGNATURES), set(names) ^ set(qa.SIGNATURES)
 
 
-@pytest.mark.parametrize("header", ["text-decoder.h", "ggml-backends.h", "gguf-model.h", "decoder-input.h"])
+@pytest.mark.parametrize("header", ["text-decoder.h", "ggml-backends.h", "gguf-model.h", "decoder-input.h",
+                                    "tokenizer.h"])
 def test_cpp_drop_in_exports(header):
     syms = exported()
     names = header_functions(header)
@@ -87,7 +88,8 @@ def test_no_device_errors_are_loud(qa):
 
 
 def test_tool_argument_errors():
-    r = subprocess.run([TOOL, "--prefill", "--generate", "2"], capture_output=True, text=True, timeout=60)
+    r = subprocess.run([TOOL, "--size", "0.6b", "--prefill", "--generate", "2"], capture_output=True, text=True,
+                       timeout=60)
     assert r.returncode == 2 and "mutually exclusive" in r.stderr
     r = subprocess.run([TOOL, "--generate", "2000"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 2 and "up to 1024" in r.stderr

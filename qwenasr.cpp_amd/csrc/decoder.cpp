@@ -285,7 +285,7 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
         }
         Prof pr(d, kFamPrefillAttn);
         rc = causal_f32_launch(d->qkv, W3, d->qkv + QD, d->qkv + QD + KD, W3, rows, c.n_heads, c.n_kv_heads,
-                               d->scale, d->attn, s);
+                               d->scale, d->attn, QD, s);
         if (rc != QA_OK) return rc;
     } else if (kind == kDecode) {
         // append + attend in one launch: one token per stream at position d_lens[s]

@@ -60,6 +60,6 @@ int prefill_mfma_launch(const float * q, int32_t q_stride, const void * k, const
                         size_t workspace_bytes, hipStream_t stream);
 int causal_f32_launch(const float * q, int32_t q_stride, const float * k, const float * v, int64_t row_stride,
                       int32_t n_tokens, int32_t n_heads, int32_t n_kv_heads, float scale, float * out,
-                      hipStream_t stream);
+                      int32_t out_stride, hipStream_t stream);
 
 }  // namespace qa

@@ -30,7 +30,8 @@ struct RowsParams {
     float * out;              // [T][q_stride]
     int64_t head_stride;      // elements between KV heads
     int64_t row_stride;       // elements between positions
-    int32_t q_stride;
+    int32_t q_stride;         // elements between the q rows of two tokens
+    int32_t out_stride;       // elements between the output rows of two tokens
     int32_t n_past, n_tokens;
     float scale;
 };
@@ -188,7 +189,7 @@ __global__ __launch_bounds__(256) void prefill_rows_kernel(RowsParams p) {
     __syncthreads();
     const int hh = threadIdx.x >> 7;
     const int d = threadIdx.x & (kHeadDim - 1);
-    p.out[static_cast<int64_t>(t) * p.q_stride + (h0 + hh) * kHeadDim + d] =
+    p.out[static_cast<int64_t>(t) * p.out_stride + (h0 + hh) * kHeadDim + d] =
         (red[0][hh][d] + red[1][hh][d]) + (red[2][hh][d] + red[3][hh][d]);
 }
 
@@ -231,6 +232,7 @@ int prefill_attn_launch(const float * q, int32_t q_stride, const void * cache, c
     p.q = q;
     p.out = out;
     p.q_stride = q_stride;
+    p.out_stride = q_stride;
     p.n_past = n_past;
     p.n_tokens = n_tokens;
     p.scale = scale;
@@ -261,9 +263,14 @@ namespace qa {
 
 int causal_f32_launch(const float * q, int32_t q_stride, const float * k, const float * v, int64_t row_stride,
                       int32_t n_tokens, int32_t n_heads, int32_t n_kv_heads, float scale, float * out,
-                      hipStream_t stream) {
+                      int32_t out_stride, hipStream_t stream) {
     if (!q || !k || !v || !out || n_tokens <= 0 || n_kv_heads <= 0 || n_heads != kRep * n_kv_heads) {
         return fail(QA_ERR_INVALID, "causal f32 attention: invalid arguments");
+    }
+    // every row of q and of the output holds all n_heads heads: the kernel reads and writes
+    // [t * stride, t * stride + n_heads * head_dim) of each
+    if (q_stride < n_heads * kHeadDim || out_stride < n_heads * kHeadDim || row_stride < kHeadDim * n_kv_heads) {
+        return fail(QA_ERR_INVALID, "causal f32 attention: a row stride is shorter than its row");
     }
     if (n_tokens > kMaxRowsKeys) return fail(QA_ERR_INVALID, "causal f32 attention: more than 8192 tokens");
     RowsParams p{};
@@ -272,6 +279,7 @@ int causal_f32_launch(const float * q, int32_t q_stride, const float * k, const 
     p.v = v;
     p.out = out;
     p.q_stride = q_stride;
+    p.out_stride = out_stride;
     p.n_past = 0;
     p.n_tokens = n_tokens;
     p.scale = scale;
@@ -285,5 +293,6 @@ int causal_f32_launch(const float * q, int32_t q_stride, const float * k, const 
 extern "C" int qa_causal_attn_f32(const float * q, const float * k, const float * v, int32_t n_tokens,
                                   int32_t n_heads, int32_t n_kv_heads, float scale, float * out, void * stream) {
     return qa::causal_f32_launch(q, n_heads * qa::kHeadDim, k, v, static_cast<int64_t>(n_kv_heads) * qa::kHeadDim,
-                                 n_tokens, n_heads, n_kv_heads, scale, out, qa::as_stream(stream));
+                                 n_tokens, n_heads, n_kv_heads, scale, out, n_heads * qa::kHeadDim,
+                                 qa::as_stream(stream));
 }

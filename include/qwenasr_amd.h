@@ -154,6 +154,23 @@ int qa_decode_step_attn(const float * qkv, const float * q_norm_w, const float *
                         int32_t max_len, int32_t n_heads, float rope_theta, float eps, float scale, float * out,
                         void * workspace, size_t workspace_bytes, void * stream);
 
+/* Allocation-free qa_decode_step_attn.  No counterpart in the reference: it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * kernels, arguments and results as qa_decode_step_attn, without the workspace: it lives in a
+ * file-scope device array of QA_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds until
+ * the process ends.  The call allocates nothing (no hipMalloc, hipFree or allocating library routine);
+ * it zeroes its merge counters with a small kernel each time, so any sequence of calls with different
+ * layouts is correct.  A layout whose workspace (qa_decode_attn_workspace_bytes(layout->n_streams,
+ * n_heads, layout->max_seq)) exceeds the maximum is rejected with QA_ERR_INVALID before any launch;
+ * 48 MiB covers 32 streams of 4.5k positions or one stream of 150k.  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (different streams, threads or processes' graphs replayed
+ * concurrently) race and must be serialised by the caller.                                        */
+#define QA_NOALLOC_SCRATCH_BYTES ((size_t)48 << 20)
+int qa_decode_step_attn_noalloc(const float * qkv, const float * q_norm_w, const float * k_norm_w, void * cache,
+                                const qa_kv_layout * layout, int32_t layer, const int32_t * n_past, int32_t n_streams,
+                                int32_t max_len, int32_t n_heads, float rope_theta, float eps, float scale, float * out,
+                                void * stream);
+
 /* Causal prefill attention over the cache (row a7): the n_tokens queries of stream `stream_idx` at
  * positions n_past .. n_past + n_tokens - 1, query t attending keys [0, n_past + t].  Same
  * arithmetic as qa_decode_attn.  f16 caches run on CDNA4 f16 MFMA as two kernels (row statistics,

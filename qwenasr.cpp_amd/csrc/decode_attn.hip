@@ -50,6 +50,7 @@
 
 #include <cmath>
 #include <cstdlib>
+#include <mutex>
 
 namespace qa {
 namespace {
@@ -864,6 +865,45 @@ int decode_step_attn_launch(const float * qkv, const float * q_norm_w, const flo
     return launch_decode(p, true, make_rope_table(rope_theta), layout, n_streams, workspace, workspace_bytes, stream);
 }
 
+// ---- allocation-free variant (qa_decode_step_attn_noalloc)
+// The workspace of the decode step lives in this file-scope device array instead of memory the caller
+// or the library allocates.  Each GPU holds its own copy, at its own address, until the process ends.
+// Host code never passes `scratch` itself to a kernel (on the host that name is a stand-in, not a
+// device address): the address comes from hipGetSymbolAddress, once per device, with the device
+// current, and is kept in noalloc_ptrs.
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = QA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+void * noalloc_ptrs[kMaxDevices] = {};
+std::mutex noalloc_mutex;
+
+int noalloc_scratch(void ** out) {
+    int device = 0;
+    QA_HIP(hipGetDevice(&device));
+    if (device < 0 || device >= kMaxDevices) return fail(QA_ERR_DEVICE, "decode attention: device index out of range");
+    std::lock_guard<std::mutex> lock(noalloc_mutex);
+    if (!noalloc_ptrs[device]) {
+        void * p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_fail(e, "hipGetSymbolAddress (decode attention scratch)");
+        noalloc_ptrs[device] = p;
+    }
+    *out = noalloc_ptrs[device];
+    return QA_OK;
+}
+
+// Zeroes n 32-bit words with vector stores (a kernel rather than hipMemsetAsync, so a captured call
+// holds no memset node).
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t * p, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+}  // namespace
+
 size_t decode_attn_workspace(int32_t n_streams, int32_t n_kv_heads, int32_t max_seq) {
     if (n_streams <= 0 || n_kv_heads <= 0 || max_seq <= 0) return 0;
     return workspace_layout(n_streams, n_kv_heads, max_seq).total;
@@ -897,4 +937,35 @@ extern "C" int qa_decode_step_attn(const float * qkv, const float * q_norm_w, co
     }
     return decode_step_attn_launch(qkv, q_norm_w, k_norm_w, cache, *layout, layer, n_past, n_streams, max_len, n_heads,
                                    rope_theta, eps, scale, out, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int qa_decode_step_attn_noalloc(const float * qkv, const float * q_norm_w, const float * k_norm_w,
+                                           void * cache, const qa_kv_layout * layout, int32_t layer,
+                                           const int32_t * n_past, int32_t n_streams, int32_t max_len, int32_t n_heads,
+                                           float rope_theta, float eps, float scale, float * out, void * stream) {
+    using namespace qa;
+    if (qa_kv_layout_check(layout) != QA_OK) return QA_ERR_INVALID;
+    if (!qkv || !q_norm_w || !k_norm_w || !cache || !n_past || !out) {
+        return fail(QA_ERR_INVALID, "qa_decode_step_attn_noalloc: null pointer");
+    }
+    if (n_heads <= 0 || n_heads % kRep != 0) return fail(QA_ERR_INVALID, "qa_decode_step_attn_noalloc: invalid n_heads");
+    const Workspace w = workspace_layout(layout->n_streams, layout->n_kv_heads, layout->max_seq);
+    if (w.total > kNoAllocScratchBytes) {
+        return fail(QA_ERR_INVALID, "qa_decode_step_attn_noalloc: the cache capacity needs " + std::to_string(w.total) +
+                                        " bytes of scratch, more than its maximum of " +
+                                        std::to_string(kNoAllocScratchBytes));
+    }
+    int rc = check_shape(*layout, n_streams, max_len, n_heads, layer);
+    if (rc != QA_OK) return rc;
+    void * base = nullptr;
+    rc = noalloc_scratch(&base);
+    if (rc != QA_OK) return rc;
+    // A previous call may have used another capacity, whose partials now lie where this layout keeps
+    // its merge counters: clear this layout's counters on every call.
+    const int64_t n_words = static_cast<int64_t>((w.total - w.counters) / sizeof(uint32_t));
+    hipLaunchKernelGGL(zero_words_kernel, dim3(static_cast<unsigned>((n_words + 255) / 256)), dim3(256), 0,
+                       as_stream(stream), reinterpret_cast<uint32_t *>(static_cast<char *>(base) + w.counters), n_words);
+    QA_LAUNCH_CHECK("zero_words_kernel");
+    return decode_step_attn_launch(qkv, q_norm_w, k_norm_w, cache, *layout, layer, n_past, n_streams, max_len, n_heads,
+                                   rope_theta, eps, scale, out, base, w.total, as_stream(stream));
 }

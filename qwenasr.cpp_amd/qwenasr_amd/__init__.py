@@ -22,6 +22,7 @@ LIB_PATH = os.path.join(_PKG_DIR, "libqwenasr_amd.so")
 
 QA_OK, QA_ERR_INVALID, QA_ERR_CAPACITY, QA_ERR_DEVICE, QA_ERR_NO_DEVICE, QA_ERR_ALLOC, QA_ERR_RANGE = range(7)
 QA_CACHE_F32, QA_CACHE_F16 = 0, 1
+QA_NOALLOC_SCRATCH_BYTES = 48 << 20   # include/qwenasr_amd.h
 
 
 class QaError(RuntimeError):
@@ -97,6 +98,8 @@ SIGNATURES = {
     "qa_decode_attn": (C.c_int, vp, vp, C.POINTER(KvLayout), i32, vp, i32, i32, i32, f32, vp, vp, sz, vp),
     "qa_decode_step_attn": (C.c_int, vp, vp, vp, vp, C.POINTER(KvLayout), i32, vp, i32, i32, i32, f32, f32, f32, vp,
                             vp, sz, vp),
+    "qa_decode_step_attn_noalloc": (C.c_int, vp, vp, vp, vp, C.POINTER(KvLayout), i32, vp, i32, i32, i32, f32, f32,
+                                    f32, vp, vp),
     "qa_prefill_attn_workspace_bytes": (sz, i32, i32),
     "qa_prefill_attn": (C.c_int, vp, vp, C.POINTER(KvLayout), i32, i32, i32, i32, i32, f32, vp, vp, sz, vp),
     "qa_causal_attn_f32": (C.c_int, vp, vp, vp, i32, i32, i32, f32, vp, vp),

@@ -2,8 +2,13 @@
 
     python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--config 3] [--no-cpu-baseline]
 
-Workload (config 3): Qwen3-ASR-1.7B decoder, seeded N(0, 0.02) f32 weights, f16 KV cache, prefill of
-3913 positions (3900 audio rows + 13 random prompt ids), then greedy decode at ~4k context.
+Workload (config 3): Qwen3-ASR-1.7B decoder, seeded N(0, 0.02) weights, f16 KV cache, prefill of
+3913 positions (3900 audio rows + 13 random prompt ids), then greedy decode at ~4k context.  The
+weights are rounded to bf16 values and kept as f32 (--weights bf16-exact, the default): a checkpoint
+converted from the released bf16 weights holds exactly such values (convert.py:386-387 widens each
+bf16 tensor with tensor.float()).  The decoder then streams bf16 copies of them and computes the same
+f32 results; --weights f32 keeps unrounded draws (f32 weights streamed).  A short decode of the same
+model with the f32 weights streamed (QA_WEIGHTS_F32=1) is reported beside the main figure.
 A step is one decode token: embedding gather, 28 layers (q|k|v GEMV, fused K/V append + split-K
 attention, o / gate-up / down GEMVs), LM head and device argmax.  value = decode tokens/s over exactly
 --steps steps, weights and cache resident in HBM, bracketed by device synchronisation.
@@ -340,6 +345,10 @@ def main():
     ap.add_argument("--multistream-steps", type=int, default=16)
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--weights", choices=["bf16-exact", "f32"], default="bf16-exact",
+                    help="bf16-exact: weights rounded to bf16 values (a converted bf16 checkpoint); f32: unrounded")
+    ap.add_argument("--f32-compare-steps", type=int, default=64,
+                    help="decode steps timed with the f32 weights streamed, on the same model (0: skip)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 10 times (reference for HBM traffic counters)")
     ap.add_argument("--kernel", choices=["append", "prefill", "decode-attn", "multistream", "multistream-attn"],
@@ -364,12 +373,13 @@ def main():
     assert qa.device_count() > 0, "bench.py needs a HIP device"
     w = configs.CONFIGS[args.config]
     t0 = time.perf_counter()
-    model = qa.Model(w.size, n_layers=w.n_layers)
+    model = qa.Model(w.size, n_layers=w.n_layers, bf16=args.weights == "bf16-exact")
     x = qa.prompt_input(model, w.audio_tokens, w.prompt_tokens)
-    log(f"synthetic {w.size.name} built in {time.perf_counter() - t0:.1f}s")
+    log(f"synthetic {w.size.name} ({args.weights} weights) built in {time.perf_counter() - t0:.1f}s")
     max_seq = w.prompt + args.warmup + args.steps + args.profile_steps + 2
     dec = qa.Decoder(model, 1, max_seq, w.cache_type)
-    log(f"decoder ready (weights + {max_seq}-position f16 cache on device)")
+    weights_streamed = "bf16 copies of bf16-exact weights" if dec.weights_bf16 else "f32"
+    log(f"decoder ready (weights + {max_seq}-position f16 cache on device; GEMVs stream {weights_streamed})")
 
     # the first prefill also allocates the prompt-sized workspaces and loads rocBLAS's kernels; the
     # second (same input, n_past 0 again: the cache rows are rewritten) is the steady-state time
@@ -411,6 +421,28 @@ def main():
     log("per-step device time by family, event-bracketed (ms): " +
         ", ".join(f"{k} {v[0] / args.profile_steps:.3f}" for k, v in fam.items()))
 
+    f32_cmp = None
+    if args.f32_compare_steps > 0 and dec.weights_bf16:
+        # the same model and context with the f32 weights streamed (the kernels the golden tests pin)
+        os.environ["QA_WEIGHTS_F32"] = "1"
+        d32 = qa.Decoder(model, 1, max_seq, w.cache_type)
+        del os.environ["QA_WEIGHTS_F32"]
+        d32.forward(x, 0, want_logits=False)
+        warm = d32.decode_streams(np.array([first], np.int32), args.warmup) if args.warmup else np.array([[first]])
+        qa.check(qa.lib.qa_device_synchronize())
+        t1 = time.perf_counter()
+        ids32 = d32.decode_streams(np.array([int(warm[-1, 0])], np.int32), args.f32_compare_steps)
+        qa.check(qa.lib.qa_device_synchronize())
+        dt32 = time.perf_counter() - t1
+        d32.close()
+        # the same arithmetic on the same values: the ids follow the main run's token for token
+        n_cmp = min(args.f32_compare_steps, args.steps)
+        same = bool(np.array_equal(ids32[:n_cmp, 0], ids[:n_cmp, 0]))
+        f32_cmp = {"steps": args.f32_compare_steps, "ms_per_step": round(dt32 * 1e3 / args.f32_compare_steps, 4),
+                   "tok_s": round(args.f32_compare_steps / dt32, 3), "ids_equal_to_main_run": same,
+                   "weight_bytes_per_token": None}
+        log(f"same model, f32 weights streamed: {f32_cmp['ms_per_step']:.3f} ms/token (ids equal: {same})")
+
     attn_us, L, attn_bytes, n_launch = attention_roofline(qa, dec, args.roofline_reps)
     achieved = attn_bytes / (attn_us * 1e-6) / 1e9
     log(f"decode-step attention: {attn_us:.2f} us per launch over {n_launch} launches at L={L}: "
@@ -430,9 +462,12 @@ def main():
         f"(device ms per step by family: {ms4['family_ms_per_step']})")
 
     traffic, traffic_note = measured_traffic(attn_bytes)
-    weight_bytes = int(4 * sum(model.tensor(n).size for n in (
+    n_weights = int(sum(model.tensor(n).size for n in (
         [f"text.blk.{l}.{t}.weight" for l in range(model.cfg.n_layers) for t in
          ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")] + ["text.output.weight"])))
+    weight_bytes = n_weights * (2 if weights_streamed != "f32" else 4)
+    if f32_cmp is not None:
+        f32_cmp["weight_bytes_per_token"] = 4 * n_weights
     result = {
         "metric": METRIC,
         "value": round(args.steps / dt, 3),
@@ -445,11 +480,13 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded N(0,0.02) f32 weights, N(0,1) audio rows, random prompt ids)",
+        "data": (f"synthetic (seeded N(0,0.02) weights{', rounded to bf16 values as in a converted bf16 checkpoint' if args.weights == 'bf16-exact' else ''}, "
+                 f"N(0,1) audio rows, random prompt ids)"),
         "config": {"workload": f"config {args.config}: {w.size.name} decoder, prefill {w.prompt} positions, greedy "
                                f"decode of {args.steps} tokens at context {ctx0}..{ctx0 + args.steps}, f16 KV cache, "
-                               f"f32 weights, batch 1",
-                   "kv_cache": "f16", "prompt_positions": w.prompt},
+                               f"{args.weights} weights, batch 1",
+                   "kv_cache": "f16", "prompt_positions": w.prompt, "weights": args.weights,
+                   "weights_streamed": weights_streamed},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": traffic_note,
                      "kernel": "decode attention of one layer: decode_scores_kernel (fused K/V append) + "
@@ -464,6 +501,7 @@ def main():
         "prefill_family_ms": prefill_fam,
         "weight_bytes_per_token": weight_bytes,
         "weight_stream_gbs": round(weight_bytes / (dt / args.steps) / 1e9, 1),
+        "decode_f32_weights_streamed": f32_cmp,
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(model, ctx0, args.cpu_steps)

@@ -227,6 +227,18 @@ int qa_gemm_rows_fused(const float * W, int32_t out_dim, int32_t in_dim, const f
 /* y[r][o] = sum_i W[o][i] * x[r][i]  (+ y[r][o] when accumulate != 0); rows small (decode).     */
 int qa_gemv(const float * W, int32_t out_dim, int32_t in_dim, const float * x, int32_t rows,
             float * y, int32_t accumulate, void * stream);
+/* One decode-step GEMV with its fused neighbours (text-decoder.cpp:365-373, 465-493, 602), the     *
+ * kernel the decoder runs at batch 1: y = W x (epilogue 0), y += W x (1), or y[o] = silu(g) * u     *
+ * with W = [gate rows; up rows] of 2 out_dim rows (2); norm_w != NULL first replaces x by           *
+ * RMSNorm(x) * norm_w (eps).  Pass the weights as f32 (W) or, for bf16-exact weights, as their     *
+ * bf16 bits (W_bf16, see qa_pack_bf16): both give the same result bit for bit.                     *
+ * in_dim one of 1024, 2048, 3072, 4096, 6144.                                                       */
+int qa_gemv_fused(const float * W, const uint16_t * W_bf16, int32_t out_dim, int32_t in_dim, const float * x,
+                  float * y, int32_t epilogue, const float * norm_w, float eps, void * stream);
+/* dst[i] = the high 16 bits of src[i] (device buffers); *inexact (device, cleared by the caller)     *
+ * gets bit 0 set when any low half is non-zero, i.e. when src is not bf16-exact.  A checkpoint      *
+ * converted from bf16 weights (convert.py:386-387 widens them with tensor.float()) is bf16-exact.  */
+int qa_pack_bf16(const float * src, int64_t n, uint16_t * dst, uint32_t * inexact, void * stream);
 /* RMSNorm of each row (text-decoder.cpp:92-98): y = x * (1/sqrtf(mean(x^2) + eps)) * w.          */
 int qa_rmsnorm_rows(const float * x, const float * w, int32_t rows, int32_t dim, float eps, float * y,
                     void * stream);
@@ -292,6 +304,9 @@ void qa_synth_fill_ids(int32_t * out, size_t n, uint64_t base_seed, const char *
  * GGUF tensor name, norm weights 1.0, output.weight tied to token_embd (same host buffer).       */
 typedef struct qa_model qa_model;
 int qa_model_synthetic(const qa_text_config * cfg, uint64_t seed, qa_model ** out);
+/* Rounds every tensor of the model to the nearest bf16 value (ties to even), kept as f32: the      *
+ * values a checkpoint converted from the released bf16 weights holds (convert.py:386-387).        */
+int qa_model_round_bf16(qa_model * model);
 void qa_model_free(qa_model * model);
 /* Host view of one tensor by GGUF name (e.g. "text.blk.3.attn_q.weight"); NULL if absent. */
 const float * qa_model_tensor(const qa_model * model, const char * name, int64_t * n_elems);
@@ -353,6 +368,10 @@ typedef struct qa_decoder qa_decoder;
 int qa_decoder_create(const qa_text_config * cfg, const qa_model_weights * weights, int32_t n_streams,
                       int32_t max_seq, int32_t cache_type, qa_decoder ** out);
 void qa_decoder_destroy(qa_decoder * dec);
+/* 1 when the decoder holds bf16 copies of its projection and LM-head weights (every one of them was   *
+ * bf16-exact at creation, as in a checkpoint converted from bf16 weights, convert.py:386-387, and    *
+ * QA_WEIGHTS_F32=1 was not set), which the batch-1 GEMVs then read with unchanged f32 results.     */
+int qa_decoder_weights_bf16(const qa_decoder * dec);
 /* Host mirror of the per-stream lengths (cur_len of the reference, text-decoder.cpp:186). */
 int qa_decoder_cur_len(const qa_decoder * dec, int32_t stream, int32_t * cur_len);
 /* Reads the device-side lengths (what the kernels use) into lens[n_streams]. */

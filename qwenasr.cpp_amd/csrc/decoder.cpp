@@ -31,6 +31,12 @@ struct DevLayer {
     float * k_norm = nullptr;
     float * gu = nullptr;      // [2 intermediate][hidden]     (gate rows, up rows)
     float * down = nullptr;    // [hidden][intermediate]
+    // bf16 copies of the projection weights (their high halves), present only when every weight of
+    // the model is bf16-exact; the batch-1 GEMVs read these
+    uint16_t * qkv16 = nullptr;
+    uint16_t * o16 = nullptr;
+    uint16_t * gu16 = nullptr;
+    uint16_t * down16 = nullptr;
 };
 
 enum Kind { kDecode = 0, kPrefill = 1, kNoCache = 2 };
@@ -51,7 +57,9 @@ struct qa_decoder {
     float * embd = nullptr;
     float * out_norm = nullptr;
     float * out_w = nullptr;
+    uint16_t * out_w16 = nullptr;
     std::vector<void *> weight_allocs;
+    std::vector<void *> b16_allocs;     // the bf16 weight copies (freed again if the model is not exact)
     void * cache = nullptr;
     qa_kv_layout layout{};
     int32_t * d_lens = nullptr;
@@ -267,7 +275,8 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
     {
         Prof pr(d, kFamProj);
         if (rows == 1) {
-            rc = gemv_launch(kEpiStoreOp, true, L.qkv, W3, H, d->x, d->qkv, L.attn_norm, c.rms_norm_eps, s);
+            rc = gemv_launch(kEpiStoreOp, true, L.qkv, W3, H, d->x, d->qkv, L.attn_norm, c.rms_norm_eps, s,
+                             L.qkv16);
         } else if (fused) {
             rc = fused_gemm(d, L.qkv, W3, H, d->x, rows, d->qkv, false, norm_in(d, L.attn_norm));
         } else {
@@ -308,9 +317,11 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
     }
     Prof pr(d, kFamProj);
     if (rows == 1) {
-        rc = gemv_launch(kEpiAccumOp, false, L.o, H, QD, d->attn, d->x, nullptr, 0.0f, s);
-        if (rc == QA_OK) rc = gemv_launch(kEpiSwigluOp, true, L.gu, I, H, d->x, d->act, L.ffn_norm, c.rms_norm_eps, s);
-        if (rc == QA_OK) rc = gemv_launch(kEpiAccumOp, false, L.down, H, I, d->act, d->x, nullptr, 0.0f, s);
+        rc = gemv_launch(kEpiAccumOp, false, L.o, H, QD, d->attn, d->x, nullptr, 0.0f, s, L.o16);
+        if (rc == QA_OK) {
+            rc = gemv_launch(kEpiSwigluOp, true, L.gu, I, H, d->x, d->act, L.ffn_norm, c.rms_norm_eps, s, L.gu16);
+        }
+        if (rc == QA_OK) rc = gemv_launch(kEpiAccumOp, false, L.down, H, I, d->act, d->x, nullptr, 0.0f, s, L.down16);
     } else if (fused) {
         GemmRowsFusion gu = norm_in(d, L.ffn_norm);
         gu.swiglu = true;
@@ -337,7 +348,7 @@ int logits_and_pick(qa_decoder * d, int32_t first, int32_t rows, bool pick, bool
         const float * xr = d->x + static_cast<int64_t>(first) * c.hidden;
         if (rows == 1) {
             rc = gemv_launch(kEpiStoreOp, true, d->out_w, c.vocab, c.hidden, xr, d->logits, d->out_norm,
-                             c.rms_norm_eps, d->stream);
+                             c.rms_norm_eps, d->stream, d->out_w16);
         } else if (fused && first == 0) {
             rc = fused_gemm(d, d->out_w, c.vocab, c.hidden, xr, rows, d->logits, false, norm_in(d, d->out_norm));
         } else {
@@ -408,7 +419,49 @@ float top2_margin(const std::vector<float> & v, int32_t best) {
     return v[best] - second;
 }
 
+// bf16 copies of the projection and LM-head weights for the batch-1 GEMVs, kept only when every one
+// of them is bf16-exact (a checkpoint converted from bf16 weights); then the GEMVs read half the bytes
+// and compute the same f32 results.  QA_WEIGHTS_F32=1 keeps the f32 weights only.
+int pack_weights_bf16(qa_decoder * d) {
+    const char * e = std::getenv("QA_WEIGHTS_F32");
+    if (e && std::strcmp(e, "1") == 0) return QA_OK;
+    const qa_text_config & c = d->cfg;
+    const size_t H = c.hidden, QD = static_cast<size_t>(c.n_heads) * kHeadDim,
+                 KD = static_cast<size_t>(c.n_kv_heads) * kHeadDim, I = c.intermediate;
+    uint32_t * flag = nullptr;
+    int rc = dmalloc_t(d->b16_allocs, 64, &flag);
+    if (rc == QA_OK && hipMemsetAsync(flag, 0, 4, d->stream) != hipSuccess) rc = fail(QA_ERR_DEVICE, "clear failed");
+    auto pack = [&](const float * src, size_t n, uint16_t ** dst) {
+        if (rc != QA_OK) return;
+        rc = dmalloc_t(d->b16_allocs, n, dst);
+        if (rc == QA_OK) rc = pack_bf16_launch(src, static_cast<int64_t>(n), *dst, flag, d->stream);
+    };
+    for (DevLayer & L : d->layers) {
+        pack(L.qkv, (QD + 2 * KD) * H, &L.qkv16);
+        pack(L.o, H * QD, &L.o16);
+        pack(L.gu, 2 * I * H, &L.gu16);
+        pack(L.down, H * I, &L.down16);
+    }
+    if (d->out_w) pack(d->out_w, static_cast<size_t>(c.vocab) * H, &d->out_w16);
+    uint32_t inexact = 1;
+    if (rc == QA_OK && (hipMemcpyAsync(&inexact, flag, 4, hipMemcpyDeviceToHost, d->stream) != hipSuccess ||
+                        hipStreamSynchronize(d->stream) != hipSuccess)) {
+        rc = fail(QA_ERR_DEVICE, "bf16 weight check failed");
+    }
+    if (rc != QA_OK || inexact != 0) {
+        for (void * p : d->b16_allocs) (void)hipFree(p);
+        d->b16_allocs.clear();
+        for (DevLayer & L : d->layers) L.qkv16 = L.o16 = L.gu16 = L.down16 = nullptr;
+        d->out_w16 = nullptr;
+    }
+    return rc;
+}
+
 }  // namespace
+
+extern "C" int qa_decoder_weights_bf16(const qa_decoder * d) {
+    return d && !d->layers.empty() && d->layers[0].qkv16 ? 1 : 0;
+}
 
 extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weights * w, int32_t n_streams,
                                  int32_t max_seq, int32_t cache_type, qa_decoder ** out) {
@@ -490,6 +543,8 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
         }
     }
     if (rc != QA_OK) return bail(rc);
+    rc = pack_weights_bf16(d);
+    if (rc != QA_OK) return bail(rc);
 
     d->layout.n_layers = cfg->n_layers;
     d->layout.n_streams = n_streams;
@@ -534,6 +589,7 @@ extern "C" void qa_decoder_destroy(qa_decoder * d) {
     }
     free_acts(d);
     for (void * p : d->weight_allocs) (void)hipFree(p);
+    for (void * p : d->b16_allocs) (void)hipFree(p);
     if (d->staging) (void)hipFree(d->staging);
     if (d->cache) (void)hipFree(d->cache);
     if (d->h_ids) (void)hipHostFree(d->h_ids);

@@ -3,9 +3,14 @@
 //
 // These replace the GGML ops around the KV-cache path in text-decoder.cpp:365-373 and 465-493
 // (linear_ggml with PREC_F32, rms_norm * w, silu * up, add, logits view) and the host argmax of
-// 2266-2274.  Weights stay f32 (the reference requires f32 tensors, require_f32_tensor 29-42), so a
+// 2266-2274.  Weights are f32 (the reference requires f32 tensors, require_f32_tensor 29-42), so a
 // decode step streams every weight byte once: the GEMV is HBM-bound and is written for that --
 // each wave keeps its input row in registers and walks whole weight rows with 16-byte loads.
+//
+// A checkpoint converted from the released bf16 weights (convert.py:386-387 widens bf16 tensors
+// with tensor.float()) holds f32 values whose low 16 bits are zero.  For such weights the GEMV can
+// read a bf16 copy (the high halves) and widen each value back to the same f32 in registers: the
+// products and sums are the f32 kernel's, operation for operation, at half the bytes.
 #include "ops.hpp"
 
 #include <algorithm>
@@ -18,7 +23,8 @@ namespace {
 enum { kEpiStore = 0, kEpiAccum = 1, kEpiSwiglu = 2 };
 
 struct GemvParams {
-    const float * W;        // [rows_w][in_dim]; for SwiGLU rows_w = 2 * out_dim (gate rows, then up rows)
+    const void * W;         // [rows_w][in_dim] f32, or bf16 bits (B16); for SwiGLU rows_w = 2 * out_dim
+                            // (gate rows, then up rows)
     const float * x;        // [in_dim]
     float * y;              // [out_dim]
     const float * norm_w;   // pre-RMSNorm weight (PRENORM only)
@@ -48,11 +54,27 @@ __device__ inline float dot4(const f4 a, const f4 b, float acc) {
     return acc;
 }
 
+typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+
+// four bf16 values (little-endian: element 0 in the low half of .x) widened to the f32 values whose
+// high halves they are
+__device__ inline f4 widen_bf16x4(const u2 b) {
+    f4 r;
+    r.x = __uint_as_float(b.x << 16);
+    r.y = __uint_as_float(b.x & 0xffff0000u);
+    r.z = __uint_as_float(b.y << 16);
+    r.w = __uint_as_float(b.y & 0xffff0000u);
+    return r;
+}
+
 // IN4 = in_dim / 256 (each lane holds 4 * IN4 input elements), NR rows per wave iteration.
 // Load order: x and the norm weight first, then the weight rows of the wave's first iteration, so the
 // RMSNorm of x (which waits for its own loads only: vector loads complete in issue order) runs while
 // the weight rows stream in.  Rows past out_dim re-read the last row and are not stored.
-template <int IN4, int NR, int EPI, bool PRENORM>
+// B16: W holds bf16 bits; lane l reads elements k 256 + 4 l .. + 3 as one 8-byte load where the f32
+// kernel reads them as one 16-byte load, so both kernels assign every element to the same lane, step
+// and fmaf.
+template <int IN4, int NR, int EPI, bool PRENORM, bool B16>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & (kWave - 1);
@@ -69,20 +91,37 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     }
     f4 wv[NR][IN4];
     f4 wu[NR][IN4];
+    u2 bv[NR][IN4];
+    u2 bu[NR][IN4];
     auto load_rows = [&](int o0) {
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-            const int o = min(o0 + r, p.out_dim - 1);
-            const float * wr = p.W + o * in + lane * 4;
-#pragma unroll
-            for (int k = 0; k < IN4; ++k) {
-                wv[r][k] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(wr + k * 256));
-            }
-            if constexpr (EPI == kEpiSwiglu) {
-                const float * wur = p.W + (o + p.out_dim) * in + lane * 4;
+            const int64_t o = min(o0 + r, p.out_dim - 1);
+            if constexpr (B16) {
+                const uint16_t * wr = static_cast<const uint16_t *>(p.W) + o * in + lane * 4;
 #pragma unroll
                 for (int k = 0; k < IN4; ++k) {
-                    wu[r][k] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(wur + k * 256));
+                    bv[r][k] = __builtin_nontemporal_load(reinterpret_cast<const u2 *>(wr + k * 256));
+                }
+                if constexpr (EPI == kEpiSwiglu) {
+                    const uint16_t * wur = static_cast<const uint16_t *>(p.W) + (o + p.out_dim) * in + lane * 4;
+#pragma unroll
+                    for (int k = 0; k < IN4; ++k) {
+                        bu[r][k] = __builtin_nontemporal_load(reinterpret_cast<const u2 *>(wur + k * 256));
+                    }
+                }
+            } else {
+                const float * wr = static_cast<const float *>(p.W) + o * in + lane * 4;
+#pragma unroll
+                for (int k = 0; k < IN4; ++k) {
+                    wv[r][k] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(wr + k * 256));
+                }
+                if constexpr (EPI == kEpiSwiglu) {
+                    const float * wur = static_cast<const float *>(p.W) + (o + p.out_dim) * in + lane * 4;
+#pragma unroll
+                    for (int k = 0; k < IN4; ++k) {
+                        wu[r][k] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(wur + k * 256));
+                    }
                 }
             }
         }
@@ -123,8 +162,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
         for (int r = 0; r < NR; ++r) {
 #pragma unroll
             for (int k = 0; k < IN4; ++k) {
-                acc[r] = dot4(wv[r][k], xv[k], acc[r]);
-                if constexpr (EPI == kEpiSwiglu) accu[r] = dot4(wu[r][k], xv[k], accu[r]);
+                if constexpr (B16) {
+                    acc[r] = dot4(widen_bf16x4(bv[r][k]), xv[k], acc[r]);
+                    if constexpr (EPI == kEpiSwiglu) accu[r] = dot4(widen_bf16x4(bu[r][k]), xv[k], accu[r]);
+                } else {
+                    acc[r] = dot4(wv[r][k], xv[k], acc[r]);
+                    if constexpr (EPI == kEpiSwiglu) accu[r] = dot4(wu[r][k], xv[k], accu[r]);
+                }
             }
         }
 #pragma unroll
@@ -145,19 +189,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     }
 }
 
-template <int IN4, int NR, int EPI, bool PRENORM>
+template <int IN4, int NR, int EPI, bool PRENORM, bool B16>
 int launch_gemv_t(const GemvParams & p, hipStream_t stream) {
     const int64_t waves = (static_cast<int64_t>(p.out_dim) + NR - 1) / NR;
     int64_t blocks = (waves + 3) / 4;
     if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL((gemv_kernel<IN4, NR, EPI, PRENORM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+    hipLaunchKernelGGL((gemv_kernel<IN4, NR, EPI, PRENORM, B16>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                        stream, p);
     QA_LAUNCH_CHECK("gemv_kernel");
     return QA_OK;
 }
 
 // Rows per wave: the default keeps 16-32 KB of weights in flight per wave (measured on the 1.7B decode
-// step: 2 rows at in_dim 2048 beat 4 by 1.6%); QA_GEMV_NR = 1, 2 or 4 overrides it (tuning).
+// step: 2 f32 rows at in_dim 2048 beat 4 by 1.6%); QA_GEMV_NR = 1, 2 or 4 overrides it (tuning).
 int gemv_rows_override() {
     static const int v = [] {
         const char * e = std::getenv("QA_GEMV_NR");
@@ -167,27 +211,48 @@ int gemv_rows_override() {
     return v;
 }
 
-template <int IN4, int EPI, bool PRENORM>
+template <int IN4, int EPI, bool PRENORM, bool B16>
 int launch_gemv_nr(int nr, const GemvParams & p, hipStream_t stream) {
     switch (nr) {
-        case 1: return launch_gemv_t<IN4, 1, EPI, PRENORM>(p, stream);
-        case 2: return launch_gemv_t<IN4, 2, EPI, PRENORM>(p, stream);
-        default: return launch_gemv_t<IN4, 4, EPI, PRENORM>(p, stream);
+        case 1: return launch_gemv_t<IN4, 1, EPI, PRENORM, B16>(p, stream);
+        case 2: return launch_gemv_t<IN4, 2, EPI, PRENORM, B16>(p, stream);
+        default: return launch_gemv_t<IN4, 4, EPI, PRENORM, B16>(p, stream);
+    }
+}
+
+// default rows per wave: about 16 KB (32 KB for gate|up, which reads two rows per output) of weights
+// per wave, i.e. twice the f32 row count for bf16 rows
+template <int EPI, bool PRENORM, bool B16>
+int launch_gemv_in(const GemvParams & p, hipStream_t stream) {
+    const int forced = gemv_rows_override();
+    const bool sw = EPI == kEpiSwiglu;
+    auto nr = [&](int f32_rows) { return forced ? forced : B16 ? std::min(4, 2 * f32_rows) : f32_rows; };
+    switch (p.in_dim) {
+        case 1024: return launch_gemv_nr<4, EPI, PRENORM, B16>(nr(sw ? 2 : 4), p, stream);
+        case 2048: return launch_gemv_nr<8, EPI, PRENORM, B16>(nr(2), p, stream);
+        case 3072: return launch_gemv_nr<12, EPI, PRENORM, B16>(nr(sw ? 1 : 2), p, stream);
+        case 4096: return launch_gemv_nr<16, EPI, PRENORM, B16>(nr(sw ? 1 : 2), p, stream);
+        case 6144: return launch_gemv_nr<24, EPI, PRENORM, B16>(nr(1), p, stream);
+        default: return fail(QA_ERR_INVALID, "gemv: in_dim must be one of 1024, 2048, 3072, 4096, 6144");
     }
 }
 
 template <int EPI, bool PRENORM>
-int launch_gemv_in(const GemvParams & p, hipStream_t stream) {
-    const int forced = gemv_rows_override();
-    const bool sw = EPI == kEpiSwiglu;
-    switch (p.in_dim) {
-        case 1024: return launch_gemv_nr<4, EPI, PRENORM>(forced ? forced : sw ? 2 : 4, p, stream);
-        case 2048: return launch_gemv_nr<8, EPI, PRENORM>(forced ? forced : 2, p, stream);
-        case 3072: return launch_gemv_nr<12, EPI, PRENORM>(forced ? forced : sw ? 1 : 2, p, stream);
-        case 4096: return launch_gemv_nr<16, EPI, PRENORM>(forced ? forced : sw ? 1 : 2, p, stream);
-        case 6144: return launch_gemv_nr<24, EPI, PRENORM>(forced ? forced : 1, p, stream);
-        default: return fail(QA_ERR_INVALID, "gemv: in_dim must be one of 1024, 2048, 3072, 4096, 6144");
+int launch_gemv_w(const GemvParams & p, bool b16, hipStream_t stream) {
+    return b16 ? launch_gemv_in<EPI, PRENORM, true>(p, stream) : launch_gemv_in<EPI, PRENORM, false>(p, stream);
+}
+
+// dst[i] = high half of src[i]; *inexact |= 1 where a low half is non-zero (src not bf16-exact)
+__global__ __launch_bounds__(256) void pack_bf16_kernel(const float * src, int64_t n, uint16_t * dst,
+                                                        uint32_t * inexact) {
+    uint32_t bad = 0;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) {
+        const uint32_t b = __float_as_uint(src[i]);
+        bad |= b & 0xffffu;
+        dst[i] = static_cast<uint16_t>(b >> 16);
     }
+    if (__any(bad != 0) && (threadIdx.x & (kWave - 1)) == 0) atomicOr(inexact, 1u);
 }
 
 // ---------------------------------------------------------------- skinny GEMM (2..64 token rows)
@@ -854,12 +919,23 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float * logits, int v
 }  // namespace
 
 int gemv_launch(int epi, bool prenorm, const float * W, int32_t out_dim, int32_t in_dim, const float * x,
-                float * y, const float * norm_w, float eps, hipStream_t stream) {
-    GemvParams p{W, x, y, norm_w, out_dim, in_dim, eps};
-    if (!W || !x || !y || out_dim <= 0 || (prenorm && !norm_w)) return fail(QA_ERR_INVALID, "gemv: invalid arguments");
-    if (epi == kEpiStore) return prenorm ? launch_gemv_in<kEpiStore, true>(p, stream) : launch_gemv_in<kEpiStore, false>(p, stream);
-    if (epi == kEpiAccum) return prenorm ? launch_gemv_in<kEpiAccum, true>(p, stream) : launch_gemv_in<kEpiAccum, false>(p, stream);
-    return prenorm ? launch_gemv_in<kEpiSwiglu, true>(p, stream) : launch_gemv_in<kEpiSwiglu, false>(p, stream);
+                float * y, const float * norm_w, float eps, hipStream_t stream, const uint16_t * W16) {
+    GemvParams p{W16 ? static_cast<const void *>(W16) : static_cast<const void *>(W), x, y, norm_w, out_dim, in_dim,
+                 eps};
+    const bool b16 = W16 != nullptr;
+    if (!p.W || !x || !y || out_dim <= 0 || (prenorm && !norm_w)) return fail(QA_ERR_INVALID, "gemv: invalid arguments");
+    if (epi == kEpiStore) return prenorm ? launch_gemv_w<kEpiStore, true>(p, b16, stream) : launch_gemv_w<kEpiStore, false>(p, b16, stream);
+    if (epi == kEpiAccum) return prenorm ? launch_gemv_w<kEpiAccum, true>(p, b16, stream) : launch_gemv_w<kEpiAccum, false>(p, b16, stream);
+    return prenorm ? launch_gemv_w<kEpiSwiglu, true>(p, b16, stream) : launch_gemv_w<kEpiSwiglu, false>(p, b16, stream);
+}
+
+int pack_bf16_launch(const float * src, int64_t n, uint16_t * dst, uint32_t * inexact, hipStream_t stream) {
+    if (!src || !dst || !inexact || n < 0) return fail(QA_ERR_INVALID, "pack_bf16: invalid arguments");
+    if (n == 0) return QA_OK;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
+    hipLaunchKernelGGL(pack_bf16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, src, n, dst, inexact);
+    QA_LAUNCH_CHECK("pack_bf16_kernel");
+    return QA_OK;
 }
 
 size_t gemm_rows_workspace_bytes(int32_t N, int32_t K, int32_t rows) {
@@ -1002,6 +1078,19 @@ extern "C" int qa_gemv(const float * W, int32_t out_dim, int32_t in_dim, const f
         if (rc != QA_OK) return rc;
     }
     return QA_OK;
+}
+
+extern "C" int qa_gemv_fused(const float * W, const uint16_t * W_bf16, int32_t out_dim, int32_t in_dim,
+                             const float * x, float * y, int32_t epilogue, const float * norm_w, float eps,
+                             void * stream) {
+    using namespace qa;
+    if ((W == nullptr) == (W_bf16 == nullptr)) return fail(QA_ERR_INVALID, "qa_gemv_fused: pass exactly one of W, W_bf16");
+    if (epilogue < kEpiStore || epilogue > kEpiSwiglu) return fail(QA_ERR_INVALID, "qa_gemv_fused: unknown epilogue");
+    return gemv_launch(epilogue, norm_w != nullptr, W, out_dim, in_dim, x, y, norm_w, eps, as_stream(stream), W_bf16);
+}
+
+extern "C" int qa_pack_bf16(const float * src, int64_t n, uint16_t * dst, uint32_t * inexact, void * stream) {
+    return qa::pack_bf16_launch(src, n, dst, inexact, qa::as_stream(stream));
 }
 
 extern "C" size_t qa_argmax_workspace_bytes(int32_t rows) {

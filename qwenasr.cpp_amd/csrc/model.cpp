@@ -9,6 +9,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -73,6 +74,22 @@ extern "C" int qa_model_synthetic(const qa_text_config * cfg, uint64_t seed, qa_
         return fail(QA_ERR_ALLOC, "qa_model_synthetic: out of host memory");
     }
     *out = m.release();
+    return QA_OK;
+}
+
+extern "C" int qa_model_round_bf16(qa_model * model) {
+    if (!model) return qa::fail(QA_ERR_INVALID, "qa_model_round_bf16: null model");
+    std::set<const std::vector<float> *> done;   // tied tensors share one buffer: round it once
+    for (auto & kv : model->tensors) {
+        if (!done.insert(kv.second.get()).second) continue;
+        for (float & v : *kv.second) {
+            uint32_t b;
+            std::memcpy(&b, &v, 4);
+            if ((b & 0x7f800000u) != 0x7f800000u) b += 0x7fffu + ((b >> 16) & 1u);   // nearest, ties to even
+            b &= 0xffff0000u;
+            std::memcpy(&v, &b, 4);
+        }
+    }
     return QA_OK;
 }
 

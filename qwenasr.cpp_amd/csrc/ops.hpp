@@ -7,8 +7,11 @@ namespace qa {
 
 enum { kEpiStoreOp = 0, kEpiAccumOp = 1, kEpiSwigluOp = 2 };
 
+// W16 (optional): the same weights as bf16 bits, read instead of W when given (bf16-exact weights)
 int gemv_launch(int epi, bool prenorm, const float * W, int32_t out_dim, int32_t in_dim, const float * x, float * y,
-                const float * norm_w, float eps, hipStream_t stream);
+                const float * norm_w, float eps, hipStream_t stream, const uint16_t * W16 = nullptr);
+// dst = high halves of src; *inexact |= 1 if any low half of src is non-zero
+int pack_bf16_launch(const float * src, int64_t n, uint16_t * dst, uint32_t * inexact, hipStream_t stream);
 // Y[rows][N] (+)= X[rows][K] W[N][K]^T for 1..64 rows (K a multiple of 32), f32 MFMA.
 size_t gemm_rows_workspace_bytes(int32_t N, int32_t K, int32_t rows);
 // Fusions of the <= 32-row kernel (gemm_rows_fusable):

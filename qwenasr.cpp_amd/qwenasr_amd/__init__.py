@@ -105,6 +105,8 @@ SIGNATURES = {
     "qa_causal_attn_f32": (C.c_int, vp, vp, vp, i32, i32, i32, f32, vp, vp),
     "qa_qk_prep": (C.c_int, vp, i32, i32, i32, vp, vp, i32, f32, f32, vp),
     "qa_gemv": (C.c_int, vp, i32, i32, vp, i32, vp, i32, vp),
+    "qa_gemv_fused": (C.c_int, vp, vp, i32, i32, vp, vp, i32, vp, f32, vp),
+    "qa_pack_bf16": (C.c_int, vp, i64, vp, vp, vp),
     "qa_rmsnorm_rows": (C.c_int, vp, vp, i32, i32, f32, vp, vp),
     "qa_swiglu_rows": (C.c_int, vp, i32, i32, vp, vp),
     "qa_add_inplace": (C.c_int, vp, vp, sz, vp),
@@ -118,6 +120,8 @@ SIGNATURES = {
     "qa_synth_fill_const": (None, fp, sz, f32),
     "qa_synth_fill_ids": (None, ip, sz, u64, C.c_char_p, i32, i32),
     "qa_model_synthetic": (C.c_int, C.POINTER(TextConfig), u64, C.POINTER(vp)),
+    "qa_model_round_bf16": (C.c_int, vp),
+    "qa_decoder_weights_bf16": (C.c_int, vp),
     "qa_model_free": (None, vp),
     "qa_model_tensor": (fp, vp, C.c_char_p, C.POINTER(i64)),
     "qa_model_config": (C.c_int, vp, C.POINTER(TextConfig)),
@@ -265,15 +269,21 @@ def synth_ids(n: int, seed: int, name: str, lo: int, hi: int) -> np.ndarray:
 
 
 class Model:
-    """Seeded synthetic Qwen3-ASR text model held in host memory (GGUF tensor names)."""
+    """Seeded synthetic Qwen3-ASR text model held in host memory (GGUF tensor names).
+
+    bf16=True rounds every tensor to bf16 (kept as f32): the values of a checkpoint converted from
+    the released bf16 weights (convert.py:386-387), for which the decoder streams bf16 copies."""
 
     def __init__(self, size: ModelSize, n_layers: int | None = None, seed: int = SEED_WEIGHTS,
-                 vocab: int | None = None):
+                 vocab: int | None = None, bf16: bool = False):
         self.size = size
         self.cfg = size.config(n_layers, vocab)
+        self.bf16 = bf16
         h = vp()
         check(lib.qa_model_synthetic(C.byref(self.cfg), seed, C.byref(h)))
         self.handle = h
+        if bf16:
+            check(lib.qa_model_round_bf16(h))
 
     def tensor(self, name: str) -> np.ndarray:
         n = i64()
@@ -367,6 +377,11 @@ class Decoder:
         v = i32()
         check(lib.qa_decoder_cur_len(self.handle, stream, C.byref(v)))
         return v.value
+
+    @property
+    def weights_bf16(self) -> bool:
+        """True when the batch-1 GEMVs read bf16 copies of bf16-exact weights (qa_decoder_weights_bf16)."""
+        return bool(lib.qa_decoder_weights_bf16(self.handle))
 
     def device_lens(self) -> np.ndarray:
         out = np.zeros(self.n_streams, dtype=np.int32)

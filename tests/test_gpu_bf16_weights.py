@@ -1,0 +1,150 @@
+"""bf16-exact weights on the GPU: the decoder's bf16 weight copies give the f32 results bit for bit.
+
+A checkpoint converted from the released bf16 weights (convert.py:386-387 widens each bf16 tensor
+with tensor.float()) holds f32 values with zero low halves.  The decoder then keeps bf16 copies of
+its projection and LM-head weights and the batch-1 GEMVs widen them back in registers.  These tests
+hold that path to bit-equality with the f32 GEMV on the same values (every epilogue, every input
+width), to a float64 restatement of the GEMV, and, end to end, to the f32-storage decoder and the
+oracle's greedy ids."""
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu(qa):
+    assert qa.device_count() > 0, "no HIP device: GPU tests need the MI355X"
+
+
+def bf16_round(a):
+    """Nearest bf16 value (ties to even) of each f32, as f32 (torch's own conversion)."""
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).to(torch.float32).numpy()
+
+
+def high_halves(a):
+    return (np.ascontiguousarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def gemv_f64(w, x, epilogue, norm_w, eps, y0):
+    x = x.astype(np.float64)
+    if norm_w is not None:
+        x32 = x.astype(np.float32)
+        scale = np.float32(1.0) / np.sqrt(np.float32(np.sum(x * x) / x.size) + np.float32(eps))
+        x = ((x32 * scale) * norm_w).astype(np.float64)
+    if epilogue == 2:
+        n = w.shape[0] // 2
+        g, u = w[:n].astype(np.float64) @ x, w[n:].astype(np.float64) @ x
+        return g / (1.0 + np.exp(-g)) * u
+    y = w.astype(np.float64) @ x
+    return y + y0 if epilogue == 1 else y
+
+
+def run_gemv(qa, w, x, epilogue, norm_w, y0, b16):
+    out_dim = w.shape[0] // 2 if epilogue == 2 else w.shape[0]
+    d_x = qa.DeviceArray.from_numpy(x)
+    d_y = qa.DeviceArray.from_numpy(y0.copy())
+    d_n = qa.DeviceArray.from_numpy(norm_w) if norm_w is not None else None
+    if b16:
+        d_w = qa.DeviceArray.from_numpy(high_halves(w))
+        args = (None, d_w.ptr)
+    else:
+        d_w = qa.DeviceArray.from_numpy(w)
+        args = (d_w.ptr, None)
+    qa.check(qa.lib.qa_gemv_fused(*args, out_dim, w.shape[1], d_x.ptr, d_y.ptr, epilogue,
+                                  d_n.ptr if d_n is not None else None, 1e-6, None))
+    qa.synchronize()
+    return d_y.numpy()
+
+
+@pytest.mark.parametrize("in_dim", [1024, 2048, 3072, 4096, 6144])
+@pytest.mark.parametrize("epilogue,prenorm", [(0, False), (0, True), (1, False), (2, True)])
+@pytest.mark.parametrize("out_dim", [1, 100, 4096])
+def test_gemv_bf16_copy_equals_f32_bit_for_bit(qa, in_dim, epilogue, prenorm, out_dim):
+    rng = np.random.default_rng(in_dim * 7 + out_dim + epilogue)
+    rows = 2 * out_dim if epilogue == 2 else out_dim
+    w = bf16_round(rng.standard_normal((rows, in_dim)) * 0.02)
+    assert not (w.view(np.uint32) & 0xffff).any()
+    x = rng.standard_normal(in_dim).astype(np.float32)
+    norm_w = (1.0 + 0.1 * rng.standard_normal(in_dim)).astype(np.float32) if prenorm else None
+    y0 = rng.standard_normal(out_dim).astype(np.float32)
+    y32 = run_gemv(qa, w, x, epilogue, norm_w, y0, False)
+    y16 = run_gemv(qa, w, x, epilogue, norm_w, y0, True)
+    np.testing.assert_array_equal(y16.view(np.uint32), y32.view(np.uint32))
+    np.testing.assert_allclose(y16, gemv_f64(w, x, epilogue, norm_w, 1e-6, y0), rtol=2e-5, atol=2e-5)
+
+
+def test_gemv_fused_rejects_ambiguous_weights(qa):
+    d = qa.DeviceArray((64,), np.float32)
+    for args in ((None, None), (d.ptr, d.ptr)):
+        with pytest.raises(qa.QaError) as e:
+            qa.check(qa.lib.qa_gemv_fused(*args, 4, 1024, d.ptr, d.ptr, 0, None, 1e-6, None))
+        assert e.value.code == qa.QA_ERR_INVALID
+    with pytest.raises(qa.QaError):
+        qa.check(qa.lib.qa_gemv_fused(d.ptr, None, 4, 1000, d.ptr, d.ptr, 0, None, 1e-6, None))
+
+
+@pytest.mark.parametrize("n", [1, 255, 4096, 1000003])
+def test_pack_bf16_flags_inexact_values(qa, n):
+    rng = np.random.default_rng(n)
+    a = bf16_round(rng.standard_normal(n))
+    flag = qa.DeviceArray((1,), np.uint32)
+    d_a = qa.DeviceArray.from_numpy(a)
+    d_b = qa.DeviceArray((n,), np.uint16)
+    qa.check(qa.lib.qa_pack_bf16(d_a.ptr, n, d_b.ptr, flag.ptr, None))
+    qa.synchronize()
+    assert int(flag.numpy()[0]) == 0
+    np.testing.assert_array_equal(d_b.numpy(), high_halves(a))
+    b = a.copy()
+    b.view(np.uint32)[n // 2] |= 1           # one value with a non-zero low half
+    d_a.upload(b)
+    qa.check(qa.lib.qa_pack_bf16(d_a.ptr, n, d_b.ptr, flag.ptr, None))
+    qa.synchronize()
+    assert int(flag.numpy()[0]) == 1
+
+
+def _decoder(qa, model, max_seq, f32_weights):
+    old = os.environ.pop("QA_WEIGHTS_F32", None)
+    try:
+        if f32_weights:
+            os.environ["QA_WEIGHTS_F32"] = "1"
+        return qa.Decoder(model, 1, max_seq, qa.QA_CACHE_F16)
+    finally:
+        os.environ.pop("QA_WEIGHTS_F32", None)
+        if old is not None:
+            os.environ["QA_WEIGHTS_F32"] = old
+
+
+def test_decoder_keeps_bf16_copies_only_for_exact_weights(qa):
+    exact = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=2, bf16=True)
+    plain = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=2)
+    with _decoder(qa, exact, 64, False) as d:
+        assert d.weights_bf16
+    with _decoder(qa, exact, 64, True) as d:
+        assert not d.weights_bf16
+    with _decoder(qa, plain, 64, False) as d:
+        assert not d.weights_bf16          # N(0, 0.02) draws are not bf16 values
+
+
+def test_bf16_weights_generate_equals_f32_weights_and_oracle(qa, orc, greedy):
+    """0.6B shapes, 3 layers, bf16-exact weights: the bf16-copy decoder and the f32 decoder produce
+    bit-identical logits and identical ids; both match the oracle's greedy ids."""
+    model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=3, bf16=True)
+    om = orc.OracleModel.from_product_model(model)
+    x = qa.prompt_input(model, 40, 9)
+    N = 24
+    ref = om.generate(x, N, qa.STOP_IDS, om.cache(49 + N, True))
+    outs, logits = [], []
+    for f32_weights in (False, True):
+        with _decoder(qa, model, 49 + N, f32_weights) as dec:
+            assert dec.weights_bf16 == (not f32_weights)
+            outs.append(dec.generate(x, N, margins=True))
+            logits.append(dec.forward(x, 0))
+    assert outs[0] == outs[1]
+    np.testing.assert_array_equal(logits[0].view(np.uint32), logits[1].view(np.uint32))
+    assert greedy.match(outs[0]["ids"], ref["ids"], ref["margins"], ref["runner_up"],
+                        "bf16-exact weights, 0.6B x 3 layers") is None

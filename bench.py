@@ -227,7 +227,7 @@ def kernel_only(which: str, reps: int):
         from qwenasr_amd import configs
 
         w = configs.CONFIGS[4]
-        model = qa.Model(w.size, n_layers=w.n_layers)
+        model = qa.Model(w.size, n_layers=w.n_layers, bf16=True)
         print(json.dumps(dict(kernel=which, **multistream_decode(qa, model, reps))), flush=True)
         return
     import ctypes as C
@@ -310,6 +310,7 @@ def multistream_decode(qa, model, steps: int):
     lens = configs.cfg4_lengths(w.streams)
     first = configs.cfg4_first_ids(w.streams).astype(np.int32)
     with qa.Decoder(model, w.streams, w.max_seq, w.cache_type) as dec:
+        streamed = "bf16 copies of bf16-exact weights" if dec.weights_bf16 else "f32 weights"
         for s_ in range(w.streams):
             dec.set_cur_len(s_, int(lens[s_]))
         ids = dec.decode_streams(first, 2)                  # warm
@@ -331,7 +332,7 @@ def multistream_decode(qa, model, steps: int):
     return {"streams": w.streams, "steps": steps, "ms_per_step": round(dt * 1e3 / steps, 3),
             "tok_s": round(w.streams * steps / dt, 1), "family_ms_per_step": fam,
             "workload": f"config 4: {w.streams} streams, contexts {int(lens.min())}..{int(lens.max())} + {steps + 2}, "
-                        f"lock-step greedy decode, f16 cache, f32 weights"}
+                        f"lock-step greedy decode, f16 cache, {streamed} streamed"}
 
 
 def main():

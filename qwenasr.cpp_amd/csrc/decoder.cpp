@@ -235,8 +235,8 @@ bool fused_rows(const qa_decoder * d, int32_t rows) {
 }
 
 int fused_gemm(qa_decoder * d, const float * W, int32_t N, int32_t K, const float * X, int32_t rows, float * Y,
-               bool accumulate, const GemmRowsFusion & f) {
-    return gemm_rows_launch(W, N, K, X, rows, Y, accumulate, d->gr_ws, d->gr_ws_bytes, d->stream, &f);
+               bool accumulate, const GemmRowsFusion & f, const uint16_t * W16) {
+    return gemm_rows_launch(W, N, K, X, rows, Y, accumulate, d->gr_ws, d->gr_ws_bytes, d->stream, &f, W16);
 }
 
 GemmRowsFusion norm_in(const qa_decoder * d, const float * norm_w) {
@@ -278,7 +278,7 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
             rc = gemv_launch(kEpiStoreOp, true, L.qkv, W3, H, d->x, d->qkv, L.attn_norm, c.rms_norm_eps, s,
                              L.qkv16);
         } else if (fused) {
-            rc = fused_gemm(d, L.qkv, W3, H, d->x, rows, d->qkv, false, norm_in(d, L.attn_norm));
+            rc = fused_gemm(d, L.qkv, W3, H, d->x, rows, d->qkv, false, norm_in(d, L.attn_norm), L.qkv16);
         } else {
             rc = rmsnorm_rows_launch(d->x, L.attn_norm, rows, H, c.rms_norm_eps, d->xn, s);
             if (rc == QA_OK) rc = sgemm(d, L.qkv, W3, H, d->xn, rows, d->qkv, 0.0f);
@@ -325,9 +325,9 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
     } else if (fused) {
         GemmRowsFusion gu = norm_in(d, L.ffn_norm);
         gu.swiglu = true;
-        rc = fused_gemm(d, L.o, H, QD, d->attn, rows, d->x, true, stats_out(d));
-        if (rc == QA_OK) rc = fused_gemm(d, L.gu, 2 * I, H, d->x, rows, d->act, false, gu);
-        if (rc == QA_OK) rc = fused_gemm(d, L.down, H, I, d->act, rows, d->x, true, stats_out(d));
+        rc = fused_gemm(d, L.o, H, QD, d->attn, rows, d->x, true, stats_out(d), L.o16);
+        if (rc == QA_OK) rc = fused_gemm(d, L.gu, 2 * I, H, d->x, rows, d->act, false, gu, L.gu16);
+        if (rc == QA_OK) rc = fused_gemm(d, L.down, H, I, d->act, rows, d->x, true, stats_out(d), L.down16);
     } else {
         rc = sgemm(d, L.o, H, QD, d->attn, rows, d->x, 1.0f);
         if (rc == QA_OK) rc = rmsnorm_rows_launch(d->x, L.ffn_norm, rows, H, c.rms_norm_eps, d->xn, s);
@@ -350,7 +350,8 @@ int logits_and_pick(qa_decoder * d, int32_t first, int32_t rows, bool pick, bool
             rc = gemv_launch(kEpiStoreOp, true, d->out_w, c.vocab, c.hidden, xr, d->logits, d->out_norm,
                              c.rms_norm_eps, d->stream, d->out_w16);
         } else if (fused && first == 0) {
-            rc = fused_gemm(d, d->out_w, c.vocab, c.hidden, xr, rows, d->logits, false, norm_in(d, d->out_norm));
+            rc = fused_gemm(d, d->out_w, c.vocab, c.hidden, xr, rows, d->logits, false, norm_in(d, d->out_norm),
+                            d->out_w16);
         } else {
             rc = rmsnorm_rows_launch(xr, d->out_norm, rows, c.hidden, c.rms_norm_eps, d->xn, d->stream);
             if (rc == QA_OK) rc = sgemm(d, d->out_w, c.vocab, c.hidden, d->xn, rows, d->logits, 0.0f);

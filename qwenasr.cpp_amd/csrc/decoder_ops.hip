@@ -220,13 +220,14 @@ int launch_gemv_nr(int nr, const GemvParams & p, hipStream_t stream) {
     }
 }
 
-// default rows per wave: about 16 KB (32 KB for gate|up, which reads two rows per output) of weights
-// per wave, i.e. twice the f32 row count for bf16 rows
+// default rows per wave: 16-32 KB of f32 weights per wave; bf16 rows at least 2 per wave (the 1.7B
+// decode step's bf16 GEMVs, traced at 1, 2 and 4 rows: 2 is fastest for every shape, by up to 20%
+// over 4 for o-proj, 10% over 1 for q|k|v)
 template <int EPI, bool PRENORM, bool B16>
 int launch_gemv_in(const GemvParams & p, hipStream_t stream) {
     const int forced = gemv_rows_override();
     const bool sw = EPI == kEpiSwiglu;
-    auto nr = [&](int f32_rows) { return forced ? forced : B16 ? std::min(4, 2 * f32_rows) : f32_rows; };
+    auto nr = [&](int f32_rows) { return forced ? forced : B16 ? std::max(2, f32_rows) : f32_rows; };
     switch (p.in_dim) {
         case 1024: return launch_gemv_nr<4, EPI, PRENORM, B16>(nr(sw ? 2 : 4), p, stream);
         case 2048: return launch_gemv_nr<8, EPI, PRENORM, B16>(nr(2), p, stream);
@@ -292,6 +293,7 @@ struct GemmRowsParams {
     int32_t N, K, rows, ks, slice, accumulate;
     uint32_t x_magic;         // ceil(2^32 / (slice / 4)): X staging index / vectors per token row
     uint32_t x_magic_last;    // the same for the last slice (K - (ks - 1) slice)
+    const uint16_t * W16;     // gemm_rows32_kernel: the weights as bf16 bits, read instead of W when set
     // fusions of gemm_rows32_kernel (null / 0: none)
     const float * norm_w;     // X is RMSNorm(X) * norm_w, with the row sums of squares in stats_in
     const double * stats_in;  // [n_stats_in][32]: partial sums of squares of each X row (summed in order)
@@ -495,11 +497,13 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
 // instruction into registers, written to a per-wave LDS block and read back in operand layout (row
 // stride 68 floats: the 16-byte reads of 16 consecutive rows fall on distinct banks).  P blocks of
 // loads are in flight per wave while one block is computed.
+// B16: W16 holds the weights as bf16 bits (bf16-exact weights); each lane loads the same 4 elements
+// as 8 bytes and widens them before the LDS write, so the MFMA operands are the f32 kernel's.
 constexpr int kG32Rows = 32;         // weight rows per workgroup (one MFMA block)
 constexpr int kG32Blk = 64;          // k per block
 constexpr int kG32Ls = kG32Blk + 4;  // LDS row stride (floats)
 
-template <int P>
+template <int P, bool B16>
 __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
 #pragma clang fp contract(off)
     __shared__ __attribute__((aligned(16))) float lw[4][kG32Rows * kG32Ls];
@@ -534,6 +538,7 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
     // gate rows and the 16 matching up rows (W = [gate rows; up rows], N = 2 I).
     const int lr = lane >> 4, lc = 4 * (lane & 15);
     const float * wbase = p.W + k_begin + kG32Blk * wave + lc;
+    const uint16_t * wbase16 = p.W16 + k_begin + kG32Blk * wave + lc;
     const float * xbase = p.X + k_begin + kG32Blk * wave + lc;
     const float * nbase = prenorm ? p.norm_w + k_begin + kG32Blk * wave + lc : nullptr;
     int64_t wrow[8];
@@ -546,13 +551,17 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
         xrow[i] = min(line, p.rows - 1) * p.K;
     }
     v4f wr[P][8], xr[P][8], nw[P];
+    u2 wb[P][8];
     auto load = [&](int u, int b) {
         const int o = min(b, last) * 4 * kG32Blk;
 #pragma unroll
         for (int i = 0; i < 8; ++i) xr[u][i] = *reinterpret_cast<const v4f *>(xbase + xrow[i] + o);
         if (prenorm) nw[u] = *reinterpret_cast<const v4f *>(nbase + o);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) wr[u][i] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(wbase + wrow[i] + o));
+        for (int i = 0; i < 8; ++i) {
+            if constexpr (B16) wb[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u2 *>(wbase16 + wrow[i] + o));
+            else wr[u][i] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(wbase + wrow[i] + o));
+        }
     };
     if (my > 0) {
 #pragma unroll
@@ -592,7 +601,8 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) xv[e] = xv[e] * sc[i] * nw[u][e];
             }
-            *reinterpret_cast<v4f *>(myw + (4 * i + lr) * kG32Ls + lc) = wr[u][i];
+            if constexpr (B16) *reinterpret_cast<v4f *>(myw + (4 * i + lr) * kG32Ls + lc) = widen_bf16x4(wb[u][i]);
+            else *reinterpret_cast<v4f *>(myw + (4 * i + lr) * kG32Ls + lc) = wr[u][i];
             *reinterpret_cast<v4f *>(myx + (4 * i + lr) * kG32Ls + lc) = xv;
         }
         // the block is read back by other lanes of this wave: LDS operations of a wave complete in order
@@ -950,8 +960,9 @@ bool gemm_rows_fusable(int32_t N, int32_t K, int32_t rows) {
 }
 
 int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int32_t rows, float * Y, bool accumulate,
-                     void * workspace, size_t workspace_bytes, hipStream_t stream, const GemmRowsFusion * fusion) {
-    if (!W || !X || !Y || N <= 0 || N > kGrMaxTiles * kGrTile || K <= 0 || K % 32 != 0 || rows < 1 ||
+                     void * workspace, size_t workspace_bytes, hipStream_t stream, const GemmRowsFusion * fusion,
+                     const uint16_t * W16) {
+    if ((!W && !W16) || !X || !Y || N <= 0 || N > kGrMaxTiles * kGrTile || K <= 0 || K % 32 != 0 || rows < 1 ||
         rows > kGrMaxRows) {
         return fail(QA_ERR_INVALID, "gemm_rows: invalid shape");
     }
@@ -966,6 +977,7 @@ int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int
         }
     }
     const GemmRowsPlan pl = gemm_rows_plan(N, K, rows, fused && fusion->swiglu);
+    if (!W && !pl.rows32) return fail(QA_ERR_INVALID, "gemm_rows: bf16 weights need rows <= 32 and K % 64 == 0");
     const size_t need = gemm_rows_workspace_bytes(N, K, rows);
     if (!workspace || workspace_bytes < need) return fail(QA_ERR_INVALID, "gemm_rows: workspace too small");
     GemmRowsParams p{};
@@ -994,8 +1006,14 @@ int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int
     }
     if (pl.rows32) {
         const dim3 grid(static_cast<unsigned>(pl.tiles * pl.ks));
-        if (pl.depth == 2) hipLaunchKernelGGL((gemm_rows32_kernel<2>), grid, dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((gemm_rows32_kernel<1>), grid, dim3(256), 0, stream, p);
+        p.W16 = W16;
+        if (W16) {
+            if (pl.depth == 2) hipLaunchKernelGGL((gemm_rows32_kernel<2, true>), grid, dim3(256), 0, stream, p);
+            else hipLaunchKernelGGL((gemm_rows32_kernel<1, true>), grid, dim3(256), 0, stream, p);
+        } else {
+            if (pl.depth == 2) hipLaunchKernelGGL((gemm_rows32_kernel<2, false>), grid, dim3(256), 0, stream, p);
+            else hipLaunchKernelGGL((gemm_rows32_kernel<1, false>), grid, dim3(256), 0, stream, p);
+        }
         QA_LAUNCH_CHECK("gemm_rows32_kernel");
         return QA_OK;
     }
@@ -1199,4 +1217,20 @@ extern "C" int qa_gemm_rows_fused(const float * W, int32_t out_dim, int32_t in_d
     f.swiglu = swiglu != 0;
     return qa::gemm_rows_launch(W, out_dim, in_dim, x, rows, y, accumulate != 0, workspace, workspace_bytes,
                                 qa::as_stream(stream), &f);
+}
+
+extern "C" int qa_gemm_rows_fused_bf16(const uint16_t * W_bf16, int32_t out_dim, int32_t in_dim, const float * x,
+                                       int32_t rows, float * y, int32_t accumulate, const float * norm_w,
+                                       const double * stats_in, int32_t n_stats_in, float eps, double * stats_out,
+                                       int32_t swiglu, void * workspace, size_t workspace_bytes, void * stream) {
+    if (!W_bf16) return qa::fail(QA_ERR_INVALID, "qa_gemm_rows_fused_bf16: null weights");
+    qa::GemmRowsFusion f;
+    f.norm_w = norm_w;
+    f.stats_in = stats_in;
+    f.n_stats_in = n_stats_in;
+    f.eps = eps;
+    f.stats_out = stats_out;
+    f.swiglu = swiglu != 0;
+    return qa::gemm_rows_launch(nullptr, out_dim, in_dim, x, rows, y, accumulate != 0, workspace, workspace_bytes,
+                                qa::as_stream(stream), &f, W_bf16);
 }

@@ -28,9 +28,11 @@ struct GemmRowsFusion {
     bool swiglu = false;
 };
 bool gemm_rows_fusable(int32_t N, int32_t K, int32_t rows);
+// W16 (optional): the same weights as bf16 bits (bf16-exact weights), read instead of W by the <= 32-row
+// kernel with the same results; the longer-row kernel reads W
 int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int32_t rows, float * Y, bool accumulate,
                      void * workspace, size_t workspace_bytes, hipStream_t stream,
-                     const GemmRowsFusion * fusion = nullptr);
+                     const GemmRowsFusion * fusion = nullptr, const uint16_t * W16 = nullptr);
 size_t argmax_workspace_bytes(int32_t rows);
 int argmax_launch(const float * logits, int32_t rows, int32_t vocab, int32_t * ids, void * workspace,
                   hipStream_t stream);

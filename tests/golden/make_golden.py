@@ -1,11 +1,14 @@
 """Writes the golden fixtures of configs 0-4 from the CPU oracle (run once, on any x86-64 host).
 
-    python tests/golden/make_golden.py [--configs 0,1,2,3,4] [--cfg4-streams 4]
+    python tests/golden/make_golden.py [--configs 0,1,2,3,4] [--cfg4-streams 4] [--bf16]
 
 Inputs come from the product's seeded generator (the same bits the GPU path receives); outputs come
 from oracle/qa_oracle.c.  Each fixture records a checksum of its inputs so a drift of the generator
 is caught before any comparison.  The reference's own goldens (real-weight JFK ids, README.md:301-303)
 need a checkpoint and audio that do not exist here, so these fixtures are the oracle's.
+
+--bf16 rounds the synthetic weights to bf16 values first (what a checkpoint converted from the released
+bf16 weights holds, convert.py:386-387) and writes cfg{N}_bf16.json: the bench's own workload.
 """
 from __future__ import annotations
 
@@ -55,16 +58,17 @@ def cfg0():
                             v_row=cache.v[0, :, 156].tolist()))
 
 
-def greedy(index: int):
+def greedy(index: int, bf16: bool = False):
     w = configs.CONFIGS[index]
     t0 = time.time()
-    model = qa.Model(w.size, n_layers=w.n_layers)
+    model = qa.Model(w.size, n_layers=w.n_layers, bf16=bf16)
     om = orc.OracleModel.from_product_model(model)
     x = qa.prompt_input(model, w.audio_tokens, w.prompt_tokens)
     cache = om.cache(w.max_seq, f16=w.cache_type == qa.QA_CACHE_F16)
     out = om.generate(x, w.new_tokens, qa.STOP_IDS, cache)
     assert out["rc"] == 0, out["rc"]
-    write(f"cfg{index}.json", dict(config=index, input_digest=digest(x, model.tensor("text.blk.0.attn_q.weight")),
+    write(f"cfg{index}{'_bf16' if bf16 else ''}.json",
+          dict(config=index, input_digest=digest(x, model.tensor("text.blk.0.attn_q.weight")), bf16_weights=bf16,
                                    prompt_tokens=w.prompt, requested=w.new_tokens, ids=out["ids"],
                                    stopped=out["stopped"], total_tokens=out["total_tokens"], cur_len=out["cur_len"],
                                    margins=out["margins"], runner_up=out["runner_up"],
@@ -99,6 +103,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--configs", default="0,1,2,3,4")
     ap.add_argument("--cfg4-streams", type=int, default=4)
+    ap.add_argument("--bf16", action="store_true", help="bf16-exact weights (configs 1-3)")
     args = ap.parse_args()
     for c in [int(v) for v in args.configs.split(",")]:
         t = time.time()
@@ -106,6 +111,8 @@ def main():
             cfg0()
         elif c == 4:
             cfg4(args.cfg4_streams)
+        elif args.bf16:
+            greedy(c, bf16=True)
         else:
             greedy(c)
         print(f"config {c}: {time.time() - t:.1f}s", flush=True)

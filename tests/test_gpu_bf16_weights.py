@@ -148,3 +148,102 @@ def test_bf16_weights_generate_equals_f32_weights_and_oracle(qa, orc, greedy):
     np.testing.assert_array_equal(logits[0].view(np.uint32), logits[1].view(np.uint32))
     assert greedy.match(outs[0]["ids"], ref["ids"], ref["margins"], ref["runner_up"],
                         "bf16-exact weights, 0.6B x 3 layers") is None
+
+
+def _row_stats(x, dim):
+    n = (dim + 31) // 32
+    st = np.zeros((n, 32), np.float64)
+    for k in range(n):
+        st[k, :x.shape[0]] = np.sum(x[:, 32 * k:32 * k + 32].astype(np.float64) ** 2, axis=1)
+    return st
+
+
+@pytest.mark.parametrize("out_dim,in_dim,rows", [(4096, 2048, 32), (2048, 2048, 7), (12288, 2048, 32),
+                                                  (2048, 6144, 32), (1056, 1024, 5), (151936 // 8, 2048, 32)])
+def test_gemm_rows_bf16_copy_equals_f32_bit_for_bit(qa, out_dim, in_dim, rows):
+    """The multi-stream step's 32-row GEMM with bf16 weights equals it with the f32 weights, bit for
+    bit, with each fusion: RMSNorm input + accumulate + statistics out, and the SwiGLU epilogue."""
+    rng = np.random.default_rng(out_dim + in_dim + rows)
+    w = bf16_round(rng.standard_normal((out_dim, in_dim)) * 0.02)
+    x = rng.standard_normal((rows, in_dim)).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(in_dim)).astype(np.float32)
+    y0 = rng.standard_normal((rows, out_dim)).astype(np.float32)
+    st_in = _row_stats(x, in_dim)
+    d_x = qa.DeviceArray.from_numpy(x)
+    d_nw = qa.DeviceArray.from_numpy(nw) if st_in.shape[0] <= 128 else None
+    d_st = qa.DeviceArray.from_numpy(st_in) if d_nw is not None else None
+    wsb = qa.lib.qa_gemm_rows_workspace_bytes(out_dim, in_dim, rows)
+    ws = qa.DeviceArray((wsb,), np.uint8)
+    d_w32 = qa.DeviceArray.from_numpy(w)
+    d_w16 = qa.DeviceArray.from_numpy(high_halves(w))
+    ptr = lambda a: a.ptr if a is not None else None
+    print(f"gemm_rows bf16 {out_dim}x{in_dim} rows={rows}", flush=True)
+    outs = []
+    for fn, d_w in ((qa.lib.qa_gemm_rows_fused, d_w32), (qa.lib.qa_gemm_rows_fused_bf16, d_w16)):
+        d_y = qa.DeviceArray.from_numpy(y0)
+        d_so = qa.DeviceArray(((out_dim + 31) // 32, 32), np.float64)
+        qa.check(fn(d_w.ptr, out_dim, in_dim, d_x.ptr, rows, d_y.ptr, 1, ptr(d_nw), ptr(d_st), st_in.shape[0],
+                    1e-6, d_so.ptr, 0, ws.ptr, wsb, None))
+        res = [d_y.numpy(), d_so.numpy()]
+        if out_dim % 32 == 0:
+            d_a = qa.DeviceArray((rows, out_dim // 2), np.float32)
+            qa.check(fn(d_w.ptr, out_dim, in_dim, d_x.ptr, rows, d_a.ptr, 0, ptr(d_nw), ptr(d_st), st_in.shape[0],
+                        1e-6, None, 1, ws.ptr, wsb, None))
+            res.append(d_a.numpy())
+        qa.synchronize()
+        outs.append(res)
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a.view(np.uint8), b.view(np.uint8))
+    if d_nw is None:                           # plain input: also against float64
+        np.testing.assert_allclose(outs[1][0], y0 + x.astype(np.float64) @ w.T.astype(np.float64), rtol=1e-4,
+                                   atol=2e-4)
+
+
+def test_gemm_rows_bf16_rejects_unsupported_shapes(qa):
+    d = qa.DeviceArray((1 << 16,), np.float32)
+    ws = qa.DeviceArray((1 << 20,), np.uint8)
+    with pytest.raises(qa.QaError) as e:       # 33 rows take the longer-row kernel, which reads f32 weights
+        qa.check(qa.lib.qa_gemm_rows_fused_bf16(d.ptr, 64, 64, d.ptr, 33, d.ptr, 0, None, None, 0, 1e-6, None, 0,
+                                                ws.ptr, 1 << 20, None))
+    assert e.value.code == qa.QA_ERR_INVALID
+    with pytest.raises(qa.QaError):
+        qa.check(qa.lib.qa_gemm_rows_fused_bf16(None, 64, 64, d.ptr, 4, d.ptr, 0, None, None, 0, 1e-6, None, 0,
+                                                ws.ptr, 1 << 20, None))
+
+
+@pytest.mark.parametrize("n_streams", [5, 32])
+def test_bf16_weights_multistream_equals_f32_weights_and_oracle(qa, orc, greedy, n_streams):
+    """The multi-stream decode step with bf16-exact weights: the bf16-copy decoder and the f32 decoder
+    give identical ids, and both match the oracle decoding each stream alone (0.6B, 2 layers)."""
+    from qwenasr_amd import configs
+
+    model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=2, bf16=True)
+    om = orc.OracleModel.from_product_model(model)
+    rng = np.random.default_rng(100 + n_streams)
+    lens = rng.integers(20, 180, n_streams)
+    first = rng.integers(0, model.cfg.vocab, n_streams).astype(np.int32)
+    steps, cap = 4, 200
+    kv = [configs.cfg4_stream_kv(2000 + s, int(lens[s]), n_layers=2) for s in range(n_streams)]
+    got = []
+    for f32_weights in (False, True):
+        old = os.environ.pop("QA_WEIGHTS_F32", None)
+        if f32_weights:
+            os.environ["QA_WEIGHTS_F32"] = "1"
+        try:
+            dec = qa.Decoder(model, n_streams, cap, qa.QA_CACHE_F16)
+        finally:
+            os.environ.pop("QA_WEIGHTS_F32", None)
+            if old is not None:
+                os.environ["QA_WEIGHTS_F32"] = old
+        with dec:
+            assert dec.weights_bf16 == (not f32_weights)
+            for s in range(n_streams):
+                dec.fill_cache(s, kv[s][0], kv[s][1], int(lens[s]))
+            got.append(dec.decode_streams(first, steps))
+    np.testing.assert_array_equal(got[0], got[1])
+    for s in range(n_streams):
+        cache = om.cache(cap, True)
+        cache.fill(kv[s][0], kv[s][1], int(lens[s]))
+        ids, margins, runner = om.decode_steps(cache, int(first[s]), steps)
+        greedy.match(got[0][:, s].tolist(), list(ids), list(margins), list(runner),
+                     f"bf16-exact weights, {n_streams}-stream step, stream {s}")

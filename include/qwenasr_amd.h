@@ -224,8 +224,9 @@ int qa_gemm_rows_fused(const float * W, int32_t out_dim, int32_t in_dim, const f
                        int32_t n_stats_in, float eps, double * stats_out, int32_t swiglu,
                        void * workspace, size_t workspace_bytes, void * stream);
 /* qa_gemm_rows_fused with the weights given as bf16 bits (the high halves of bf16-exact f32 weights,  *
- * see qa_pack_bf16): the same result bit for bit as qa_gemm_rows_fused on the f32 weights, reading    *
- * half the bytes.  rows <= 32 and in_dim % 64 == 0.                                                   */
+ * see qa_pack_bf16), reading half the bytes.  The products run on bf16 MFMAs with each x split into    *
+ * three bf16 parts (x = hi + mid + lo exactly): every product is exact and the sums are f32, as in     *
+ * qa_gemm_rows_fused, in another order.  rows <= 32 and in_dim % 64 == 0.                             */
 int qa_gemm_rows_fused_bf16(const uint16_t * W_bf16, int32_t out_dim, int32_t in_dim, const float * x, int32_t rows,
                             float * y, int32_t accumulate, const float * norm_w, const double * stats_in,
                             int32_t n_stats_in, float eps, double * stats_out, int32_t swiglu,

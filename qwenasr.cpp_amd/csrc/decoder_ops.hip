@@ -497,11 +497,41 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
 // instruction into registers, written to a per-wave LDS block and read back in operand layout (row
 // stride 68 floats: the 16-byte reads of 16 consecutive rows fall on distinct banks).  P blocks of
 // loads are in flight per wave while one block is computed.
-// B16: W16 holds the weights as bf16 bits (bf16-exact weights); each lane loads the same 4 elements
-// as 8 bytes and widens them before the LDS write, so the MFMA operands are the f32 kernel's.
+// B16: W16 holds the weights as bf16 bits (bf16-exact weights).  W is loaded 8 rows x 128 B per
+// instruction and kept in LDS as bf16; the products run on v_mfma_f32_32x32x16_bf16 with each x split
+// into three bf16 parts by truncation, x = hi + mid + lo exactly (hi takes the top 8 significant bits,
+// mid the next 8, lo the last 8), so every weight x part product is exact in f32 and the MFMA sums them
+// in f32: f32 products and f32 sums, as the f32 path, in another order (5x fewer MFMA cycles: 3 bf16
+// MFMAs per 16 k against 8 f32 ones of 4x the cycles).  hi products go to one accumulator, mid and lo
+// products to the other.
 constexpr int kG32Rows = 32;         // weight rows per workgroup (one MFMA block)
 constexpr int kG32Blk = 64;          // k per block
 constexpr int kG32Ls = kG32Blk + 4;  // LDS row stride (floats)
+constexpr int kG32LsB = kG32Blk + 8; // LDS row stride of bf16 weight rows (elements: 144 B, 16 B aligned)
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+
+// the hi, mid, lo bf16 parts (x = hi + mid + lo exactly) of 8 floats, packed two per dword
+__device__ inline void split_bf16x3(const v4f a, const v4f b, u4v & hi, u4v & mid, u4v & lo) {
+    float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    uint32_t h[8], m[8], l[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t u = __float_as_uint(x[e]);
+        h[e] = u & 0xffff0000u;
+        const float r1 = x[e] - __uint_as_float(h[e]);
+        m[e] = __float_as_uint(r1) & 0xffff0000u;
+        const float r2 = r1 - __uint_as_float(m[e]);
+        l[e] = __float_as_uint(r2) & 0xffff0000u;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        hi[j] = (h[2 * j] >> 16) | h[2 * j + 1];
+        mid[j] = (m[2 * j] >> 16) | m[2 * j + 1];
+        lo[j] = (l[2 * j] >> 16) | l[2 * j + 1];
+    }
+}
 
 template <int P, bool B16>
 __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
@@ -538,29 +568,36 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
     // gate rows and the 16 matching up rows (W = [gate rows; up rows], N = 2 I).
     const int lr = lane >> 4, lc = 4 * (lane & 15);
     const float * wbase = p.W + k_begin + kG32Blk * wave + lc;
-    const uint16_t * wbase16 = p.W16 + k_begin + kG32Blk * wave + lc;
+    // bf16 rows: lane loads 8 elements, row 8 i + lane / 8 (i = 0..3), k 8 (lane % 8) .. + 7
+    const int lr16 = lane >> 3, lc16 = 8 * (lane & 7);
+    const uint16_t * wbase16 = p.W16 + k_begin + kG32Blk * wave + lc16;
     const float * xbase = p.X + k_begin + kG32Blk * wave + lc;
     const float * nbase = prenorm ? p.norm_w + k_begin + kG32Blk * wave + lc : nullptr;
+    auto weight_row = [&](int line) {
+        const int wr_row = p.swiglu ? (line < 16 ? 16 * tile + line : (p.N >> 1) + 16 * tile + line - 16) : row0 + line;
+        return static_cast<int64_t>(min(wr_row, p.N - 1)) * p.K;
+    };
     int64_t wrow[8];
     int xrow[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int line = 4 * i + lr;
-        const int wr_row = p.swiglu ? (line < 16 ? 16 * tile + line : (p.N >> 1) + 16 * tile + line - 16) : row0 + line;
-        wrow[i] = static_cast<int64_t>(min(wr_row, p.N - 1)) * p.K;
+        wrow[i] = B16 ? weight_row(8 * (i & 3) + lr16) : weight_row(line);
         xrow[i] = min(line, p.rows - 1) * p.K;
     }
     v4f wr[P][8], xr[P][8], nw[P];
-    u2 wb[P][8];
+    u4v wb[P][4];
     auto load = [&](int u, int b) {
         const int o = min(b, last) * 4 * kG32Blk;
 #pragma unroll
         for (int i = 0; i < 8; ++i) xr[u][i] = *reinterpret_cast<const v4f *>(xbase + xrow[i] + o);
         if (prenorm) nw[u] = *reinterpret_cast<const v4f *>(nbase + o);
+        if constexpr (B16) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            if constexpr (B16) wb[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u2 *>(wbase16 + wrow[i] + o));
-            else wr[u][i] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(wbase + wrow[i] + o));
+            for (int i = 0; i < 4; ++i) wb[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(wbase16 + wrow[i] + o));
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) wr[u][i] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(wbase + wrow[i] + o));
         }
     };
     if (my > 0) {
@@ -593,6 +630,7 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
     float * myx = lx[wave];
     const int r = lane & 31, h = lane >> 5;
     v16f acc0 = {}, acc1 = {};
+    uint16_t * myw16 = reinterpret_cast<uint16_t *>(myw);
     auto compute = [&](int u) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -601,12 +639,32 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) xv[e] = xv[e] * sc[i] * nw[u][e];
             }
-            if constexpr (B16) *reinterpret_cast<v4f *>(myw + (4 * i + lr) * kG32Ls + lc) = widen_bf16x4(wb[u][i]);
-            else *reinterpret_cast<v4f *>(myw + (4 * i + lr) * kG32Ls + lc) = wr[u][i];
+            if constexpr (!B16) *reinterpret_cast<v4f *>(myw + (4 * i + lr) * kG32Ls + lc) = wr[u][i];
             *reinterpret_cast<v4f *>(myx + (4 * i + lr) * kG32Ls + lc) = xv;
+        }
+        if constexpr (B16) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) *reinterpret_cast<u4v *>(myw16 + (8 * i + lr16) * kG32LsB + lc16) = wb[u][i];
         }
         // the block is read back by other lanes of this wave: LDS operations of a wave complete in order
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if constexpr (B16) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                // MFMA step s: k 16 s + 8 h + 0..7 for lane half h (A: weight row r, B: token r)
+                const u4v a = *reinterpret_cast<const u4v *>(myw16 + r * kG32LsB + 16 * s + 8 * h);
+                const v4f x0 = *reinterpret_cast<const v4f *>(myx + r * kG32Ls + 16 * s + 8 * h);
+                const v4f x1 = *reinterpret_cast<const v4f *>(myx + r * kG32Ls + 16 * s + 8 * h + 4);
+                u4v bh, bm, bl;
+                split_bf16x3(x0, x1, bh, bm, bl);
+                const bf16x8 av = __builtin_bit_cast(bf16x8, a);
+                acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bh), acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bm), acc1, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bl), acc1, 0, 0, 0);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            return;
+        }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             // MFMA step s: k 16 s + 4 h + j (acc0) and 16 s + 8 + 4 h + j (acc1), j = 0..3 -- the same
@@ -757,8 +815,17 @@ struct GemmRowsPlan {
     int depth;       // blocks in flight per wave (gemm_rows32_kernel)
 };
 
+// tuning overrides of the <= 32-row plan: QA_GR32_WGS (workgroup target, default 256) and QA_GR32_DEPTH
+// (blocks in flight per wave, 1 or 2)
+int env_int(const char * name, int fallback) {
+    const char * e = std::getenv(name);
+    return e ? std::atoi(e) : fallback;
+}
+
 GemmRowsPlan gemm_rows_plan(int32_t N, int32_t K, int32_t rows, bool one_slice = false) {
     GemmRowsPlan pl{};
+    static const int target_wgs = std::max(64, env_int("QA_GR32_WGS", 256));
+    static const int forced_depth = env_int("QA_GR32_DEPTH", 0);
     if (rows <= kG32Rows && K % kG32Blk == 0) {
         // ~256 workgroups at least (one per CU); a K slice keeps >= 4 blocks (one per wave) and at most
         // 8 slices are merged.  Measured at 32 rows (1.7B shapes): q|k|v 2 slices, o and down 4, gate|up
@@ -766,11 +833,11 @@ GemmRowsPlan gemm_rows_plan(int32_t N, int32_t K, int32_t rows, bool one_slice =
         // register file then holds 2 waves per SIMD either way), one when there are more workgroups.
         pl.rows32 = true;
         pl.tiles = (N + kG32Rows - 1) / kG32Rows;
-        int ks = std::max(1, std::min({(256 + pl.tiles / 2) / pl.tiles, 8, K / (4 * kG32Blk)}));
+        int ks = std::max(1, std::min({(target_wgs + pl.tiles / 2) / pl.tiles, 8, K / (4 * kG32Blk)}));
         if (pl.tiles > kGrMaxTiles || one_slice) ks = 1;           // counters exist for kGrMaxTiles tiles
         pl.slice = ((K + ks - 1) / ks + kG32Blk - 1) / kG32Blk * kG32Blk;
         pl.ks = (K + pl.slice - 1) / pl.slice;
-        pl.depth = pl.tiles * pl.ks <= 256 ? 2 : 1;
+        pl.depth = forced_depth == 1 || forced_depth == 2 ? forced_depth : pl.tiles * pl.ks <= 256 ? 2 : 1;
         return pl;
     }
     pl.tiles = (N + kGrTile - 1) / kGrTile;

@@ -160,43 +160,53 @@ def _row_stats(x, dim):
 
 @pytest.mark.parametrize("out_dim,in_dim,rows", [(4096, 2048, 32), (2048, 2048, 7), (12288, 2048, 32),
                                                   (2048, 6144, 32), (1056, 1024, 5), (151936 // 8, 2048, 32)])
-def test_gemm_rows_bf16_copy_equals_f32_bit_for_bit(qa, out_dim, in_dim, rows):
-    """The multi-stream step's 32-row GEMM with bf16 weights equals it with the f32 weights, bit for
-    bit, with each fusion: RMSNorm input + accumulate + statistics out, and the SwiGLU epilogue."""
+def test_gemm_rows_bf16_matches_float64(qa, out_dim, in_dim, rows):
+    """The multi-stream step's 32-row GEMM on bf16 weights (bf16 MFMAs over x split into three bf16
+    parts: exact products, f32 sums) against float64 of the same f32 inputs, with each fusion: RMSNorm
+    input + accumulate + statistics out, and the SwiGLU epilogue.  The bar is about ten times the f32
+    accumulation error of these sums; the f32-weight kernel meets the same bar on the same inputs."""
     rng = np.random.default_rng(out_dim + in_dim + rows)
+    eps = np.float32(1e-6)
     w = bf16_round(rng.standard_normal((out_dim, in_dim)) * 0.02)
     x = rng.standard_normal((rows, in_dim)).astype(np.float32)
     nw = (1.0 + 0.1 * rng.standard_normal(in_dim)).astype(np.float32)
     y0 = rng.standard_normal((rows, out_dim)).astype(np.float32)
     st_in = _row_stats(x, in_dim)
     d_x = qa.DeviceArray.from_numpy(x)
-    d_nw = qa.DeviceArray.from_numpy(nw) if st_in.shape[0] <= 128 else None
-    d_st = qa.DeviceArray.from_numpy(st_in) if d_nw is not None else None
+    norm = st_in.shape[0] <= 128
+    d_nw = qa.DeviceArray.from_numpy(nw) if norm else None
+    d_st = qa.DeviceArray.from_numpy(st_in) if norm else None
+    # the normalised input as both kernels form it: scale = 1 / sqrtf(float(ss / K) + eps), (x * scale) * w
+    if norm:
+        ss = np.sum(x.astype(np.float64) ** 2, axis=1)
+        scale = (np.float32(1.0) / np.sqrt((ss / in_dim).astype(np.float32) + eps)).astype(np.float32)
+        xn = ((x * scale[:, None]).astype(np.float32) * nw[None, :]).astype(np.float32)
+    else:
+        xn = x
+    ref = xn.astype(np.float64) @ w.T.astype(np.float64)
     wsb = qa.lib.qa_gemm_rows_workspace_bytes(out_dim, in_dim, rows)
     ws = qa.DeviceArray((wsb,), np.uint8)
     d_w32 = qa.DeviceArray.from_numpy(w)
     d_w16 = qa.DeviceArray.from_numpy(high_halves(w))
     ptr = lambda a: a.ptr if a is not None else None
     print(f"gemm_rows bf16 {out_dim}x{in_dim} rows={rows}", flush=True)
-    outs = []
     for fn, d_w in ((qa.lib.qa_gemm_rows_fused, d_w32), (qa.lib.qa_gemm_rows_fused_bf16, d_w16)):
         d_y = qa.DeviceArray.from_numpy(y0)
         d_so = qa.DeviceArray(((out_dim + 31) // 32, 32), np.float64)
         qa.check(fn(d_w.ptr, out_dim, in_dim, d_x.ptr, rows, d_y.ptr, 1, ptr(d_nw), ptr(d_st), st_in.shape[0],
-                    1e-6, d_so.ptr, 0, ws.ptr, wsb, None))
-        res = [d_y.numpy(), d_so.numpy()]
-        if out_dim % 32 == 0:
-            d_a = qa.DeviceArray((rows, out_dim // 2), np.float32)
-            qa.check(fn(d_w.ptr, out_dim, in_dim, d_x.ptr, rows, d_a.ptr, 0, ptr(d_nw), ptr(d_st), st_in.shape[0],
-                        1e-6, None, 1, ws.ptr, wsb, None))
-            res.append(d_a.numpy())
+                    eps, d_so.ptr, 0, ws.ptr, wsb, None))
         qa.synchronize()
-        outs.append(res)
-    for a, b in zip(*outs):
-        np.testing.assert_array_equal(a.view(np.uint8), b.view(np.uint8))
-    if d_nw is None:                           # plain input: also against float64
-        np.testing.assert_allclose(outs[1][0], y0 + x.astype(np.float64) @ w.T.astype(np.float64), rtol=1e-4,
-                                   atol=2e-4)
+        y = d_y.numpy()
+        np.testing.assert_allclose(y, y0 + ref, rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(d_so.numpy()[:, :rows], _row_stats(y, out_dim)[:, :rows], rtol=1e-12, atol=0)
+        if out_dim % 32 == 0:
+            half = out_dim // 2
+            d_a = qa.DeviceArray((rows, half), np.float32)
+            qa.check(fn(d_w.ptr, out_dim, in_dim, d_x.ptr, rows, d_a.ptr, 0, ptr(d_nw), ptr(d_st), st_in.shape[0],
+                        eps, None, 1, ws.ptr, wsb, None))
+            qa.synchronize()
+            g, u = ref[:, :half], ref[:, half:]
+            np.testing.assert_allclose(d_a.numpy(), g / (1.0 + np.exp(-g)) * u, rtol=1e-5, atol=1e-5)
 
 
 def test_gemm_rows_bf16_rejects_unsupported_shapes(qa):
@@ -213,8 +223,8 @@ def test_gemm_rows_bf16_rejects_unsupported_shapes(qa):
 
 @pytest.mark.parametrize("n_streams", [5, 32])
 def test_bf16_weights_multistream_equals_f32_weights_and_oracle(qa, orc, greedy, n_streams):
-    """The multi-stream decode step with bf16-exact weights: the bf16-copy decoder and the f32 decoder
-    give identical ids, and both match the oracle decoding each stream alone (0.6B, 2 layers)."""
+    """The multi-stream decode step with bf16-exact weights: the bf16-copy decoder (bf16 MFMAs) and the
+    f32 decoder both match the oracle decoding each stream alone (0.6B, 2 layers)."""
     from qwenasr_amd import configs
 
     model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=2, bf16=True)
@@ -240,10 +250,10 @@ def test_bf16_weights_multistream_equals_f32_weights_and_oracle(qa, orc, greedy,
             for s in range(n_streams):
                 dec.fill_cache(s, kv[s][0], kv[s][1], int(lens[s]))
             got.append(dec.decode_streams(first, steps))
-    np.testing.assert_array_equal(got[0], got[1])
     for s in range(n_streams):
         cache = om.cache(cap, True)
         cache.fill(kv[s][0], kv[s][1], int(lens[s]))
         ids, margins, runner = om.decode_steps(cache, int(first[s]), steps)
-        greedy.match(got[0][:, s].tolist(), list(ids), list(margins), list(runner),
-                     f"bf16-exact weights, {n_streams}-stream step, stream {s}")
+        for g, name in zip(got, ("bf16 copies", "f32 weights")):
+            greedy.match(g[:, s].tolist(), list(ids), list(margins), list(runner),
+                         f"bf16-exact weights ({name}), {n_streams}-stream step, stream {s}")

@@ -75,10 +75,10 @@ def greedy(index: int, bf16: bool = False):
                                    oracle_seconds=round(time.time() - t0, 1)))
 
 
-def cfg4(n_check: int):
+def cfg4(n_check: int, bf16: bool = False):
     w = configs.CONFIGS[4]
     t0 = time.time()
-    model = qa.Model(w.size, n_layers=w.n_layers)
+    model = qa.Model(w.size, n_layers=w.n_layers, bf16=bf16)
     om = orc.OracleModel.from_product_model(model)
     lens = configs.cfg4_lengths(w.streams)
     first = configs.cfg4_first_ids(w.streams)
@@ -95,7 +95,7 @@ def cfg4(n_check: int):
         streams[str(s)] = dict(length=L, first_id=int(first[s]), ids=ids, margins=marg, runner_up=second,
                                cur_len=cache.cur_len)
         print(f"  cfg4 stream {s} (len {L}) done at {time.time() - t0:.0f}s", flush=True)
-    write("cfg4.json", dict(config=4, lengths=lens.tolist(), first_ids=first.tolist(), steps=w.steps,
+    write(f"cfg4{'_bf16' if bf16 else ''}.json", dict(config=4, bf16_weights=bf16, lengths=lens.tolist(), first_ids=first.tolist(), steps=w.steps,
                             streams=streams, oracle_seconds=round(time.time() - t0, 1)))
 
 
@@ -103,14 +103,14 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--configs", default="0,1,2,3,4")
     ap.add_argument("--cfg4-streams", type=int, default=4)
-    ap.add_argument("--bf16", action="store_true", help="bf16-exact weights (configs 1-3)")
+    ap.add_argument("--bf16", action="store_true", help="bf16-exact weights (configs 1-4)")
     args = ap.parse_args()
     for c in [int(v) for v in args.configs.split(",")]:
         t = time.time()
         if c == 0:
             cfg0()
         elif c == 4:
-            cfg4(args.cfg4_streams)
+            cfg4(args.cfg4_streams, bf16=args.bf16)
         elif args.bf16:
             greedy(c, bf16=True)
         else:

@@ -257,3 +257,29 @@ def test_bf16_weights_multistream_equals_f32_weights_and_oracle(qa, orc, greedy,
         for g, name in zip(got, ("bf16 copies", "f32 weights")):
             greedy.match(g[:, s].tolist(), list(ids), list(margins), list(runner),
                          f"bf16-exact weights ({name}), {n_streams}-stream step, stream {s}")
+
+
+def test_bf16_weights_long_prefill_matches_oracle(qa, orc, greedy):
+    """A 300-position prompt (longer than the 64 rows of the skinny GEMM): with bf16 copies the prefill's
+    projections run as three rocBLAS bf16 GEMMs over the exact three-part split of their inputs (exact
+    products, f32 sums).  Logits against the oracle and against the f32-weight decoder, then greedy ids."""
+    model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=3, bf16=True)
+    om = orc.OracleModel.from_product_model(model)
+    x = qa.prompt_input(model, 290, 10)
+    N = 16
+    ref_logits = om.forward_cached(x, 0, om.cache(300 + N, True))
+    ref = om.generate(x, N, qa.STOP_IDS, om.cache(300 + N, True))
+    logits = {}
+    for f32_weights in (False, True):
+        with _decoder(qa, model, 300 + N, f32_weights) as dec:
+            assert dec.weights_bf16 == (not f32_weights)
+            logits[f32_weights] = dec.forward(x, 0)
+            if not f32_weights:
+                out = dec.generate(x, N, margins=True)
+    for got in logits.values():
+        err = float(np.abs(got.astype(np.float64) - ref_logits).max())
+        rel = float(np.linalg.norm(got - ref_logits) / np.linalg.norm(ref_logits))
+        assert err <= 2e-3 and rel <= 1e-3, (err, rel)
+    assert float(np.abs(logits[False].astype(np.float64) - logits[True]).max()) <= 2e-3
+    assert greedy.match(out["ids"], ref["ids"], ref["margins"], ref["runner_up"],
+                        "bf16-exact weights, 300-position prompt") is None

@@ -23,8 +23,8 @@ def digest(*arrays) -> str:
     return h.hexdigest()[:16]
 
 
-def golden(index):
-    with open(os.path.join(GOLDEN, f"cfg{index}.json")) as f:
+def golden(index, bf16=False):
+    with open(os.path.join(GOLDEN, f"cfg{index}{'_bf16' if bf16 else ''}.json")) as f:
         return json.load(f)
 
 
@@ -98,19 +98,24 @@ def test_small_model_greedy_matches_oracle(qa, orc, greedy, f16):
         close(logits, ref_logits, atol=2e-3, rtol_l2=1e-3)
 
 
-@pytest.mark.parametrize("index", [1, 2, 3])
-def test_config_greedy_matches_golden(qa, greedy, index):
+@pytest.mark.parametrize("index,bf16", [(1, False), (2, False), (3, False), (3, True)])
+def test_config_greedy_matches_golden(qa, greedy, index, bf16):
+    """Configs 1-3 with seeded N(0, 0.02) f32 weights (the f32 kernels), and config 3 -- the bench
+    workload -- with those weights rounded to bf16 values (a converted bf16 checkpoint: the decoder
+    streams bf16 copies and the prefill of the 3913-position prompt runs the same kernels)."""
     from qwenasr_amd import configs
 
-    g = golden(index)
+    g = golden(index, bf16)
     w = configs.CONFIGS[index]
-    model = qa.Model(w.size, n_layers=w.n_layers)
+    model = qa.Model(w.size, n_layers=w.n_layers, bf16=bf16)
     x = qa.prompt_input(model, w.audio_tokens, w.prompt_tokens)
     assert digest(x, model.tensor("text.blk.0.attn_q.weight")) == g["input_digest"]
-    print(f"config {index}: prompt {w.prompt}, {w.new_tokens} tokens", flush=True)
+    label = f"config {index}{' (bf16-exact weights)' if bf16 else ''}"
+    print(f"{label}: prompt {w.prompt}, {w.new_tokens} tokens", flush=True)
     with qa.Decoder(model, 1, w.max_seq, w.cache_type) as dec:
+        assert dec.weights_bf16 == bf16
         out = dec.generate(x, w.new_tokens, margins=True)
-        div = greedy.match(out["ids"], g["ids"], g["margins"], g["runner_up"], f"config {index}")
+        div = greedy.match(out["ids"], g["ids"], g["margins"], g["runner_up"], label)
         if div is None:
             assert out["stopped"] == g["stopped"] and out["total_tokens"] == g["total_tokens"]
             assert dec.cur_len(0) == g["cur_len"]
@@ -119,16 +124,20 @@ def test_config_greedy_matches_golden(qa, greedy, index):
         assert dec.device_lens().tolist() == [dec.cur_len(0)]
 
 
-def test_config4_ragged_streams_match_golden(qa, greedy):
+@pytest.mark.parametrize("bf16", [False, True])
+def test_config4_ragged_streams_match_golden(qa, greedy, bf16):
+    """Config 4, all 32 streams, with f32 weights (f32-MFMA skinny GEMMs) and with bf16-exact weights
+    (bf16 copies, bf16-MFMA skinny GEMMs over the three-part split of the activations)."""
     from qwenasr_amd import configs
 
-    g = golden(4)
+    g = golden(4, bf16)
     w = configs.CONFIGS[4]
     lens = configs.cfg4_lengths(w.streams)
     first = configs.cfg4_first_ids(w.streams)
     assert lens.tolist() == g["lengths"] and first.tolist() == g["first_ids"]
-    model = qa.Model(w.size, n_layers=w.n_layers)
+    model = qa.Model(w.size, n_layers=w.n_layers, bf16=bf16)
     with qa.Decoder(model, w.streams, w.max_seq, w.cache_type) as dec:
+        assert dec.weights_bf16 == bf16
         for s in range(w.streams):
             k, v = configs.cfg4_stream_kv(s, int(lens[s]))
             dec.fill_cache(s, k, v, int(lens[s]))
@@ -138,7 +147,8 @@ def test_config4_ragged_streams_match_golden(qa, greedy):
         assert ids.shape == (w.steps, w.streams)
         assert sorted(int(s) for s in g["streams"]) == list(range(w.streams))   # every stream has a golden
         for s, ref in g["streams"].items():
-            greedy.match(ids[:, int(s)].tolist(), ref["ids"], ref["margins"], ref["runner_up"], f"config 4 stream {s}")
+            greedy.match(ids[:, int(s)].tolist(), ref["ids"], ref["margins"], ref["runner_up"],
+                         f"config 4{' (bf16-exact weights)' if bf16 else ''} stream {s}")
         assert dec.device_lens().tolist() == (lens + w.steps).tolist()
         assert [dec.cur_len(s) for s in range(w.streams)] == (lens + w.steps).tolist()
 

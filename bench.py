@@ -69,9 +69,16 @@ def cpu_baseline(model, length: int, steps: int):
     t0 = time.perf_counter()
     om.decode_steps(cache, 1234, steps)
     dt = time.perf_counter() - t0
+    # the oracle reads every f32 weight once per token (it has no bf16 copies), plus the f16 cache prefix
+    wbytes = 4 * sum(model.tensor(f"text.blk.{l}.{t}.weight").size for l in range(c.n_layers)
+                     for t in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"))
+    wbytes += 4 * model.tensor("text.output.weight").size
+    kv = 2 * 2 * c.n_layers * c.n_kv_heads * c.head_dim * (length + steps // 2)
+    gbs = (wbytes + kv) * steps / dt / 1e9
     return dict(value=round(steps / dt, 4), unit="tok/s", cores=cores, kind="port",
                 sample=f"{steps} decode steps of the 1.7B decoder by the CPU oracle (C, OpenMP, {cores} threads) at "
-                       f"context {length + 1}..{length + steps + 1}, f16 cache, {dt:.1f} s")
+                       f"context {length + 1}..{length + steps + 1}, f16 cache, {dt:.1f} s; it streams the f32 "
+                       f"weights and the cache prefix at {gbs:.0f} GB/s of host memory")
 
 
 def measured_traffic(bytes_per_launch: int):
@@ -344,7 +351,7 @@ def main():
     ap.add_argument("--roofline-reps", type=int, default=20)
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--multistream-steps", type=int, default=16)
-    ap.add_argument("--cpu-steps", type=int, default=16)
+    ap.add_argument("--cpu-steps", type=int, default=192, help="oracle decode steps of the CPU baseline (~10-20 s)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--weights", choices=["bf16-exact", "f32"], default="bf16-exact",
                     help="bf16-exact: weights rounded to bf16 values (a converted bf16 checkpoint); f32: unrounded")

@@ -140,7 +140,8 @@ def attention_roofline(qa, dec, reps: int):
     n = reps * lay.n_layers
     us = ms.value * 1e3 / n
     L = ctx + 1
-    bytes_per_launch = 4096 * L + 16384
+    elem = 2 if lay.cache_type == qa.QA_CACHE_F16 else 4
+    bytes_per_launch = 2 * cfg.n_kv_heads * cfg.head_dim * elem * L + 16384   # K and V rows, q in, o out
     return us, L, bytes_per_launch, n
 
 
@@ -355,6 +356,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--weights", choices=["bf16-exact", "f32"], default="bf16-exact",
                     help="bf16-exact: weights rounded to bf16 values (a converted bf16 checkpoint); f32: unrounded")
+    ap.add_argument("--kv-cache", choices=["f16", "f32"], default=None,
+                    help="cache type (default: the config's, f16 for configs 2 and 3; f32 is the drop-in's default)")
     ap.add_argument("--f32-compare-steps", type=int, default=64,
                     help="decode steps timed with the f32 weights streamed, on the same model (0: skip)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -385,9 +388,13 @@ def main():
     x = qa.prompt_input(model, w.audio_tokens, w.prompt_tokens)
     log(f"synthetic {w.size.name} ({args.weights} weights) built in {time.perf_counter() - t0:.1f}s")
     max_seq = w.prompt + args.warmup + args.steps + args.profile_steps + 2
+    if args.kv_cache:
+        import dataclasses
+        w = dataclasses.replace(w, cache_type=qa.QA_CACHE_F16 if args.kv_cache == "f16" else qa.QA_CACHE_F32)
+    kv_name = "f16" if w.cache_type == qa.QA_CACHE_F16 else "f32"
     dec = qa.Decoder(model, 1, max_seq, w.cache_type)
     weights_streamed = "bf16 copies of bf16-exact weights" if dec.weights_bf16 else "f32"
-    log(f"decoder ready (weights + {max_seq}-position f16 cache on device; GEMVs stream {weights_streamed})")
+    log(f"decoder ready (weights + {max_seq}-position {kv_name} cache on device; GEMVs stream {weights_streamed})")
 
     # the first prefill also allocates the prompt-sized workspaces and loads rocBLAS's kernels; the
     # second (same input, n_past 0 again: the cache rows are rewritten) is the steady-state time
@@ -491,9 +498,9 @@ def main():
         "data": (f"synthetic (seeded N(0,0.02) weights{', rounded to bf16 values as in a converted bf16 checkpoint' if args.weights == 'bf16-exact' else ''}, "
                  f"N(0,1) audio rows, random prompt ids)"),
         "config": {"workload": f"config {args.config}: {w.size.name} decoder, prefill {w.prompt} positions, greedy "
-                               f"decode of {args.steps} tokens at context {ctx0}..{ctx0 + args.steps}, f16 KV cache, "
+                               f"decode of {args.steps} tokens at context {ctx0}..{ctx0 + args.steps}, {kv_name} KV cache, "
                                f"{args.weights} weights, batch 1",
-                   "kv_cache": "f16", "prompt_positions": w.prompt, "weights": args.weights,
+                   "kv_cache": kv_name, "prompt_positions": w.prompt, "weights": args.weights,
                    "weights_streamed": weights_streamed},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": traffic_note,

@@ -16,6 +16,7 @@
 #include "ops.hpp"
 
 #include <cmath>
+#include <cstdlib>
 
 namespace qa {
 namespace {
@@ -193,6 +194,173 @@ __global__ __launch_bounds__(256) void prefill_rows_kernel(RowsParams p) {
         (red[0][hh][d] + red[1][hh][d]) + (red[2][hh][d] + red[3][hh][d]);
 }
 
+// f32 K/V on f32 MFMA (v_mfma_f32_16x16x4_f32: exact f32 products, f32 sums).  A workgroup owns 64
+// queries x both query heads of one KV head (8 waves: wave w takes head w % 2 and queries 16 (w / 2) ..
+// + 15) and walks the keys in tiles of 32, staged in LDS (double-buffered, the next tile in registers
+// while the current one is computed).  Each wave computes S^T = K Q^T (keys x queries): the operand
+// layout of the product then holds, in each lane, 4 keys of one query, which is exactly the B operand
+// of O^T = V^T P^T, so P never moves.  Softmax is online, in f32, with the running sum in double:
+// p_j = exp(s_j - m) rescaled as m grows, and o / l at the end -- the same f32 arithmetic as
+// prefill_rows_kernel in another association (about 1e-6 relative).
+// Lane layouts of v_mfma_f32_16x16x4_f32 (lane l, g = l / 16): A[m = l % 16][k = g], B[k = g][n = l % 16],
+// C[m = 4 g + i][n = l % 16], i = 0..3.
+constexpr int kF32Tile = 32;                  // keys per tile
+constexpr int kF32KLs = kHeadDim + 8;         // K row stride in LDS (floats): 16-byte reads of 16 rows
+constexpr int kF32VLs = kHeadDim + 16;        // V row stride: the 4 lane groups read 4 rows of one column
+constexpr int kF32Queries = 64;
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(512) void prefill_f32mfma_kernel(RowsParams p) {
+    __shared__ __attribute__((aligned(16))) float ks[2][kF32Tile * kF32KLs];
+    __shared__ __attribute__((aligned(16))) float vs[2][kF32Tile * kF32VLs];
+    const int n_qb = (p.n_tokens + kF32Queries - 1) / kF32Queries;
+    const int qb = n_qb - 1 - static_cast<int>(blockIdx.x);        // longest query blocks first
+    const int kvh = blockIdx.y;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int hh = wave & 1, qi = wave >> 1;
+    const int q0 = qb * kF32Queries;
+    const int qrow = q0 + 16 * qi + c;                              // this lane's query (token index)
+    const int qpos = p.n_past + min(qrow, p.n_tokens - 1);          // its position (rows past T: the last)
+    const int n_keys = p.n_past + min(q0 + kF32Queries, p.n_tokens);   // keys of the workgroup's last query
+    const int n_tiles = (n_keys + kF32Tile - 1) / kF32Tile;
+
+    // q of this lane's query, d = 16 u + 4 g + 0..3 (the B operand order)
+    f4v qreg[8];
+    {
+        const float * qp = p.q + static_cast<int64_t>(min(qrow, p.n_tokens - 1)) * p.q_stride +
+                           (kRep * kvh + hh) * kHeadDim + 4 * g;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) qreg[u] = *reinterpret_cast<const f4v *>(qp + 16 * u);
+    }
+    const float * kbase = static_cast<const float *>(p.k) + kvh * p.head_stride;
+    const float * vbase = static_cast<const float *>(p.v) + kvh * p.head_stride;
+    // tile staging: thread t loads 16 bytes at key t / 32 (+ 16), d 4 (t % 32), for K and for V
+    const int lk = threadIdx.x >> 5, ld = 4 * (threadIdx.x & 31);
+    f4v kr[2], vr[2];
+    auto load_tile = [&](int tile) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int key = min(tile * kF32Tile + lk + 16 * h, n_keys - 1);
+            kr[h] = *reinterpret_cast<const f4v *>(kbase + static_cast<int64_t>(key) * p.row_stride + ld);
+            vr[h] = *reinterpret_cast<const f4v *>(vbase + static_cast<int64_t>(key) * p.row_stride + ld);
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            *reinterpret_cast<f4v *>(&ks[buf][(lk + 16 * h) * kF32KLs + ld]) = kr[h];
+            *reinterpret_cast<f4v *>(&vs[buf][(lk + 16 * h) * kF32VLs + ld]) = vr[h];
+        }
+    };
+    load_tile(0);
+    store_tile(0);
+    if (n_tiles > 1) load_tile(1);
+    __syncthreads();
+
+    f4v oacc[8];
+#pragma unroll
+    for (int db = 0; db < 8; ++db) oacc[db] = f4v{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY;
+    double l_run = 0.0;
+    for (int t = 0; t < n_tiles; ++t) {
+        const int buf = t & 1;
+        const float * kt = ks[buf];
+        const float * vt = vs[buf];
+        // S^T for keys 16 b + 0..15 of the tile
+        f4v sacc[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            sacc[b] = f4v{0.f, 0.f, 0.f, 0.f};
+            const float * kr_l = kt + (16 * b + c) * kF32KLs + 4 * g;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const f4v a = *reinterpret_cast<const f4v *>(kr_l + 16 * u);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sacc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], qreg[u][j], sacc[b], 0, 0, 0);
+            }
+        }
+        // scale, causal mask, online softmax of this lane's query over the tile's 32 keys
+        float sv[2][4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int kp = t * kF32Tile + 16 * b + 4 * g + i;
+                const float x = kp <= qpos ? sacc[b][i] * p.scale : -INFINITY;
+                sv[b][i] = x;
+                mx = fmaxf(mx, x);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const float m_new = fmaxf(m_run, mx);
+        const float corr = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+        float psum = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float e = sv[b][i] == -INFINITY ? 0.0f : expf(sv[b][i] - m_new);
+                sv[b][i] = e;
+                psum += e;
+            }
+        }
+        psum += __shfl_xor(psum, 16, kWave);
+        psum += __shfl_xor(psum, 32, kWave);
+        l_run = l_run * static_cast<double>(corr) + static_cast<double>(psum);
+        m_run = m_new;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) oacc[db] *= corr;
+        // O^T[d][q] += V^T[d][key] P^T[key][q]: keys 16 b + 4 g + i of the tile in k-slot g of step (b, i)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float * vrow = vt + (16 * b + 4 * g + i) * kF32VLs + c;
+#pragma unroll
+                for (int db = 0; db < 8; ++db) {
+                    oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * db], sv[b][i], oacc[db], 0, 0, 0);
+                }
+            }
+        }
+        // stage the next tile (its loads were issued a tile ago) and issue the loads of the one after.
+        // Buffer buf ^ 1 last held tile t - 1, which every wave finished before the previous barrier.
+        if (t + 1 < n_tiles) {
+            store_tile(buf ^ 1);
+            if (t + 2 < n_tiles) load_tile(t + 2);
+            __syncthreads();
+        }
+    }
+    // oacc[db][i] = O^T[d = 16 db + 4 g + i][q = c]; normalise and store
+    if (qrow < p.n_tokens) {
+        const float r = static_cast<float>(1.0 / l_run);
+        float * out = p.out + static_cast<int64_t>(qrow) * p.out_stride + (kRep * kvh + hh) * kHeadDim + 4 * g;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            f4v o = oacc[db] * r;
+            *reinterpret_cast<f4v *>(out + 16 * db) = o;
+        }
+    }
+}
+
+int launch_f32mfma(const RowsParams & p, int n_kv_heads, hipStream_t stream) {
+    const int n_qb = (p.n_tokens + kF32Queries - 1) / kF32Queries;
+    hipLaunchKernelGGL(prefill_f32mfma_kernel, dim3(static_cast<unsigned>(n_qb), static_cast<unsigned>(n_kv_heads)),
+                       dim3(512), 0, stream, p);
+    QA_LAUNCH_CHECK("prefill_f32mfma_kernel");
+    return QA_OK;
+}
+
+// QA_PREFILL_F32_ROWS=1 keeps the f32 row kernel (comparison)
+bool f32_rows_forced() {
+    const char * e = std::getenv("QA_PREFILL_F32_ROWS");
+    return e && std::atoi(e) != 0;
+}
+
 template <typename CT, bool R16>
 int launch_rows(const RowsParams & p, int n_kv_heads, hipStream_t stream) {
     const int nk_pad = (p.n_past + p.n_tokens + 63) & ~63;
@@ -240,6 +408,7 @@ int prefill_attn_launch(const float * q, int32_t q_stride, const void * cache, c
     p.row_stride = kHeadDim;
     p.k = k0;
     p.v = v0;
+    if (!f32_rows_forced()) return launch_f32mfma(p, layout.n_kv_heads, stream);
     return launch_rows<float, false>(p, layout.n_kv_heads, stream);
 }
 
@@ -285,6 +454,7 @@ int causal_f32_launch(const float * q, int32_t q_stride, const float * k, const 
     p.scale = scale;
     p.head_stride = kHeadDim;
     p.row_stride = row_stride;
+    if (!f32_rows_forced()) return launch_f32mfma(p, n_kv_heads, stream);
     return launch_rows<float, false>(p, n_kv_heads, stream);
 }
 

@@ -274,6 +274,38 @@ def test_prefill_attention(qa, orc, f16, n_past, T):
     check_close(got[t], dec)
 
 
+@pytest.mark.parametrize("n_past,T", [(0, 3913), (700, 1300)])
+def test_prefill_attention_f32_mfma_equals_row_kernel(qa, orc, n_past, T):
+    """f32 cache, long prompts: the f32-MFMA kernel (online softmax, exact f32 products) against the f32
+    row kernel (QA_PREFILL_F32_ROWS=1, two passes) over every row, and sampled rows against the oracle's
+    decode over their prefix."""
+    import os
+
+    L = n_past + T
+    lay = layout(qa, 2, 1, L + 3, False)
+    cache = Cache(qa, lay)
+    rng = np.random.default_rng(L + 17)
+    k, v = cache.fill(rng, 1, [L])[0]
+    q = rng.standard_normal((T, 16, 128)).astype(np.float32)
+    d_q = dev(qa, q)
+    outs = []
+    for rows in ("0", "1"):
+        os.environ["QA_PREFILL_F32_ROWS"] = rows
+        try:
+            d_out = zeros(qa, (T, 2048))
+            print(f"prefill f32 rows-kernel={rows} n_past={n_past} T={T}", flush=True)
+            qa.check(qa.lib.qa_prefill_attn(d_q.ptr, cache.ptr, C.byref(lay), 1, 0, n_past, T, 16, SCALE, d_out.ptr,
+                                            None, 0, NULL_STREAM))
+            qa.synchronize()
+            outs.append(d_out.numpy().reshape(T, 16, 128))
+        finally:
+            os.environ.pop("QA_PREFILL_F32_ROWS", None)
+    check_close(outs[0], outs[1], atol=2e-5, rtol_l2=2e-6)
+    for t in (0, 1, 63, 64, T // 2, T - 1):
+        ref = orc.cache_attention(k[:, :n_past + t + 1], v[:, :n_past + t + 1], q[t:t + 1], n_past + t, False)[0]
+        check_close(outs[0][t], ref)
+
+
 def test_prefill_attention_long_split_rows(qa, orc):
     """Config-3 prefill shape (T = 3913, f16 cache): the longest query tiles are split over two
     workgroups and merged.  Sampled rows, in split and unsplit tiles, equal a decode over their prefix."""

@@ -211,11 +211,9 @@ constexpr int kF32Queries = 64;
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(512) void prefill_f32mfma_kernel(RowsParams p) {
-    __shared__ __attribute__((aligned(16))) float ks[2][kF32Tile * kF32KLs];
-    __shared__ __attribute__((aligned(16))) float vs[2][kF32Tile * kF32VLs];
-    const int n_qb = (p.n_tokens + kF32Queries - 1) / kF32Queries;
-    const int qb = n_qb - 1 - static_cast<int>(blockIdx.x);        // longest query blocks first
+// One query block of 64 (8 waves) against its causal key range.
+__device__ inline void f32mfma_block(const RowsParams & p, float (*ks)[kF32Tile * kF32KLs],
+                                     float (*vs)[kF32Tile * kF32VLs], int qb) {
     const int kvh = blockIdx.y;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x >> 6;
@@ -347,9 +345,24 @@ __global__ __launch_bounds__(512) void prefill_f32mfma_kernel(RowsParams p) {
     }
 }
 
+__global__ __launch_bounds__(512) void prefill_f32mfma_kernel(RowsParams p) {
+    __shared__ __attribute__((aligned(16))) float ks[2][kF32Tile * kF32KLs];
+    __shared__ __attribute__((aligned(16))) float vs[2][kF32Tile * kF32VLs];
+    const int n_qb = (p.n_tokens + kF32Queries - 1) / kF32Queries;
+    // causal balance: workgroup i takes query block n_qb - 1 - i, then block i, so every workgroup
+    // walks about the same number of key tiles
+    const int first = n_qb - 1 - static_cast<int>(blockIdx.x);
+    f32mfma_block(p, ks, vs, first);
+    const int second = static_cast<int>(blockIdx.x);
+    if (second < first) {
+        __syncthreads();                 // every wave is done with the first block's LDS tiles
+        f32mfma_block(p, ks, vs, second);
+    }
+}
+
 int launch_f32mfma(const RowsParams & p, int n_kv_heads, hipStream_t stream) {
     const int n_qb = (p.n_tokens + kF32Queries - 1) / kF32Queries;
-    hipLaunchKernelGGL(prefill_f32mfma_kernel, dim3(static_cast<unsigned>(n_qb), static_cast<unsigned>(n_kv_heads)),
+    hipLaunchKernelGGL(prefill_f32mfma_kernel, dim3(static_cast<unsigned>((n_qb + 1) / 2), static_cast<unsigned>(n_kv_heads)),
                        dim3(512), 0, stream, p);
     QA_LAUNCH_CHECK("prefill_f32mfma_kernel");
     return QA_OK;

@@ -72,6 +72,30 @@ def test_harness_generate_command(checkpoint):
     assert int(meta["total_tokens"]) == ref["total_tokens"] and int(meta["generated_tokens"]) == len(ids)
 
 
+def test_harness_generate_command_bf16_checkpoint(tmp_path, qa, orc, greedy):
+    """A GGUF holding bf16-exact weights (what the reference's converter writes from the released bf16
+    checkpoint, convert.py:386-387) through the drop-in: the decoder keeps bf16 weight copies and the
+    generated ids still match the oracle's on the same f32 values."""
+    model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=2, vocab=2048, bf16=True)
+    gguf = tmp_path / "model_bf16.gguf"
+    model.write_gguf(str(gguf))
+    wav = tmp_path / "clip.wav"
+    with wave.open(str(wav), "wb") as w:
+        w.setnchannels(1)
+        w.setsampwidth(2)
+        w.setframerate(16000)
+        w.writeframes(bytes(2 * 176000))
+    n = 8
+    meta = run(harness_generate_argv(gguf, wav, n))
+    ids = [int(v) for v in meta["generated_ids"].split(",") if v]
+    om = orc.OracleModel.from_product_model(model)
+    x = qa.prompt_input(model, 143, 13)
+    stops = [model.cfg.vocab - 5, model.cfg.vocab - 7, model.cfg.vocab - 5]
+    ref = om.generate(x, n, stops, om.cache(156 + n, f16=False))
+    assert greedy.match(ids, ref["ids"], ref["margins"], ref["runner_up"],
+                        "driver generate, bf16-exact GGUF (f32 cache)") is None
+
+
 def test_harness_prefill_command(checkpoint):
     """check_text_prefill.py:37-60: --prefill --out logits.f32, file shape (vocab,) against the oracle's
     non-cached prefill."""

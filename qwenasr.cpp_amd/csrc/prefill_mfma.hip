@@ -6,11 +6,14 @@
 // QK^T and the normalised probabilities to f16 before PV; both are exactly the f16 operands the MFMA
 // takes, with f32 accumulation.
 //
-// Tiling.  A workgroup (8 waves) owns 64 query tokens of one stream and both query heads of one KV
-// head: 128 query columns, every K/V byte of the head shared by both heads.  Wave w takes head
-// 2g + w/4 and tokens [16 (w & 3), +16).  Per 64-key tile a wave computes S^T = K Q^T (keys x queries,
-// 16x16 blocks, head dim in 4 steps of 32), so after the MFMA each lane holds 16 keys of one query
-// column.
+// Tiling.  A workgroup (8 waves) owns 128 query tokens of one stream and both query heads of one KV
+// head: 256 query columns, every K/V byte of the head shared by both heads and by all 128 tokens.
+// Wave w takes head 2g + w/4 and tokens [32 (w & 3), +32) as two blocks of 16 columns.  Per 64-key
+// tile a wave computes S^T = K Q^T (keys x queries, 16x16 blocks, head dim in 4 steps of 32) for both
+// blocks, each K fragment read from LDS once and used by the MFMAs of both blocks (likewise each V^T
+// fragment in PV).  After the MFMA each lane holds 16 keys of one query column per block.
+// (Measured at T = 3913: with 64 query tokens per workgroup the steps waited on the K/V tile loads,
+// each CU pulling one 32 KB tile per step for every 128 columns; 128 tokens halve that traffic.)
 //
 // Exact GGML softmax needs the row max and sum before any PV, so the key tiles are walked twice, by two
 // kernels over the same work items:
@@ -50,9 +53,11 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBQ = 64;     // query tokens per workgroup
+constexpr int kBQ = 128;    // query tokens per workgroup
 constexpr int kBK = 64;     // keys per tile
-constexpr int kPfThreads = 512;   // 8 waves: wave w takes head 2g + w / 4 and query tokens 16 (w % 4) .. + 15
+constexpr int kQB = 2;      // 16-column query blocks per wave
+constexpr int kCols = 2 * kBQ;    // query columns per workgroup (both heads)
+constexpr int kPfThreads = 512;   // 8 waves: wave w takes head 2g + w / 4 and query tokens 32 (w % 4) .. + 31
 // Row strides: a 16-byte LDS read by 16 lanes of consecutive rows is conflict-free on gfx950 when the
 // stride in dwords is 8 mod 16 (measured: 80, 112, 144 halfs conflict-free; 72, 88, 96, 136 halfs
 // lose ~half the LDS cycles to bank conflicts).
@@ -72,7 +77,7 @@ constexpr int kPfMaxMerge = 8192;       // merge counters: one per (KV head, que
 constexpr int kPfCutUnits = 2048;       // (KV head, query tile) units up to which long tiles are cut
 constexpr size_t kPfQueueBytes = 2 * kPfMaxHeads * kPfCounterStride * sizeof(uint32_t);
 constexpr size_t kPfFixedBytes = kPfQueueBytes + static_cast<size_t>(kPfMaxMerge) * kPfCounterStride * sizeof(uint32_t);
-constexpr size_t kPfPartialFloats = 8 * 512 * 4;    // one part's O: 8 float4 per thread
+constexpr size_t kPfPartialFloats = kQB * 8 * kPfThreads * 4;    // one part's O: 16 float4 per thread
 
 struct alignas(16) PrefillStat {
     float m;
@@ -93,7 +98,7 @@ struct MfmaParams {
     int32_t n_items;          // work items per KV head: n_qt + (n_qt - qt_cut)
     float scale;
     uint32_t * queue;         // pull counters of this pass, one per KV head (every call leaves them zero)
-    PrefillStat * stats;      // [n_kv][n_qt][2 parts][128 columns]
+    PrefillStat * stats;      // [n_kv][n_qt][2 parts][kCols columns]
     float * partial;          // [n_kv][n_qt - qt_cut][2 parts][kPfPartialFloats]
     uint32_t * counters;      // [n_kv][n_qt - qt_cut][kPfCounterStride]
 };
@@ -173,16 +178,23 @@ __device__ inline void store_tile(const TileRegs & r, _Float16 * sK, _Float16 * 
     }
 }
 
-// S^T tile of this wave: S[kb] = 16 keys (kb) x the wave's 16 queries.
-__device__ inline void scores_tile(const _Float16 * sK, const h8 (&qf)[4], int c16, int g4, f4 (&S)[4]) {
+// S^T tiles of this wave: S[qb][kb] = 16 keys (kb) x the 16 queries of block qb; each K fragment is
+// read once for both blocks.
+__device__ inline void scores_tile(const _Float16 * sK, const h8 (&qf)[kQB][4], int c16, int g4, f4 (&S)[kQB][4]) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) S[kb] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int qb = 0; qb < kQB; ++qb) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) S[qb][kb] = f4{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
             const h8 a = *reinterpret_cast<const h8 *>(sK + (kb * 16 + c16) * kKS + ks * 32 + g4 * 8);
-            S[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ks], S[kb], 0, 0, 0);
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) {
+                S[qb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[qb][ks], S[qb][kb], 0, 0, 0);
+            }
         }
     }
 }
@@ -222,16 +234,21 @@ __device__ inline void stats_update(const f4 (&S)[4], float c, float & m, double
     m = mn;
 }
 
-// mc = (M scale - log2 S) log2 e for this lane's query column: p = exp2(s c - mc) = exp(s scale - M) / S.
-__device__ inline void pv_tile(const f4 (&S)[4], const _Float16 * sV, float mc, float c, int c16, int g4,
-                               f4 (&O)[8]) {
-    // P^T fragments: pf[ksv] element e <-> key (2 ksv + e / 4) * 16 + g4 * 4 + e % 4
-    h8 pf[2];
+// mc[qb] = (M scale - log2 S) log2 e for this lane's query column of block qb: p = exp2(s c - mc) =
+// exp(s scale - M) / S.  Each V^T fragment is read once for both blocks.
+__device__ inline void pv_tile(const f4 (&S)[kQB][4], const _Float16 * sV, const float (&mc)[kQB], float c, int c16,
+                               int g4, f4 (&O)[kQB][8]) {
+    // P^T fragments: pf[qb][ksv] element e <-> key (2 ksv + e / 4) * 16 + g4 * 4 + e % 4
+    h8 pf[kQB][2];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int qb = 0; qb < kQB; ++qb) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            pf[kb >> 1][(kb & 1) * 4 + i] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(S[kb][i], c, -mc)));
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                pf[qb][kb >> 1][(kb & 1) * 4 + i] =
+                    static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(S[qb][kb][i], c, -mc[qb])));
+            }
         }
     }
 #pragma unroll
@@ -239,7 +256,10 @@ __device__ inline void pv_tile(const f4 (&S)[4], const _Float16 * sV, float mc, 
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
             const h8 a = *reinterpret_cast<const h8 *>(sV + (db * 16 + c16) * kVS + ksv * 32 + g4 * 8);
-            O[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pf[ksv], O[db], 0, 0, 0);
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) {
+                O[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pf[qb][ksv], O[qb][db], 0, 0, 0);
+            }
         }
     }
 }
@@ -284,7 +304,7 @@ __device__ inline Item item_of(const MfmaParams & p, int g, int k) {
     return it;
 }
 
-// One work item.  PASS 1: the part's row statistics (max and sum of exp) of its 128 query columns.
+// One work item.  PASS 1: the part's row statistics (max and sum of exp) of its kCols query columns.
 // PASS 2: p over the part's keys with the statistics of both parts of its query tile, and
 // O^T += V^T P^T; the two parts of a cut tile are added by whichever finishes second.
 template <int PASS>
@@ -307,68 +327,86 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
     const _Float16 * vh = p.v + g * p.head_stride;
     const float c = p.scale * kLog2e;
 
-    // this lane's query column and its causal key limit (keys j <= lim are attended)
-    const int tq = t0 + (wave & 3) * 16 + c16;
-    const int lim = tq < p.n_tokens ? p.n_past + tq : -1;
+    // this lane's query column of block qb and its causal key limit (keys j <= lim are attended)
+    int tq[kQB], lim[kQB], col[kQB];
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+        tq[qb] = t0 + (wave & 3) * 32 + qb * 16 + c16;
+        lim[qb] = tq[qb] < p.n_tokens ? p.n_past + tq[qb] : -1;
+        col[qb] = hh * kBQ + (wave & 3) * 32 + qb * 16 + c16;   // statistics column
+    }
     // statistics of part j of this query tile: [g][qt][j][column]
-    const int col = hh * 64 + (wave & 3) * 16 + c16;
-    PrefillStat * st = p.stats + (static_cast<int64_t>(g) * p.n_qt + it.qt) * 2 * 128;
+    PrefillStat * st = p.stats + (static_cast<int64_t>(g) * p.n_qt + it.qt) * 2 * kCols;
 
-    // Q fragments, the B operand of S^T: lane holds query column c16 and 8 dims of each 32-dim step,
-    // rounded to f16 (GGML's conversion of src1 for an f16 src0); absent tokens are zero
-    h8 qf[4];
-    {
-        const int tqc = min(tq, p.n_tokens - 1);
-        const bool ok = tq < p.n_tokens;
+    // Q fragments, the B operand of S^T: lane holds query column c16 of each block and 8 dims of each
+    // 32-dim step, rounded to f16 (GGML's conversion of src1 for an f16 src0); absent tokens are zero
+    h8 qf[kQB][4];
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+        const int tqc = min(tq[qb], p.n_tokens - 1);
+        const bool ok = tq[qb] < p.n_tokens;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const float * qp = p.q + static_cast<int64_t>(tqc) * p.q_stride + h * kHeadDim + ks * 32 + g4 * 8;
             const float4 a = *reinterpret_cast<const float4 *>(qp);
             const float4 b = *reinterpret_cast<const float4 *>(qp + 4);
-            qf[ks] = h8{static_cast<_Float16>(ok ? a.x : 0.f), static_cast<_Float16>(ok ? a.y : 0.f),
-                        static_cast<_Float16>(ok ? a.z : 0.f), static_cast<_Float16>(ok ? a.w : 0.f),
-                        static_cast<_Float16>(ok ? b.x : 0.f), static_cast<_Float16>(ok ? b.y : 0.f),
-                        static_cast<_Float16>(ok ? b.z : 0.f), static_cast<_Float16>(ok ? b.w : 0.f)};
+            qf[qb][ks] = h8{static_cast<_Float16>(ok ? a.x : 0.f), static_cast<_Float16>(ok ? a.y : 0.f),
+                            static_cast<_Float16>(ok ? a.z : 0.f), static_cast<_Float16>(ok ? a.w : 0.f),
+                            static_cast<_Float16>(ok ? b.x : 0.f), static_cast<_Float16>(ok ? b.y : 0.f),
+                            static_cast<_Float16>(ok ? b.z : 0.f), static_cast<_Float16>(ok ? b.w : 0.f)};
         }
     }
 
-    float mc = 0.f;
+    float mc[kQB];
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) mc[qb] = 0.f;
     if constexpr (PASS == 2) {
         // row max M and sum S over the parts: S = s_0 exp(m_0 - M) + s_1 exp(m_1 - M), in double; the
         // normalisation 1 / S folded into the exponent: exp2(s c - M c - log2 S); a column without keys
         // (padding) gets an exponent of -inf, so p = 0
-        const PrefillStat a = st[col];
-        PrefillStat b{-INFINITY, 0.f, 0.0};
-        if (it.cut) b = st[128 + col];
-        const float M = fmaxf(a.m, b.m);
-        double S = 0.0;
-        if (M != -INFINITY) {
-            S = a.s * static_cast<double>(__builtin_amdgcn_exp2f((a.m - M) * c));
-            if (it.cut) S += b.s * static_cast<double>(__builtin_amdgcn_exp2f((b.m - M) * c));
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) {
+            const PrefillStat a = st[col[qb]];
+            PrefillStat b{-INFINITY, 0.f, 0.0};
+            if (it.cut) b = st[kCols + col[qb]];
+            const float M = fmaxf(a.m, b.m);
+            double S = 0.0;
+            if (M != -INFINITY) {
+                S = a.s * static_cast<double>(__builtin_amdgcn_exp2f((a.m - M) * c));
+                if (it.cut) S += b.s * static_cast<double>(__builtin_amdgcn_exp2f((b.m - M) * c));
+            }
+            mc[qb] = M == -INFINITY || !(S > 0.0) ? INFINITY
+                                                  : static_cast<float>(static_cast<double>(M * c) + std::log2(S));
         }
-        mc = M == -INFINITY || !(S > 0.0) ? INFINITY : static_cast<float>(static_cast<double>(M * c) + std::log2(S));
     }
 
-    float m = -INFINITY;
-    double sum = 0.0;
-    f4 O[8];
+    float m[kQB];
+    double sum[kQB];
+    f4 O[kQB][8];
 #pragma unroll
-    for (int db = 0; db < 8; ++db) O[db] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int qb = 0; qb < kQB; ++qb) {
+        m[qb] = -INFINITY;
+        sum[qb] = 0.0;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) O[qb][db] = f4{0.f, 0.f, 0.f, 0.f};
+    }
     TileRegs regs;
     const int kt0 = it.kt0, kt1 = it.kt1;
     load_tile(kh, vh, kt0, kend, kWithV, regs);
     store_tile(regs, sK[0], sV[0], kWithV);
     if (kt0 + 1 < kt1) load_tile(kh, vh, kt0 + 1, kend, kWithV, regs);
     __syncthreads();
-    // one key tile: scores, masking (diagonal tiles only), statistics or PV, then the next tile into
-    // the other LDS buffer and the one after into registers
     auto step = [&](int kt, auto mask) {
         const int b = (kt - kt0) & 1;
-        f4 S[4];
+        f4 S[kQB][4];
         scores_tile(sK[b], qf, c16, g4, S);
-        if constexpr (decltype(mask)::value) mask_tile(S, lim, kt, g4);
+        if constexpr (decltype(mask)::value) {
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) mask_tile(S[qb], lim[qb], kt, g4);
+        }
         if constexpr (PASS == 1) {
-            stats_update(S, c, m, sum);
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) stats_update(S[qb], c, m[qb], sum[qb]);
         } else {
             pv_tile(S, sV[b], mc, c, c16, g4, O);
         }
@@ -378,19 +416,22 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
         }
         __syncthreads();
     };
-    // separate loops, so that the unmasked tiles carry no masking code at all
+    auto run = [&](int kt, auto mask) { step(kt, mask); };
     int kt = kt0;
-    for (; kt < min(kt1, kt_full); ++kt) step(kt, std::false_type{});
-    for (; kt < kt1; ++kt) step(kt, std::true_type{});
+    for (; kt < min(kt1, kt_full); ++kt) run(kt, std::false_type{});
+    for (; kt < kt1; ++kt) run(kt, std::true_type{});
 
     if constexpr (PASS == 1) {
-        // combine the 4 lanes of the query column (lane bits 4, 5) and store the part's statistics
-        float M = fmaxf(m, __shfl_xor(m, 16, kWave));
-        M = fmaxf(M, __shfl_xor(M, 32, kWave));
-        double sm = M == -INFINITY ? 0.0 : sum * static_cast<double>(__builtin_amdgcn_exp2f((m - M) * c));
-        sm += __shfl_xor(sm, 16, kWave);
-        sm += __shfl_xor(sm, 32, kWave);
-        if (g4 == 0) st[it.j * 128 + col] = PrefillStat{M, 0.0f, sm};
+        // combine the 4 lanes of each query column (lane bits 4, 5) and store the part's statistics
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) {
+            float M = fmaxf(m[qb], __shfl_xor(m[qb], 16, kWave));
+            M = fmaxf(M, __shfl_xor(M, 32, kWave));
+            double sm = M == -INFINITY ? 0.0 : sum[qb] * static_cast<double>(__builtin_amdgcn_exp2f((m[qb] - M) * c));
+            sm += __shfl_xor(sm, 16, kWave);
+            sm += __shfl_xor(sm, 32, kWave);
+            if (g4 == 0) st[it.j * kCols + col[qb]] = PrefillStat{M, 0.0f, sm};
+        }
         return;
     }
 
@@ -402,10 +443,15 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
         uint64_t * mine = reinterpret_cast<uint64_t *>(p.partial + (unit * 2 + it.j) * kPfPartialFloats);
         const uint64_t * other = reinterpret_cast<const uint64_t *>(p.partial + (unit * 2 + (it.j ^ 1)) * kPfPartialFloats);
 #pragma unroll
-        for (int db = 0; db < 8; ++db) {
-            const int e = (db * kPfThreads + static_cast<int>(threadIdx.x)) * 2;
-            __hip_atomic_store(mine + e, pack2(O[db][0], O[db][1]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(mine + e + 1, pack2(O[db][2], O[db][3]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int qb = 0; qb < kQB; ++qb) {
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                const int e = ((qb * 8 + db) * kPfThreads + static_cast<int>(threadIdx.x)) * 2;
+                __hip_atomic_store(mine + e, pack2(O[qb][db][0], O[qb][db][1]), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(mine + e + 1, pack2(O[qb][db][2], O[qb][db][3]), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
@@ -419,20 +465,27 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
         __syncthreads();
         if (!s_last) return;
 #pragma unroll
-        for (int db = 0; db < 8; ++db) {
-            const int e = (db * kPfThreads + static_cast<int>(threadIdx.x)) * 2;
-            const uint64_t lo = __hip_atomic_load(other + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const uint64_t hi = __hip_atomic_load(other + e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            O[db] += f4{lo_float(lo), hi_float(lo), lo_float(hi), hi_float(hi)};
+        for (int qb = 0; qb < kQB; ++qb) {
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                const int e = ((qb * 8 + db) * kPfThreads + static_cast<int>(threadIdx.x)) * 2;
+                const uint64_t lo = __hip_atomic_load(other + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t hi = __hip_atomic_load(other + e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                O[qb][db] += f4{lo_float(lo), hi_float(lo), lo_float(hi), hi_float(hi)};
+            }
         }
     }
 
-    // O^T: lane holds dims db * 16 + g4 * 4 + i of its query column
-    if (tq < p.n_tokens) {
-        float * op = p.out + static_cast<int64_t>(tq) * p.q_stride + h * kHeadDim + g4 * 4;
+    // O^T: lane holds dims db * 16 + g4 * 4 + i of its query column of each block
 #pragma unroll
-        for (int db = 0; db < 8; ++db) {
-            *reinterpret_cast<float4 *>(op + db * 16) = make_float4(O[db][0], O[db][1], O[db][2], O[db][3]);
+    for (int qb = 0; qb < kQB; ++qb) {
+        if (tq[qb] < p.n_tokens) {
+            float * op = p.out + static_cast<int64_t>(tq[qb]) * p.q_stride + h * kHeadDim + g4 * 4;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                *reinterpret_cast<float4 *>(op + db * 16) =
+                    make_float4(O[qb][db][0], O[qb][db][1], O[qb][db][2], O[qb][db][3]);
+            }
         }
     }
 }
@@ -442,8 +495,9 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
 // workgroups are dispatched round-robin over the 8 XCDs, so with 8 KV heads every XCD works on one
 // head, whose K/V (2 MB at 4k positions) then stays in that XCD's L2.  Each workgroup makes exactly one
 // pull past the end of its queue; the last of those resets the counter to zero for the next call.
+// Pass 1 holds no V tile and no O: 128 registers give two workgroups per CU.
 template <int PASS>
-__global__ __launch_bounds__(kPfThreads, 4) void prefill_mfma_kernel(MfmaParams p) {
+__global__ __launch_bounds__(kPfThreads, 2) void prefill_mfma_kernel(MfmaParams p) {
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][kBK * kKS];
     __shared__ __attribute__((aligned(16))) _Float16 sV[PASS == 2 ? 2 : 1][PASS == 2 ? kHeadDim * kVS : 8];
     __shared__ int s_pull;
@@ -489,7 +543,7 @@ int resident_grid() {
 size_t prefill_mfma_workspace_bytes(int32_t n_tokens, int32_t n_kv) {
     if (n_tokens <= 0 || n_kv <= 0) return 256;
     const int64_t units = (static_cast<int64_t>(n_tokens) + kBQ - 1) / kBQ * n_kv;
-    return kPfFixedBytes + static_cast<size_t>(units) * 2 * 128 * sizeof(PrefillStat) +
+    return kPfFixedBytes + static_cast<size_t>(units) * 2 * kCols * sizeof(PrefillStat) +
            (units <= kPfCutUnits ? static_cast<size_t>(units) * 2 * kPfPartialFloats * sizeof(float) : 0);
 }
 
@@ -515,7 +569,7 @@ int prefill_mfma_launch(const float * q, int32_t q_stride, const void * k, const
     // workspace holds the partial outputs; otherwise every tile is one item.
     const int n_kt_last = (n_past + n_tokens + kBK - 1) / kBK;
     const int64_t units = static_cast<int64_t>(p.n_qt) * n_kv;
-    const size_t stats_bytes = static_cast<size_t>(units) * 2 * 128 * sizeof(PrefillStat);
+    const size_t stats_bytes = static_cast<size_t>(units) * 2 * kCols * sizeof(PrefillStat);
     if (!workspace || workspace_bytes < kPfFixedBytes + stats_bytes) {
         return fail(QA_ERR_INVALID, "prefill attention: workspace too small (qa_prefill_attn_workspace_bytes)");
     }

@@ -37,6 +37,12 @@ struct DevLayer {
     uint16_t * o16 = nullptr;
     uint16_t * gu16 = nullptr;
     uint16_t * down16 = nullptr;
+    // each bf16 row three times ([N][3 K]), for the prefill GEMMs over the three-part split of their
+    // input (decoders whose capacity allows prefills longer than the skinny GEMM's rows)
+    uint16_t * qkv3 = nullptr;
+    uint16_t * o3 = nullptr;
+    uint16_t * gu3 = nullptr;
+    uint16_t * down3 = nullptr;
 };
 
 enum Kind { kDecode = 0, kPrefill = 1, kNoCache = 2 };
@@ -68,8 +74,8 @@ struct qa_decoder {
     int32_t cap_rows = 0;
     std::vector<void *> act_allocs;
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *qrot = nullptr, *attn = nullptr, *gu = nullptr, *act = nullptr;
-    uint16_t * xsplit = nullptr;   // [3][rows][max in_dim] bf16: three-part split of a GEMM input (bf16 copies)
-    size_t xsplit_elems = 0;       // per part
+    uint16_t * xsplit = nullptr;   // [rows][3 in_dim] bf16: three-part split of a GEMM input (bf16 copies)
+    size_t xsplit_elems = 0;       // a third of its size: rows x max in_dim
     float * logits = nullptr;    // [n_streams][vocab]
     void * attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
@@ -194,7 +200,7 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
         rc = dmalloc(d->act_allocs, n * sizeof(double), reinterpret_cast<void **>(&d->xstats));
     }
     // bf16 copies: longer GEMM inputs are split into three bf16 parts for rocBLAS's bf16 GEMM
-    if (rc == QA_OK && rows > kSkinnyRows && !d->layers.empty() && d->layers[0].qkv16) {
+    if (rc == QA_OK && rows > kSkinnyRows && !d->layers.empty() && d->layers[0].qkv3) {
         d->xsplit_elems = R * std::max({H, QD, I});
         rc = dmalloc_t(d->act_allocs, 3 * d->xsplit_elems, &d->xsplit);
     }
@@ -216,30 +222,29 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
 }
 
 int sgemm(qa_decoder * d, const float * W, int32_t out_dim, int32_t in_dim, const float * X, int32_t rows, float * Y,
-          float beta, const uint16_t * W16 = nullptr) {
+          float beta, const uint16_t * W3 = nullptr) {
     // Y[rows][out] (+)= X[rows][in] * W[out][in]^T.  Up to kSkinnyRows rows (multi-stream decode, short
     // prefills) the weights are streamed once by the skinny MFMA GEMM; longer prefills use rocBLAS.
     if (rows <= kSkinnyRows && in_dim % 32 == 0 && d->gr_ws) {
         return gemm_rows_launch(W, out_dim, in_dim, X, rows, Y, beta != 0.0f, d->gr_ws, d->gr_ws_bytes, d->stream);
     }
-    if (W16 && d->xsplit && static_cast<size_t>(rows) * in_dim <= d->xsplit_elems) {
-        // bf16-exact weights: X = hi + mid + lo exactly (three bf16 parts), Y = W lo + W mid + W hi on rocBLAS's
-        // bf16 GEMM with f32 accumulation -- every product exact, the sums in f32, smallest parts first
-        const size_t n = static_cast<size_t>(rows) * in_dim;
-        uint16_t * part[3] = {d->xsplit, d->xsplit + d->xsplit_elems, d->xsplit + 2 * d->xsplit_elems};
-        int rc = split_bf16x3_launch(X, static_cast<int64_t>(n), part[0], part[1], part[2], d->stream);
-        const float alpha = 1.0f, one = 1.0f;
-        for (int i = 2; i >= 0 && rc == QA_OK; --i) {
-            const float * b = i == 2 ? &beta : &one;
-            const rocblas_status st = rocblas_gemm_ex(
-                d->blas, rocblas_operation_transpose, rocblas_operation_none, out_dim, rows, in_dim, &alpha, W16,
-                rocblas_datatype_bf16_r, in_dim, part[i], rocblas_datatype_bf16_r, in_dim, b, Y, rocblas_datatype_f32_r,
-                out_dim, Y, rocblas_datatype_f32_r, out_dim, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-            if (st != rocblas_status_success) {
-                rc = fail(QA_ERR_DEVICE, std::string("rocblas_gemm_ex (bf16) failed: ") + rocblas_status_to_string(st));
-            }
+    if (W3 && d->xsplit && static_cast<size_t>(rows) * in_dim <= d->xsplit_elems) {
+        // bf16-exact weights: each row of X split into three bf16 parts, X = hi + mid + lo exactly, and
+        // Y = [W W W] [hi; mid; lo]: one rocBLAS bf16 GEMM over 3 in_dim with f32 accumulation -- every
+        // product exact, the sums in f32, Y written once (three GEMMs of in_dim would read and write Y
+        // three times)
+        int rc = split_bf16x3_rows_launch(X, rows, in_dim, d->xsplit, d->stream);
+        if (rc != QA_OK) return rc;
+        const float alpha = 1.0f;
+        const int32_t K3 = 3 * in_dim;
+        const rocblas_status st = rocblas_gemm_ex(
+            d->blas, rocblas_operation_transpose, rocblas_operation_none, out_dim, rows, K3, &alpha, W3,
+            rocblas_datatype_bf16_r, K3, d->xsplit, rocblas_datatype_bf16_r, K3, &beta, Y, rocblas_datatype_f32_r,
+            out_dim, Y, rocblas_datatype_f32_r, out_dim, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+        if (st != rocblas_status_success) {
+            return fail(QA_ERR_DEVICE, std::string("rocblas_gemm_ex (bf16) failed: ") + rocblas_status_to_string(st));
         }
-        return rc;
+        return QA_OK;
     }
     // column-major C(out x rows) = W^T(out x in) * X(in x rows)
     const float alpha = 1.0f;
@@ -309,7 +314,7 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
             rc = fused_gemm(d, L.qkv, W3, H, d->x, rows, d->qkv, false, norm_in(d, L.attn_norm), L.qkv16);
         } else {
             rc = rmsnorm_rows_launch(d->x, L.attn_norm, rows, H, c.rms_norm_eps, d->xn, s);
-            if (rc == QA_OK) rc = sgemm(d, L.qkv, W3, H, d->xn, rows, d->qkv, 0.0f, L.qkv16);
+            if (rc == QA_OK) rc = sgemm(d, L.qkv, W3, H, d->xn, rows, d->qkv, 0.0f, L.qkv3);
         }
         if (rc != QA_OK) return rc;
     }
@@ -357,11 +362,11 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
         if (rc == QA_OK) rc = fused_gemm(d, L.gu, 2 * I, H, d->x, rows, d->act, false, gu, L.gu16);
         if (rc == QA_OK) rc = fused_gemm(d, L.down, H, I, d->act, rows, d->x, true, stats_out(d), L.down16);
     } else {
-        rc = sgemm(d, L.o, H, QD, d->attn, rows, d->x, 1.0f, L.o16);
+        rc = sgemm(d, L.o, H, QD, d->attn, rows, d->x, 1.0f, L.o3);
         if (rc == QA_OK) rc = rmsnorm_rows_launch(d->x, L.ffn_norm, rows, H, c.rms_norm_eps, d->xn, s);
-        if (rc == QA_OK) rc = sgemm(d, L.gu, 2 * I, H, d->xn, rows, d->gu, 0.0f, L.gu16);
+        if (rc == QA_OK) rc = sgemm(d, L.gu, 2 * I, H, d->xn, rows, d->gu, 0.0f, L.gu3);
         if (rc == QA_OK) rc = swiglu_rows_launch(d->gu, rows, I, d->act, s);
-        if (rc == QA_OK) rc = sgemm(d, L.down, H, I, d->act, rows, d->x, 1.0f, L.down16);
+        if (rc == QA_OK) rc = sgemm(d, L.down, H, I, d->act, rows, d->x, 1.0f, L.down3);
     }
     return rc;
 }
@@ -477,10 +482,24 @@ int pack_weights_bf16(qa_decoder * d) {
                         hipStreamSynchronize(d->stream) != hipSuccess)) {
         rc = fail(QA_ERR_DEVICE, "bf16 weight check failed");
     }
+    if (rc == QA_OK && inexact == 0 && d->max_seq > kSkinnyRows) {
+        // prefill GEMMs: each bf16 row three times (see sgemm)
+        auto repeat3 = [&](const uint16_t * src, size_t N, size_t K, uint16_t ** dst) {
+            if (rc != QA_OK) return;
+            rc = dmalloc_t(d->b16_allocs, 3 * N * K, dst);
+            if (rc == QA_OK) rc = repeat3_rows_launch(src, static_cast<int64_t>(N), static_cast<int32_t>(K), *dst, d->stream);
+        };
+        for (DevLayer & L : d->layers) {
+            repeat3(L.qkv16, QD + 2 * KD, H, &L.qkv3);
+            repeat3(L.o16, H, QD, &L.o3);
+            repeat3(L.gu16, 2 * I, H, &L.gu3);
+            repeat3(L.down16, H, I, &L.down3);
+        }
+    }
     if (rc != QA_OK || inexact != 0) {
         for (void * p : d->b16_allocs) (void)hipFree(p);
         d->b16_allocs.clear();
-        for (DevLayer & L : d->layers) L.qkv16 = L.o16 = L.gu16 = L.down16 = nullptr;
+        for (DevLayer & L : d->layers) L.qkv16 = L.o16 = L.gu16 = L.down16 = L.qkv3 = L.o3 = L.gu3 = L.down3 = nullptr;
         d->out_w16 = nullptr;
     }
     return rc;

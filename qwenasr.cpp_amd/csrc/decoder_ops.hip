@@ -1006,30 +1006,57 @@ int gemv_launch(int epi, bool prenorm, const float * W, int32_t out_dim, int32_t
     return prenorm ? launch_gemv_w<kEpiSwiglu, true>(p, b16, stream) : launch_gemv_w<kEpiSwiglu, false>(p, b16, stream);
 }
 
-// hi, mid, lo = the exact three-part bf16 split of x (x = hi + mid + lo: truncations to 8 significant
-// bits, then the same of the remainder; the last remainder has at most 8 significant bits)
-__global__ __launch_bounds__(256) void split_bf16x3_kernel(const float * x, int64_t n, uint16_t * hi, uint16_t * mid,
-                                                           uint16_t * lo) {
+// Row t of out = [hi | mid | lo] of row t of x (rows x K floats): the exact three-part bf16 split,
+// x = hi + mid + lo (truncations to 8 significant bits, then the same of the remainder; the last
+// remainder has at most 8 significant bits).
+__global__ __launch_bounds__(256) void split_bf16x3_rows_kernel(const float * x, int64_t rows, int32_t K,
+                                                                uint16_t * out) {
+    const int64_t n = rows * K;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) {
+        const int64_t t = i / K, k = i - t * K;
         const float v = x[i];
         const uint32_t h = __float_as_uint(v) & 0xffff0000u;
         const float r1 = v - __uint_as_float(h);
         const uint32_t m = __float_as_uint(r1) & 0xffff0000u;
         const float r2 = r1 - __uint_as_float(m);
-        hi[i] = static_cast<uint16_t>(h >> 16);
-        mid[i] = static_cast<uint16_t>(m >> 16);
-        lo[i] = static_cast<uint16_t>(__float_as_uint(r2) >> 16);
+        uint16_t * o = out + t * 3 * K + k;
+        o[0] = static_cast<uint16_t>(h >> 16);
+        o[K] = static_cast<uint16_t>(m >> 16);
+        o[2 * K] = static_cast<uint16_t>(__float_as_uint(r2) >> 16);
     }
 }
 
-int split_bf16x3_launch(const float * x, int64_t n, uint16_t * hi, uint16_t * mid, uint16_t * lo, hipStream_t stream) {
-    if (!x || !hi || !mid || !lo || n < 0) return fail(QA_ERR_INVALID, "split_bf16x3: invalid arguments");
-    if (n == 0) return QA_OK;
-    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
-    hipLaunchKernelGGL(split_bf16x3_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, x, n, hi, mid,
-                       lo);
-    QA_LAUNCH_CHECK("split_bf16x3_kernel");
+int split_bf16x3_rows_launch(const float * x, int64_t rows, int32_t K, uint16_t * out, hipStream_t stream) {
+    if (!x || !out || rows < 0 || K <= 0) return fail(QA_ERR_INVALID, "split_bf16x3_rows: invalid arguments");
+    if (rows == 0) return QA_OK;
+    const int64_t blocks = std::min<int64_t>((rows * K + 255) / 256, 8192);
+    hipLaunchKernelGGL(split_bf16x3_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, x, rows,
+                       K, out);
+    QA_LAUNCH_CHECK("split_bf16x3_rows_kernel");
+    return QA_OK;
+}
+
+// dst row n = [src row n | src row n | src row n] (N rows of K bf16 values)
+__global__ __launch_bounds__(256) void repeat3_rows_kernel(const uint16_t * src, int64_t N, int32_t K, uint16_t * dst) {
+    const int64_t n = N * K;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) {
+        const int64_t r = i / K, k = i - r * K;
+        const uint16_t v = src[i];
+        uint16_t * o = dst + r * 3 * K + k;
+        o[0] = v;
+        o[K] = v;
+        o[2 * K] = v;
+    }
+}
+
+int repeat3_rows_launch(const uint16_t * src, int64_t N, int32_t K, uint16_t * dst, hipStream_t stream) {
+    if (!src || !dst || N < 0 || K <= 0) return fail(QA_ERR_INVALID, "repeat3_rows: invalid arguments");
+    if (N == 0) return QA_OK;
+    const int64_t blocks = std::min<int64_t>((N * K + 255) / 256, 8192);
+    hipLaunchKernelGGL(repeat3_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, src, N, K, dst);
+    QA_LAUNCH_CHECK("repeat3_rows_kernel");
     return QA_OK;
 }
 

@@ -10,8 +10,10 @@ enum { kEpiStoreOp = 0, kEpiAccumOp = 1, kEpiSwigluOp = 2 };
 // W16 (optional): the same weights as bf16 bits, read instead of W when given (bf16-exact weights)
 int gemv_launch(int epi, bool prenorm, const float * W, int32_t out_dim, int32_t in_dim, const float * x, float * y,
                 const float * norm_w, float eps, hipStream_t stream, const uint16_t * W16 = nullptr);
-// the exact three-part bf16 split of n floats: x = hi + mid + lo (each bf16, as bits)
-int split_bf16x3_launch(const float * x, int64_t n, uint16_t * hi, uint16_t * mid, uint16_t * lo, hipStream_t stream);
+// out[t] = [hi | mid | lo] of x[t] (rows x K): the exact three-part bf16 split, x = hi + mid + lo (bf16 bits)
+int split_bf16x3_rows_launch(const float * x, int64_t rows, int32_t K, uint16_t * out, hipStream_t stream);
+// dst[n] = [src[n] | src[n] | src[n]] (N x K bf16 bits)
+int repeat3_rows_launch(const uint16_t * src, int64_t N, int32_t K, uint16_t * dst, hipStream_t stream);
 // dst = high halves of src; *inexact |= 1 if any low half of src is non-zero
 int pack_bf16_launch(const float * src, int64_t n, uint16_t * dst, uint32_t * inexact, hipStream_t stream);
 // Y[rows][N] (+)= X[rows][K] W[N][K]^T for 1..64 rows (K a multiple of 32), f32 MFMA.

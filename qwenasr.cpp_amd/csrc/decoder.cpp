@@ -7,13 +7,16 @@
 //   greedy generate 2209-2311 (prefill, then argmax / stop check / break before the last forward)
 // with the data path replaced by the kernels of this library.
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
 #include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "ops.hpp"
@@ -54,11 +57,24 @@ const char * kFamNames[kFamCount] = {"kv_append", "decode_attn", "prefill_attn",
 
 }  // namespace
 
+// One hipBLASLt GEMM shape of the prefill projections: descriptors and the algorithm the library's
+// heuristic ranks first (a fixed choice per shape, so a prompt's results do not depend on timing).
+struct LtPlan {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+    bool ok = false;
+};
+
 struct qa_decoder {
     qa_text_config cfg{};
     int32_t n_streams = 0, max_seq = 0, cache_type = 0;
     hipStream_t stream = nullptr;
     rocblas_handle blas = nullptr;
+    hipblasLtHandle_t lt = nullptr;           // prefill GEMMs on bf16 copies
+    void * lt_ws = nullptr;
+    size_t lt_ws_bytes = 0;
+    std::map<std::tuple<int32_t, int32_t, int32_t>, LtPlan> lt_plans;   // (M, N, K)
     std::vector<DevLayer> layers;
     float * embd = nullptr;
     float * out_norm = nullptr;
@@ -221,30 +237,62 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
     return QA_OK;
 }
 
+// C[N][M] (column-major M x N) = beta C + A^T B: A = [M][K] and B = [N][K] bf16 rows, f32 accumulation and
+// output, on hipBLASLt with the heuristic's first algorithm for the shape.
+int lt_gemm(qa_decoder * d, int32_t M, int32_t N, int32_t K, const uint16_t * A, const uint16_t * B, float beta, float * C) {
+    LtPlan & pl = d->lt_plans[std::make_tuple(M, N, K)];
+    if (!pl.ok) {
+        const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+        bool ok = hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) == HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) == HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatrixLayoutCreate(&pl.a, HIP_R_16BF, K, M, K) == HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatrixLayoutCreate(&pl.b, HIP_R_16BF, K, N, K) == HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatrixLayoutCreate(&pl.c, HIP_R_32F, M, N, M) == HIPBLAS_STATUS_SUCCESS;
+        hipblasLtMatmulPreference_t pref = nullptr;
+        if (ok) {
+            const uint64_t wsb = d->lt_ws_bytes;
+            ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+                 hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
+                                                       sizeof(wsb)) == HIPBLAS_STATUS_SUCCESS;
+        }
+        if (ok) {
+            hipblasLtMatmulHeuristicResult_t res[1];
+            int got = 0;
+            ok = hipblasLtMatmulAlgoGetHeuristic(d->lt, pl.desc, pl.a, pl.b, pl.c, pl.c, pref, 1, res, &got) ==
+                     HIPBLAS_STATUS_SUCCESS &&
+                 got >= 1 && res[0].state == HIPBLAS_STATUS_SUCCESS && res[0].workspaceSize <= d->lt_ws_bytes;
+            if (ok) pl.algo = res[0].algo;
+        }
+        if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+        if (!ok) {
+            d->lt_plans.erase(std::make_tuple(M, N, K));
+            return fail(QA_ERR_DEVICE, "hipBLASLt: no algorithm for the prefill GEMM");
+        }
+        pl.ok = true;
+    }
+    const float alpha = 1.0f;
+    if (hipblasLtMatmul(d->lt, pl.desc, &alpha, A, pl.a, B, pl.b, &beta, C, pl.c, C, pl.c, &pl.algo, d->lt_ws,
+                        d->lt_ws_bytes, d->stream) != HIPBLAS_STATUS_SUCCESS) {
+        return fail(QA_ERR_DEVICE, "hipblasLtMatmul failed");
+    }
+    return QA_OK;
+}
+
 int sgemm(qa_decoder * d, const float * W, int32_t out_dim, int32_t in_dim, const float * X, int32_t rows, float * Y,
           float beta, const uint16_t * W3 = nullptr) {
     // Y[rows][out] (+)= X[rows][in] * W[out][in]^T.  Up to kSkinnyRows rows (multi-stream decode, short
-    // prefills) the weights are streamed once by the skinny MFMA GEMM; longer prefills use rocBLAS.
+    // prefills) the weights are streamed once by the skinny MFMA GEMM; longer prefills use hipBLASLt on
+    // the bf16 copies, or rocBLAS sgemm on f32 weights.
     if (rows <= kSkinnyRows && in_dim % 32 == 0 && d->gr_ws) {
         return gemm_rows_launch(W, out_dim, in_dim, X, rows, Y, beta != 0.0f, d->gr_ws, d->gr_ws_bytes, d->stream);
     }
-    if (W3 && d->xsplit && static_cast<size_t>(rows) * in_dim <= d->xsplit_elems) {
+    if (W3 && d->lt && d->xsplit && static_cast<size_t>(rows) * in_dim <= d->xsplit_elems) {
         // bf16-exact weights: each row of X split into three bf16 parts, X = hi + mid + lo exactly, and
-        // Y = [W W W] [hi; mid; lo]: one rocBLAS bf16 GEMM over 3 in_dim with f32 accumulation -- every
-        // product exact, the sums in f32, Y written once (three GEMMs of in_dim would read and write Y
-        // three times)
-        int rc = split_bf16x3_rows_launch(X, rows, in_dim, d->xsplit, d->stream);
-        if (rc != QA_OK) return rc;
-        const float alpha = 1.0f;
-        const int32_t K3 = 3 * in_dim;
-        const rocblas_status st = rocblas_gemm_ex(
-            d->blas, rocblas_operation_transpose, rocblas_operation_none, out_dim, rows, K3, &alpha, W3,
-            rocblas_datatype_bf16_r, K3, d->xsplit, rocblas_datatype_bf16_r, K3, &beta, Y, rocblas_datatype_f32_r,
-            out_dim, Y, rocblas_datatype_f32_r, out_dim, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-        if (st != rocblas_status_success) {
-            return fail(QA_ERR_DEVICE, std::string("rocblas_gemm_ex (bf16) failed: ") + rocblas_status_to_string(st));
-        }
-        return QA_OK;
+        // Y = [W W W] [hi; mid; lo]: one bf16 GEMM over 3 in_dim with f32 accumulation -- every product
+        // exact, the sums in f32, Y written once (three GEMMs of in_dim would read and write Y three times)
+        const int rc = split_bf16x3_rows_launch(X, rows, in_dim, d->xsplit, d->stream);
+        return rc != QA_OK ? rc : lt_gemm(d, out_dim, rows, 3 * in_dim, W3, d->xsplit, beta, Y);
     }
     // column-major C(out x rows) = W^T(out x in) * X(in x rows)
     const float alpha = 1.0f;
@@ -592,6 +640,15 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
     }
     if (rc != QA_OK) return bail(rc);
     rc = pack_weights_bf16(d);
+    if (rc == QA_OK && !d->layers.empty() && d->layers[0].qkv3) {
+        // hipBLASLt for the prefill GEMMs over the tripled bf16 rows (its workspace: 64 MiB)
+        d->lt_ws_bytes = size_t(64) << 20;
+        if (hipblasLtCreate(&d->lt) != HIPBLAS_STATUS_SUCCESS) {
+            rc = fail(QA_ERR_DEVICE, "hipBLASLt handle creation failed");
+        } else if (hipMalloc(&d->lt_ws, d->lt_ws_bytes) != hipSuccess) {
+            rc = fail(QA_ERR_ALLOC, "hipBLASLt workspace allocation failed");
+        }
+    }
     if (rc != QA_OK) return bail(rc);
 
     d->layout.n_layers = cfg->n_layers;
@@ -642,6 +699,14 @@ extern "C" void qa_decoder_destroy(qa_decoder * d) {
     if (d->cache) (void)hipFree(d->cache);
     if (d->h_ids) (void)hipHostFree(d->h_ids);
     if (d->blas) rocblas_destroy_handle(d->blas);
+    for (auto & kv : d->lt_plans) {
+        if (kv.second.a) hipblasLtMatrixLayoutDestroy(kv.second.a);
+        if (kv.second.b) hipblasLtMatrixLayoutDestroy(kv.second.b);
+        if (kv.second.c) hipblasLtMatrixLayoutDestroy(kv.second.c);
+        if (kv.second.desc) hipblasLtMatmulDescDestroy(kv.second.desc);
+    }
+    if (d->lt) hipblasLtDestroy(d->lt);
+    if (d->lt_ws) (void)hipFree(d->lt_ws);
     if (d->stream) (void)hipStreamDestroy(d->stream);
     delete d;
 }

@@ -1008,32 +1008,37 @@ int gemv_launch(int epi, bool prenorm, const float * W, int32_t out_dim, int32_t
 
 // Row t of out = [hi | mid | lo] of row t of x (rows x K floats): the exact three-part bf16 split,
 // x = hi + mid + lo (truncations to 8 significant bits, then the same of the remainder; the last
-// remainder has at most 8 significant bits).
-__global__ __launch_bounds__(256) void split_bf16x3_rows_kernel(const float * x, int64_t rows, int32_t K,
-                                                                uint16_t * out) {
-    const int64_t n = rows * K;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) {
-        const int64_t t = i / K, k = i - t * K;
-        const float v = x[i];
-        const uint32_t h = __float_as_uint(v) & 0xffff0000u;
-        const float r1 = v - __uint_as_float(h);
-        const uint32_t m = __float_as_uint(r1) & 0xffff0000u;
-        const float r2 = r1 - __uint_as_float(m);
-        uint16_t * o = out + t * 3 * K + k;
-        o[0] = static_cast<uint16_t>(h >> 16);
-        o[K] = static_cast<uint16_t>(m >> 16);
-        o[2 * K] = static_cast<uint16_t>(__float_as_uint(r2) >> 16);
-    }
+// remainder has at most 8 significant bits).  blockIdx.y = row, 4 consecutive elements per thread.
+__device__ inline uint32_t split3_pair(float a, float b, uint32_t & mid, uint32_t & lo) {
+    const uint32_t ha = __float_as_uint(a) & 0xffff0000u, hb = __float_as_uint(b) & 0xffff0000u;
+    const float ra = a - __uint_as_float(ha), rb = b - __uint_as_float(hb);
+    const uint32_t ma = __float_as_uint(ra) & 0xffff0000u, mb = __float_as_uint(rb) & 0xffff0000u;
+    const float qa = ra - __uint_as_float(ma), qb = rb - __uint_as_float(mb);
+    mid = (ma >> 16) | mb;
+    lo = (__float_as_uint(qa) >> 16) | (__float_as_uint(qb) & 0xffff0000u);
+    return (ha >> 16) | hb;
+}
+
+__global__ __launch_bounds__(256) void split_bf16x3_rows_kernel(const float * x, int32_t K, uint16_t * out) {
+    const int k = (static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x)) * 4;
+    if (k >= K) return;
+    const int64_t t = blockIdx.y;
+    const float4 v = *reinterpret_cast<const float4 *>(x + t * K + k);
+    uint32_t m0, m1, l0, l1;
+    const uint32_t h0 = split3_pair(v.x, v.y, m0, l0), h1 = split3_pair(v.z, v.w, m1, l1);
+    uint16_t * o = out + t * 3 * K + k;
+    *reinterpret_cast<uint2 *>(o) = make_uint2(h0, h1);
+    *reinterpret_cast<uint2 *>(o + K) = make_uint2(m0, m1);
+    *reinterpret_cast<uint2 *>(o + 2 * K) = make_uint2(l0, l1);
 }
 
 int split_bf16x3_rows_launch(const float * x, int64_t rows, int32_t K, uint16_t * out, hipStream_t stream) {
-    if (!x || !out || rows < 0 || K <= 0) return fail(QA_ERR_INVALID, "split_bf16x3_rows: invalid arguments");
-    if (rows == 0) return QA_OK;
-    const int64_t blocks = std::min<int64_t>((rows * K + 255) / 256, 8192);
-    hipLaunchKernelGGL(split_bf16x3_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, x, rows,
-                       K, out);
-    QA_LAUNCH_CHECK("split_bf16x3_rows_kernel");
+    if (!x || !out || rows < 0 || K <= 0 || K % 4 != 0) return fail(QA_ERR_INVALID, "split_bf16x3_rows: invalid arguments");
+    for (int64_t r0 = 0; r0 < rows; r0 += 65535) {     // grid.y <= 65535 rows per launch
+        const dim3 grid(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(std::min<int64_t>(rows - r0, 65535)));
+        hipLaunchKernelGGL(split_bf16x3_rows_kernel, grid, dim3(256), 0, stream, x + r0 * K, K, out + r0 * 3 * K);
+        QA_LAUNCH_CHECK("split_bf16x3_rows_kernel");
+    }
     return QA_OK;
 }
 

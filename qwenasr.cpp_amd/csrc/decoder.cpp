@@ -239,8 +239,23 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
 
 // C[N][M] (column-major M x N) = beta C + A^T B: A = [M][K] and B = [N][K] bf16 rows, f32 accumulation and
 // output, on hipBLASLt with the heuristic's first algorithm for the shape.
+void lt_free(LtPlan & pl) {
+    if (pl.a) hipblasLtMatrixLayoutDestroy(pl.a);
+    if (pl.b) hipblasLtMatrixLayoutDestroy(pl.b);
+    if (pl.c) hipblasLtMatrixLayoutDestroy(pl.c);
+    if (pl.desc) hipblasLtMatmulDescDestroy(pl.desc);
+    pl = LtPlan{};
+}
+
 int lt_gemm(qa_decoder * d, int32_t M, int32_t N, int32_t K, const uint16_t * A, const uint16_t * B, float beta, float * C) {
-    LtPlan & pl = d->lt_plans[std::make_tuple(M, N, K)];
+    // N is the prompt length: a serving loop meets many, so the plans are dropped once 256 have piled up
+    // (a plan holds host-side descriptors only; the calls that used them were enqueued with their values)
+    const auto key = std::make_tuple(M, N, K);
+    if (d->lt_plans.size() >= 256 && d->lt_plans.find(key) == d->lt_plans.end()) {
+        for (auto & kv : d->lt_plans) lt_free(kv.second);
+        d->lt_plans.clear();
+    }
+    LtPlan & pl = d->lt_plans[key];
     if (!pl.ok) {
         const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
         bool ok = hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
@@ -266,7 +281,8 @@ int lt_gemm(qa_decoder * d, int32_t M, int32_t N, int32_t K, const uint16_t * A,
         }
         if (pref) hipblasLtMatmulPreferenceDestroy(pref);
         if (!ok) {
-            d->lt_plans.erase(std::make_tuple(M, N, K));
+            lt_free(pl);
+            d->lt_plans.erase(key);
             return fail(QA_ERR_DEVICE, "hipBLASLt: no algorithm for the prefill GEMM");
         }
         pl.ok = true;
@@ -699,12 +715,7 @@ extern "C" void qa_decoder_destroy(qa_decoder * d) {
     if (d->cache) (void)hipFree(d->cache);
     if (d->h_ids) (void)hipHostFree(d->h_ids);
     if (d->blas) rocblas_destroy_handle(d->blas);
-    for (auto & kv : d->lt_plans) {
-        if (kv.second.a) hipblasLtMatrixLayoutDestroy(kv.second.a);
-        if (kv.second.b) hipblasLtMatrixLayoutDestroy(kv.second.b);
-        if (kv.second.c) hipblasLtMatrixLayoutDestroy(kv.second.c);
-        if (kv.second.desc) hipblasLtMatmulDescDestroy(kv.second.desc);
-    }
+    for (auto & kv : d->lt_plans) lt_free(kv.second);
     if (d->lt) hipblasLtDestroy(d->lt);
     if (d->lt_ws) (void)hipFree(d->lt_ws);
     if (d->stream) (void)hipStreamDestroy(d->stream);

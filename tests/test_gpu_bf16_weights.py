@@ -260,9 +260,10 @@ def test_bf16_weights_multistream_equals_f32_weights_and_oracle(qa, orc, greedy,
 
 
 def test_bf16_weights_long_prefill_matches_oracle(qa, orc, greedy):
-    """A 300-position prompt (longer than the 64 rows of the skinny GEMM): with bf16 copies the prefill's
-    projections run as three rocBLAS bf16 GEMMs over the exact three-part split of their inputs (exact
-    products, f32 sums).  Logits against the oracle and against the f32-weight decoder, then greedy ids."""
+    """A 300-position prompt (longer than the 64 rows of the skinny GEMM): with bf16 copies each prefill
+    projection is one hipBLASLt bf16 GEMM over the exact three-part split of its input against the tripled
+    weight rows (exact products, f32 sums).  Logits against the oracle and against the f32-weight decoder,
+    then greedy ids."""
     model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=3, bf16=True)
     om = orc.OracleModel.from_product_model(model)
     x = qa.prompt_input(model, 290, 10)
@@ -283,3 +284,23 @@ def test_bf16_weights_long_prefill_matches_oracle(qa, orc, greedy):
     assert float(np.abs(logits[False].astype(np.float64) - logits[True]).max()) <= 2e-3
     assert greedy.match(out["ids"], ref["ids"], ref["margins"], ref["runner_up"],
                         "bf16-exact weights, 300-position prompt") is None
+
+
+def test_bf16_prefill_many_prompt_lengths(qa, orc):
+    """More distinct prompt lengths than the decoder keeps GEMM plans for (256; one per length): every
+    prefill of lengths 65..334 runs, and the last-row logits of lengths before and after the plans are
+    dropped match the oracle's at the prefill tolerance."""
+    model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=1, bf16=True)
+    om = orc.OracleModel.from_product_model(model)
+    x_all = qa.prompt_input(model, 324, 10)
+    checked = (65, 200, 320, 334)
+    with _decoder(qa, model, 340, False) as dec:
+        assert dec.weights_bf16
+        for T in range(65, 335):
+            logits = dec.forward(x_all[:T], 0)
+            if T in checked:
+                print(f"prefill length {T}", flush=True)
+                ref = om.forward_cached(x_all[:T], 0, om.cache(340, True))
+                err = float(np.abs(logits.astype(np.float64) - ref).max())
+                rel = float(np.linalg.norm(logits - ref) / np.linalg.norm(ref))
+                assert err <= 2e-3 and rel <= 1e-3, (T, err, rel)

@@ -215,7 +215,7 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
         const size_t n = static_cast<size_t>((H + 31) / 32) * 32;
         rc = dmalloc(d->act_allocs, n * sizeof(double), reinterpret_cast<void **>(&d->xstats));
     }
-    // bf16 copies: longer GEMM inputs are split into three bf16 parts for rocBLAS's bf16 GEMM
+    // bf16 copies: longer GEMM inputs are split into three bf16 parts ([rows][3 in_dim]) for the bf16 GEMM
     if (rc == QA_OK && rows > kSkinnyRows && !d->layers.empty() && d->layers[0].qkv3) {
         d->xsplit_elems = R * std::max({H, QD, I});
         rc = dmalloc_t(d->act_allocs, 3 * d->xsplit_elems, &d->xsplit);
@@ -295,19 +295,32 @@ int lt_gemm(qa_decoder * d, int32_t M, int32_t N, int32_t K, const uint16_t * A,
     return QA_OK;
 }
 
+bool skinny_path(const qa_decoder * d, int32_t rows, int32_t in_dim) {
+    return rows <= kSkinnyRows && in_dim % 32 == 0 && d->gr_ws;
+}
+
+// Whether sgemm runs the bf16 GEMM over the three-part split of its input (then the producer of the
+// input may write d->xsplit itself, see sgemm's x_split).
+bool split_path(const qa_decoder * d, int32_t rows, int32_t in_dim, const uint16_t * W3) {
+    return !skinny_path(d, rows, in_dim) && W3 && d->lt && d->xsplit &&
+           static_cast<size_t>(rows) * in_dim <= d->xsplit_elems;
+}
+
 int sgemm(qa_decoder * d, const float * W, int32_t out_dim, int32_t in_dim, const float * X, int32_t rows, float * Y,
-          float beta, const uint16_t * W3 = nullptr) {
+          float beta, const uint16_t * W3 = nullptr, bool x_split = false) {
     // Y[rows][out] (+)= X[rows][in] * W[out][in]^T.  Up to kSkinnyRows rows (multi-stream decode, short
     // prefills) the weights are streamed once by the skinny MFMA GEMM; longer prefills use hipBLASLt on
-    // the bf16 copies, or rocBLAS sgemm on f32 weights.
-    if (rows <= kSkinnyRows && in_dim % 32 == 0 && d->gr_ws) {
+    // the bf16 copies, or rocBLAS sgemm on f32 weights.  x_split: the producer of X already wrote its
+    // three-part split into d->xsplit (only where split_path holds).
+    if (x_split && !split_path(d, rows, in_dim, W3)) return fail(QA_ERR_INVALID, "sgemm: split input without split path");
+    if (skinny_path(d, rows, in_dim)) {
         return gemm_rows_launch(W, out_dim, in_dim, X, rows, Y, beta != 0.0f, d->gr_ws, d->gr_ws_bytes, d->stream);
     }
-    if (W3 && d->lt && d->xsplit && static_cast<size_t>(rows) * in_dim <= d->xsplit_elems) {
+    if (split_path(d, rows, in_dim, W3)) {
         // bf16-exact weights: each row of X split into three bf16 parts, X = hi + mid + lo exactly, and
         // Y = [W W W] [hi; mid; lo]: one bf16 GEMM over 3 in_dim with f32 accumulation -- every product
         // exact, the sums in f32, Y written once (three GEMMs of in_dim would read and write Y three times)
-        const int rc = split_bf16x3_rows_launch(X, rows, in_dim, d->xsplit, d->stream);
+        const int rc = x_split ? QA_OK : split_bf16x3_rows_launch(X, rows, in_dim, d->xsplit, d->stream);
         return rc != QA_OK ? rc : lt_gemm(d, out_dim, rows, 3 * in_dim, W3, d->xsplit, beta, Y);
     }
     // column-major C(out x rows) = W^T(out x in) * X(in x rows)
@@ -377,8 +390,10 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
         } else if (fused) {
             rc = fused_gemm(d, L.qkv, W3, H, d->x, rows, d->qkv, false, norm_in(d, L.attn_norm), L.qkv16);
         } else {
-            rc = rmsnorm_rows_launch(d->x, L.attn_norm, rows, H, c.rms_norm_eps, d->xn, s);
-            if (rc == QA_OK) rc = sgemm(d, L.qkv, W3, H, d->xn, rows, d->qkv, 0.0f, L.qkv3);
+            // the RMSNorm writes the GEMM's split input directly where the GEMM takes one
+            const bool sp = split_path(d, rows, H, L.qkv3);
+            rc = rmsnorm_rows_launch(d->x, L.attn_norm, rows, H, c.rms_norm_eps, d->xn, s, sp ? d->xsplit : nullptr);
+            if (rc == QA_OK) rc = sgemm(d, L.qkv, W3, H, d->xn, rows, d->qkv, 0.0f, L.qkv3, sp);
         }
         if (rc != QA_OK) return rc;
     }
@@ -426,11 +441,12 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
         if (rc == QA_OK) rc = fused_gemm(d, L.gu, 2 * I, H, d->x, rows, d->act, false, gu, L.gu16);
         if (rc == QA_OK) rc = fused_gemm(d, L.down, H, I, d->act, rows, d->x, true, stats_out(d), L.down16);
     } else {
+        const bool sg = split_path(d, rows, H, L.gu3), sd = split_path(d, rows, I, L.down3);
         rc = sgemm(d, L.o, H, QD, d->attn, rows, d->x, 1.0f, L.o3);
-        if (rc == QA_OK) rc = rmsnorm_rows_launch(d->x, L.ffn_norm, rows, H, c.rms_norm_eps, d->xn, s);
-        if (rc == QA_OK) rc = sgemm(d, L.gu, 2 * I, H, d->xn, rows, d->gu, 0.0f, L.gu3);
-        if (rc == QA_OK) rc = swiglu_rows_launch(d->gu, rows, I, d->act, s);
-        if (rc == QA_OK) rc = sgemm(d, L.down, H, I, d->act, rows, d->x, 1.0f, L.down3);
+        if (rc == QA_OK) rc = rmsnorm_rows_launch(d->x, L.ffn_norm, rows, H, c.rms_norm_eps, d->xn, s, sg ? d->xsplit : nullptr);
+        if (rc == QA_OK) rc = sgemm(d, L.gu, 2 * I, H, d->xn, rows, d->gu, 0.0f, L.gu3, sg);
+        if (rc == QA_OK) rc = swiglu_rows_launch(d->gu, rows, I, d->act, s, sd ? d->xsplit : nullptr);
+        if (rc == QA_OK) rc = sgemm(d, L.down, H, I, d->act, rows, d->x, 1.0f, L.down3, sd);
     }
     return rc;
 }

@@ -854,12 +854,26 @@ GemmRowsPlan gemm_rows_plan(int32_t N, int32_t K, int32_t rows, bool one_slice =
 }
 
 // ---------------------------------------------------------------- row RMSNorm (T > 1 paths)
+// The exact three-part bf16 split of v (v = hi + mid + lo: truncations to 8 significant bits, then the
+// same of the remainder; the last remainder has at most 8 significant bits), stored as bf16 bits at
+// o[0], o[K], o[2 K]: the layout of one row of the prefill GEMM's split input.
+__device__ inline void store_split3(uint16_t * o, int64_t K, float v) {
+    const uint32_t h = __float_as_uint(v) & 0xffff0000u;
+    const float r1 = v - __uint_as_float(h);
+    const uint32_t m = __float_as_uint(r1) & 0xffff0000u;
+    const float r2 = r1 - __uint_as_float(m);
+    o[0] = static_cast<uint16_t>(h >> 16);
+    o[K] = static_cast<uint16_t>(m >> 16);
+    o[2 * K] = static_cast<uint16_t>(__float_as_uint(r2) >> 16);
+}
+
+// y = RMSNorm(x) w per row, as f32 rows of y or (split != null) as the three-part split rows of the
+// prefill GEMM's input ([rows][3 dim] bf16 bits)
 __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float * x, const float * w, int dim, float eps,
-                                                           float * y) {
+                                                           float * y, uint16_t * split) {
 #pragma clang fp contract(off)
     const int r = blockIdx.x;
     const float * xr = x + static_cast<int64_t>(r) * dim;
-    float * yr = y + static_cast<int64_t>(r) * dim;
     double ss = 0.0;
     for (int i = threadIdx.x; i < dim; i += 256) ss += static_cast<double>(xr[i]) * xr[i];
     ss = wave_sum_d(ss);
@@ -868,20 +882,27 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float * x, cons
     __syncthreads();
     const double tot = (part[0] + part[1]) + (part[2] + part[3]);
     const float scale = 1.0f / sqrtf(static_cast<float>(tot / static_cast<double>(dim)) + eps);
+    if (split) {
+        uint16_t * sr = split + static_cast<int64_t>(r) * 3 * dim;
+        for (int i = threadIdx.x; i < dim; i += 256) store_split3(sr + i, dim, xr[i] * scale * w[i]);
+        return;
+    }
+    float * yr = y + static_cast<int64_t>(r) * dim;
     for (int i = threadIdx.x; i < dim; i += 256) yr[i] = xr[i] * scale * w[i];
 }
 
-__global__ void swiglu_rows_kernel(const float * gu, int rows, int dim, float * a) {
+// a = silu(gate) up per row (gu rows = [gate | up], dim each), text-decoder.cpp:602; as f32 rows of a or
+// (split != null) as the three-part split rows of the prefill GEMM's input.  blockIdx.y = row.
+__global__ __launch_bounds__(256) void swiglu_rows_kernel(const float * gu, int dim, float * a, uint16_t * split) {
 #pragma clang fp contract(off)
-    const int64_t n = static_cast<int64_t>(rows) * dim;
-    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t r = i / dim;
-        const int64_t c = i - r * dim;
-        const float g = gu[r * 2 * dim + c];
-        const float u = gu[r * 2 * dim + dim + c];
-        a[i] = (g / (1.0f + expf(-g))) * u;
-    }
+    const int c = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+    if (c >= dim) return;
+    const int64_t r = blockIdx.y;
+    const float g = gu[r * 2 * dim + c];
+    const float u = gu[r * 2 * dim + dim + c];
+    const float v = (g / (1.0f + expf(-g))) * u;
+    if (split) store_split3(split + r * 3 * dim + c, dim, v);
+    else a[r * dim + c] = v;
 }
 
 __global__ void add_inplace_kernel(float * y, const float * x, size_t n) {
@@ -1174,21 +1195,23 @@ int argmax_launch(const float * logits, int32_t rows, int32_t vocab, int32_t * i
 }
 
 int rmsnorm_rows_launch(const float * x, const float * w, int32_t rows, int32_t dim, float eps, float * y,
-                        hipStream_t stream) {
+                        hipStream_t stream, uint16_t * split) {
     if (rows <= 0) return QA_OK;
     hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, x, w, dim,
-                       eps, y);
+                       eps, y, split);
     QA_LAUNCH_CHECK("rmsnorm_rows_kernel");
     return QA_OK;
 }
 
-int swiglu_rows_launch(const float * gu, int32_t rows, int32_t dim, float * a, hipStream_t stream) {
-    const int64_t n = static_cast<int64_t>(rows) * dim;
-    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
-    if (blocks <= 0) return QA_OK;
-    hipLaunchKernelGGL(swiglu_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, gu, rows,
-                       dim, a);
-    QA_LAUNCH_CHECK("swiglu_rows_kernel");
+int swiglu_rows_launch(const float * gu, int32_t rows, int32_t dim, float * a, hipStream_t stream, uint16_t * split) {
+    if (rows <= 0 || dim <= 0) return QA_OK;
+    for (int32_t r0 = 0; r0 < rows; r0 += 65535) {     // grid.y <= 65535 rows per launch
+        const dim3 grid(static_cast<unsigned>((dim + 255) / 256), static_cast<unsigned>(std::min(rows - r0, 65535)));
+        const int64_t off = static_cast<int64_t>(r0) * dim;
+        hipLaunchKernelGGL(swiglu_rows_kernel, grid, dim3(256), 0, stream, gu + 2 * off, dim, split ? nullptr : a + off,
+                           split ? split + 3 * off : nullptr);
+        QA_LAUNCH_CHECK("swiglu_rows_kernel");
+    }
     return QA_OK;
 }
 

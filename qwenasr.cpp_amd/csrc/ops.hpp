@@ -40,9 +40,12 @@ int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int
 size_t argmax_workspace_bytes(int32_t rows);
 int argmax_launch(const float * logits, int32_t rows, int32_t vocab, int32_t * ids, void * workspace,
                   hipStream_t stream);
+// split (optional): write the rows as the three-part bf16 split of the prefill GEMM's input ([rows][3 dim],
+// see split_bf16x3_rows_launch) instead of f32 rows of y / a
 int rmsnorm_rows_launch(const float * x, const float * w, int32_t rows, int32_t dim, float eps, float * y,
-                        hipStream_t stream);
-int swiglu_rows_launch(const float * gu, int32_t rows, int32_t dim, float * a, hipStream_t stream);
+                        hipStream_t stream, uint16_t * split = nullptr);
+int swiglu_rows_launch(const float * gu, int32_t rows, int32_t dim, float * a, hipStream_t stream,
+                       uint16_t * split = nullptr);
 // stats (optional, rows <= 32): [ceil(dim / 32)][32] partial sums of squares of each gathered row
 int embed_rows_launch(const float * table, int32_t n_rows, int32_t dim, const int32_t * ids, int32_t rows,
                       float * out, hipStream_t stream, double * stats = nullptr);

@@ -38,9 +38,27 @@ __device__ inline double wave_sum_d(double v) {
     return v;
 }
 
-__device__ inline float wave_sum_f(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+// Sum over the 64 lanes of a wave, complete in lane 63 only, entirely on DPP (VALU, no LDS round
+// trips): quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror and row_mirror leave every lane of
+// each 16-lane row with the row's sum; row_bcast:15 then adds row 0's sum into row 1 and row 2's into
+// row 3, and row_bcast:31 adds rows 0 + 1 into row 3.  Lane 63 ends with (r3 + r2) + (r1 + r0).
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+template <int CTRL, int ROWS>
+__device__ inline float dpp_rows_or_zero(float v) {   // DPP source in the rows of ROWS, 0 in the others
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf, false));
+}
+
+__device__ inline float wave_sum_lane63(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    v += dpp_rows_or_zero<0x142, 0xa>(v);
+    v += dpp_rows_or_zero<0x143, 0xc>(v);
     return v;
 }
 
@@ -93,7 +111,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     f4 wu[NR][IN4];
     u2 bv[NR][IN4];
     u2 bu[NR][IN4];
+    float yv[NR];   // kEpiAccum: the residual rows, loaded with the weights so that the store needs no load
     auto load_rows = [&](int o0) {
+        if constexpr (EPI == kEpiAccum) {
+#pragma unroll
+            for (int r = 0; r < NR; ++r) yv[r] = p.y[min(o0 + r, p.out_dim - 1)];
+        }
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
             const int64_t o = min(o0 + r, p.out_dim - 1);
@@ -173,13 +196,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
         }
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-            const float a = wave_sum_f(acc[r]);
+            const float a = wave_sum_lane63(acc[r]);
             float u = 0.0f;
-            if constexpr (EPI == kEpiSwiglu) u = wave_sum_f(accu[r]);
+            if constexpr (EPI == kEpiSwiglu) u = wave_sum_lane63(accu[r]);
             const int o = o0 + r;
-            if (lane == 0 && o < p.out_dim) {
+            if (lane == kWave - 1 && o < p.out_dim) {
                 if constexpr (EPI == kEpiStore) p.y[o] = a;
-                else if constexpr (EPI == kEpiAccum) p.y[o] += a;
+                else if constexpr (EPI == kEpiAccum) p.y[o] = yv[r] + a;
                 else p.y[o] = (a / (1.0f + expf(-a))) * u;   // silu(gate) * up (text-decoder.cpp:602)
             }
         }

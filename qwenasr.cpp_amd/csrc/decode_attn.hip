@@ -239,39 +239,6 @@ __device__ inline float reduce_scatter16(const float (&in)[N], int part) {
     return v[0];
 }
 
-__device__ inline float wave_max(float v) {
-    v = fmaxf(v, dpp<0xB1>(v));
-    v = fmaxf(v, dpp<0x4E>(v));
-    v = fmaxf(v, dpp<0x141>(v));
-    v = fmaxf(v, dpp<0x140>(v));
-    v = fmaxf(v, __shfl_xor(v, 16, kWave));
-    return fmaxf(v, __shfl_xor(v, 32, kWave));
-}
-
-// A double moved across lanes by DPP as two 32-bit halves.
-template <int CTRL>
-__device__ inline double dpp_d(double v) {
-    const uint64_t u = __double_as_longlong(v);
-    const uint32_t lo = __builtin_amdgcn_mov_dpp(static_cast<int>(static_cast<uint32_t>(u)), CTRL, 0xf, 0xf, false);
-    const uint32_t hi = __builtin_amdgcn_mov_dpp(static_cast<int>(static_cast<uint32_t>(u >> 32)), CTRL, 0xf, 0xf, false);
-    return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
-}
-
-__device__ inline double wave_sum_dpp_d(double v) {
-    v += dpp_d<0xB1>(v);
-    v += dpp_d<0x4E>(v);
-    v += dpp_d<0x141>(v);
-    v += dpp_d<0x140>(v);
-    v += __shfl_xor(v, 16, kWave);
-    return v + __shfl_xor(v, 32, kWave);
-}
-
-__device__ inline float wave_sum(float v) {
-    v = row_sum16(v);
-    v += __shfl_xor(v, 16, kWave);
-    return v + __shfl_xor(v, 32, kWave);
-}
-
 __device__ inline void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 __device__ inline void publish(float * p, float v) {
@@ -440,17 +407,17 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(DecodeParams p,
 
     __shared__ float s_max[kRep][4];
     __shared__ double s_sum[kRep][4];
-    float m0 = wave_max(hh == 0 ? x : -INFINITY);
-    float m1 = wave_max(hh == 1 ? x : -INFINITY);
-    if (lane == 0) { s_max[0][wave] = m0; s_max[1][wave] = m1; }
+    float m0 = wave_max_lane63(hh == 0 ? x : -INFINITY);
+    float m1 = wave_max_lane63(hh == 1 ? x : -INFINITY);
+    if (lane == kWave - 1) { s_max[0][wave] = m0; s_max[1][wave] = m1; }
     __syncthreads();
     m0 = fmaxf(fmaxf(s_max[0][0], s_max[0][1]), fmaxf(s_max[0][2], s_max[0][3]));
     m1 = fmaxf(fmaxf(s_max[1][0], s_max[1][1]), fmaxf(s_max[1][2], s_max[1][3]));
     // sum of expf(x - max) per head: f32 within the wave (at most 32 terms), double across waves
     const float e = valid && primary ? expf(x - (hh ? m1 : m0)) : 0.0f;
-    const float e0 = wave_sum(hh == 0 ? e : 0.0f);
-    const float e1 = wave_sum(hh == 1 ? e : 0.0f);
-    if (lane == 0) { s_sum[0][wave] = e0; s_sum[1][wave] = e1; }
+    const float e0 = wave_sum_lane63(hh == 0 ? e : 0.0f);
+    const float e1 = wave_sum_lane63(hh == 1 ? e : 0.0f);
+    if (lane == kWave - 1) { s_sum[0][wave] = e0; s_sum[1][wave] = e1; }
     __syncthreads();
     if (threadIdx.x < kRep) {
         const int h = threadIdx.x;
@@ -536,8 +503,8 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
         M0 = fmaxf(M0, st0[i].m);
         M1 = fmaxf(M1, st1[i].m);
     }
-    M0 = wave_max(M0);
-    M1 = wave_max(M1);
+    M0 = wave_max_all(M0);
+    M1 = wave_max_all(M1);
     // rescaled chunk sums, accumulated in double (the rescale factor in f32: its rounding is far below
     // the f32 resolution of the final 1 / sum)
     double S0 = 0.0, S1 = 0.0;
@@ -552,8 +519,8 @@ __global__ __launch_bounds__(kThreads) void decode_values_kernel(DecodeParams p)
         S0 += st0[i].s * static_cast<double>(expf(st0[i].m - M0));
         S1 += st1[i].s * static_cast<double>(expf(st1[i].m - M1));
     }
-    S0 = wave_sum_dpp_d(S0);
-    S1 = wave_sum_dpp_d(S1);
+    S0 = wave_sum_d_all(S0);
+    S1 = wave_sum_d_all(S1);
     const float r0 = static_cast<float>(1.0 / S0);
     const float r1 = static_cast<float>(1.0 / S1);
     const bool row_valid = jr < L;

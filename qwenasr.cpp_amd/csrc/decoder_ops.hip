@@ -12,6 +12,7 @@
 // read a bf16 copy (the high halves) and widen each value back to the same f32 in registers: the
 // products and sums are the f32 kernel's, operation for operation, at half the bytes.
 #include "ops.hpp"
+#include "wave.hpp"
 
 #include <algorithm>
 #include <cstdlib>
@@ -32,35 +33,6 @@ struct GemvParams {
     float eps;
 };
 
-__device__ inline double wave_sum_d(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
-}
-
-// Sum over the 64 lanes of a wave, complete in lane 63 only, entirely on DPP (VALU, no LDS round
-// trips): quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror and row_mirror leave every lane of
-// each 16-lane row with the row's sum; row_bcast:15 then adds row 0's sum into row 1 and row 2's into
-// row 3, and row_bcast:31 adds rows 0 + 1 into row 3.  Lane 63 ends with (r3 + r2) + (r1 + r0).
-template <int CTRL>
-__device__ inline float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-
-template <int CTRL, int ROWS>
-__device__ inline float dpp_rows_or_zero(float v) {   // DPP source in the rows of ROWS, 0 in the others
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf, false));
-}
-
-__device__ inline float wave_sum_lane63(float v) {
-    v += dpp_f<0xB1>(v);
-    v += dpp_f<0x4E>(v);
-    v += dpp_f<0x141>(v);
-    v += dpp_f<0x140>(v);
-    v += dpp_rows_or_zero<0x142, 0xa>(v);
-    v += dpp_rows_or_zero<0x143, 0xc>(v);
-    return v;
-}
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
@@ -166,7 +138,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
             ss += static_cast<double>(xv[k].x) * xv[k].x + static_cast<double>(xv[k].y) * xv[k].y +
                   static_cast<double>(xv[k].z) * xv[k].z + static_cast<double>(xv[k].w) * xv[k].w;
         }
-        ss = wave_sum_d(ss);
+        ss = wave_sum_d_all(ss);
         const float scale = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(p.in_dim)) + p.eps);
 #pragma unroll
         for (int k = 0; k < IN4; ++k) {
@@ -899,7 +871,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float * x, cons
     const float * xr = x + static_cast<int64_t>(r) * dim;
     double ss = 0.0;
     for (int i = threadIdx.x; i < dim; i += 256) ss += static_cast<double>(xr[i]) * xr[i];
-    ss = wave_sum_d(ss);
+    ss = wave_sum_d_all(ss);
     __shared__ double part[4];
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
     __syncthreads();

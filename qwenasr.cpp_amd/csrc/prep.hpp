@@ -10,14 +10,9 @@
 #pragma once
 
 #include "common.hpp"
+#include "wave.hpp"
 
 namespace qa {
-
-__device__ inline double wave_sum_d(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
-}
 
 // cos and sin of the RoPE angle pos * inv_freq, evaluated in double and rounded to f32 (the
 // reference's apply_rope_position, text-decoder.cpp:604-625).
@@ -33,7 +28,7 @@ __device__ inline void rope_cos_sin(int pos, double inv_freq, float & c, float &
 // every load of its prologue before the first use and share one angle evaluation between heads).
 __device__ inline void norm_rope_pair_cs(float & a, float & b, float wa, float wb, float eps, float c, float s) {
 #pragma clang fp contract(off)
-    const double ss = wave_sum_d(static_cast<double>(a) * a + static_cast<double>(b) * b);
+    const double ss = wave_sum_d_all(static_cast<double>(a) * a + static_cast<double>(b) * b);
     const double ms = ss / static_cast<double>(kHeadDim);
     const float scale = 1.0f / sqrtf(static_cast<float>(ms) + eps);
     const float na = a * scale * wa;

@@ -72,12 +72,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     const int gw = blockIdx.x * 4 + wave;
     const int nw = gridDim.x * 4;
     const int64_t in = p.in_dim;
-    f4 xv[IN4], nv[IN4];
+    // PRENORM: x is normalised once per workgroup and shared through LDS.  Wave w loads and normalises
+    // the steps k = w QK .. w QK + QK - 1 of x and the norm weight (a quarter each), instead of every
+    // wave loading all of both (16 KB per wave at in_dim 2048, twice its weight rows).
+    constexpr int QK = PRENORM ? IN4 / 4 : IN4;
+    static_assert(!PRENORM || IN4 % 4 == 0, "PRENORM needs in_dim a multiple of 1024");
+    const int k0 = PRENORM ? wave * QK : 0;
+    f4 xv[IN4], nv[QK];
 #pragma unroll
-    for (int k = 0; k < IN4; ++k) xv[k] = *reinterpret_cast<const f4 *>(p.x + k * 256 + lane * 4);
+    for (int k = 0; k < QK; ++k) xv[k] = *reinterpret_cast<const f4 *>(p.x + (k0 + k) * 256 + lane * 4);
     if (PRENORM) {
 #pragma unroll
-        for (int k = 0; k < IN4; ++k) nv[k] = *reinterpret_cast<const f4 *>(p.norm_w + k * 256 + lane * 4);
+        for (int k = 0; k < QK; ++k) nv[k] = *reinterpret_cast<const f4 *>(p.norm_w + (k0 + k) * 256 + lane * 4);
     }
     f4 wv[NR][IN4];
     f4 wu[NR][IN4];
@@ -122,31 +128,44 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
         }
     };
     int o0 = gw * NR;
-    if (o0 >= p.out_dim) return;
+    // PRENORM: every wave takes part in the staging barriers; a wave past the last row loads the last
+    // row's weights (load_rows clamps) and stores nothing
+    if (!PRENORM && o0 >= p.out_dim) return;
     asm volatile("" ::: "memory");   // x and the norm weight are issued before the weight rows
     load_rows(o0);
     // every load above is issued before the norm arithmetic: the empty asm orders the loads before it
     // (memory clobber) and the arithmetic after it (it redefines x), otherwise the scheduler hoists the
     // reduction, and its wait for x, above the weight loads
 #pragma unroll
-    for (int k = 0; k < IN4; ++k) asm volatile("" : "+v"(xv[k]) : : "memory");
-    if (PRENORM) {
-        // rms_norm_row (text-decoder.cpp:542-557): squares in double, float scale, (x * scale) * w
+    for (int k = 0; k < QK; ++k) asm volatile("" : "+v"(xv[k]) : : "memory");
+    if constexpr (PRENORM) {
+        // rms_norm_row (text-decoder.cpp:542-557): squares in double, float scale, (x * scale) * w; the
+        // squares are summed per wave quarter in double, the four quarters in a fixed order
+        __shared__ double s_ss[4];
+        __shared__ f4 s_x[IN4 * kWave];
         double ss = 0.0;
 #pragma unroll
-        for (int k = 0; k < IN4; ++k) {
+        for (int k = 0; k < QK; ++k) {
             ss += static_cast<double>(xv[k].x) * xv[k].x + static_cast<double>(xv[k].y) * xv[k].y +
                   static_cast<double>(xv[k].z) * xv[k].z + static_cast<double>(xv[k].w) * xv[k].w;
         }
-        ss = wave_sum_d_all(ss);
-        const float scale = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(p.in_dim)) + p.eps);
+        ss = wave_sum_d_lane63(ss);
+        if (lane == kWave - 1) s_ss[wave] = ss;
+        __syncthreads();
+        const double tot = (s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]);
+        const float scale = 1.0f / sqrtf(static_cast<float>(tot / static_cast<double>(p.in_dim)) + p.eps);
 #pragma unroll
-        for (int k = 0; k < IN4; ++k) {
-            xv[k].x = xv[k].x * scale * nv[k].x;
-            xv[k].y = xv[k].y * scale * nv[k].y;
-            xv[k].z = xv[k].z * scale * nv[k].z;
-            xv[k].w = xv[k].w * scale * nv[k].w;
+        for (int k = 0; k < QK; ++k) {
+            f4 v;
+            v.x = xv[k].x * scale * nv[k].x;
+            v.y = xv[k].y * scale * nv[k].y;
+            v.z = xv[k].z * scale * nv[k].z;
+            v.w = xv[k].w * scale * nv[k].w;
+            s_x[(k0 + k) * kWave + lane] = v;
         }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < IN4; ++k) xv[k] = s_x[k * kWave + lane];
     }
     for (;;) {
         float acc[NR];

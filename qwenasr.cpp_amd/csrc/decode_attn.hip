@@ -192,18 +192,6 @@ __device__ inline float dpp(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
-// Sum over the 16 lanes that hold one row (lane bits 0-3): quad_perm [1,0,3,2] and [2,3,0,1] pair the
-// lanes of each quad, row_half_mirror pairs the two quads of each half row, row_mirror the two halves.
-// Every step adds two partial sums in both lanes (a + b == b + a), so all 16 lanes end with the same
-// bits.
-__device__ inline float row_sum16(float v) {
-    v += dpp<0xB1>(v);      // quad_perm [1,0,3,2]
-    v += dpp<0x4E>(v);      // quad_perm [2,3,0,1]
-    v += dpp<0x141>(v);     // row_half_mirror
-    v += dpp<0x140>(v);     // row_mirror
-    return v;
-}
-
 // One reduce-scatter stage over the lane pairs of DPP pattern CTRL (an XOR of the lane index within
 // 16 whose top set bit is BIT): of the N live values the lane keeps the half selected by its own BIT
 // and adds the partner's copy of that half; with N == 1 the stage is a plain butterfly add.

@@ -104,6 +104,7 @@ struct qa_decoder {
     double * xstats = nullptr;   // [hidden / 32][32] partial sums of squares of the rows of x (fused steps)
     int32_t * d_ids = nullptr;
     int32_t * h_ids = nullptr;   // pinned
+    int32_t * h_ids_dev = nullptr;   // the same memory as the device addresses it
     float * staging = nullptr;
     size_t staging_bytes = 0;
     float scale = 0.0f;
@@ -452,7 +453,8 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
 }
 
 // Logits of `rows` rows starting at row `first` of d->x into d->logits[0..rows), then greedy ids.
-int logits_and_pick(qa_decoder * d, int32_t first, int32_t rows, bool pick, bool fused = false) {
+int logits_and_pick(qa_decoder * d, int32_t first, int32_t rows, bool pick, bool fused = false,
+                    const StepTail & tail = StepTail{}) {
     const qa_text_config & c = d->cfg;
     if (!d->out_w || !d->out_norm) return fail(QA_ERR_INVALID, "decoder has no output weights");
     int rc;
@@ -472,7 +474,7 @@ int logits_and_pick(qa_decoder * d, int32_t first, int32_t rows, bool pick, bool
         if (rc != QA_OK) return rc;
     }
     if (!pick) return QA_OK;
-    return argmax_launch(d->logits, rows, c.vocab, d->d_ids, d->am_ws, d->stream);
+    return argmax_launch(d->logits, rows, c.vocab, d->d_ids, d->am_ws, d->stream, tail);
 }
 
 int check_forward(const qa_decoder * d, int32_t n_tokens, int32_t n_past) {
@@ -500,26 +502,38 @@ int forward_device(qa_decoder * d, int32_t n_tokens, int32_t n_past, bool pick) 
     return rc;
 }
 
-// One decode step of `rows` streams with the token ids already in d_ids: embedding gather, every
-// layer (fused append + attention at position d_lens[s]), LM head, greedy pick into d_ids, and
-// d_lens[s] += 1.  Only device memory is read for lengths and ids, so the sequence is capturable.
-int decode_step_ops(qa_decoder * d, int32_t rows, int32_t max_len) {
+// One decode step of `rows` streams with the token ids already in d_ids: embedding gather (unless the
+// previous step's pick already left the rows in d->x: embed = false), every layer (fused append +
+// attention at position d_lens[s]), LM head, and the pick, whose kernel also advances d_lens[s], writes
+// the ids to host_ids (device-visible pinned memory, optional) and gathers the next step's embedding
+// rows into d->x.  Only device memory is read for lengths and ids, so the sequence is capturable.
+int decode_step_ops(qa_decoder * d, int32_t rows, int32_t max_len, bool embed, int32_t * host_ids) {
     const bool fused = fused_rows(d, rows);
-    int rc = embed_rows_launch(d->embd, d->cfg.vocab, d->cfg.hidden, d->d_ids, rows, d->x, d->stream,
+    int rc = QA_OK;
+    if (embed) {
+        rc = embed_rows_launch(d->embd, d->cfg.vocab, d->cfg.hidden, d->d_ids, rows, d->x, d->stream,
                                fused ? d->xstats : nullptr);
+    }
     for (int32_t l = 0; l < d->cfg.n_layers && rc == QA_OK; ++l) {
         rc = run_layer(d, l, rows, kDecode, 0, max_len, fused);
     }
-    if (rc == QA_OK) rc = logits_and_pick(d, 0, rows, true, fused);
-    if (rc == QA_OK) rc = advance_lens_launch(d->d_lens, rows, 1, d->stream);
+    StepTail tail;
+    tail.lens = d->d_lens;
+    tail.host_ids = host_ids;
+    tail.embd = d->embd;
+    tail.x = d->x;
+    tail.stats = fused ? d->xstats : nullptr;
+    tail.dim = d->cfg.hidden;
+    if (rc == QA_OK) rc = logits_and_pick(d, 0, rows, true, fused, tail);
     return rc;
 }
 
 // One decode step launched eagerly.  The step reads lengths and ids from device memory only, so the
 // host does no per-token bookkeeping beyond the launches (the reference rebuilds its graph and uploads
-// a dense mask every token, text-decoder.cpp:1658-1739).
-int decode_step(qa_decoder * d, int32_t rows) {
-    const int rc = decode_step_ops(d, rows, host_max_len(d, rows, 1));
+// a dense mask every token, text-decoder.cpp:1658-1739).  embed: d->x does not hold the embedding rows
+// of d_ids yet (the first step after a prefill or after ids came from the host).
+int decode_step(qa_decoder * d, int32_t rows, bool embed, int32_t * host_ids = nullptr) {
+    const int rc = decode_step_ops(d, rows, host_max_len(d, rows, 1), embed, host_ids);
     if (rc != QA_OK) return rc;
     for (int32_t s = 0; s < rows; ++s) d->cur_len[s] += 1;
     return QA_OK;
@@ -705,6 +719,9 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
         d->h_ids = nullptr;
         return bail(fail(QA_ERR_ALLOC, "pinned host allocation failed"));
     }
+    if (hipHostGetDevicePointer(reinterpret_cast<void **>(&d->h_ids_dev), d->h_ids, 0) != hipSuccess || !d->h_ids_dev) {
+        return bail(fail(QA_ERR_DEVICE, "pinned id buffer has no device address"));
+    }
     // cleared on the decoder's own stream, ahead of every kernel that reads them
     if (hipMemsetAsync(d->d_lens, 0, sizeof(int32_t) * n_streams, d->stream) != hipSuccess ||
         hipMemsetAsync(d->attn_ws, 0, d->attn_ws_bytes, d->stream) != hipSuccess ||
@@ -823,7 +840,7 @@ extern "C" int qa_decoder_generate(qa_decoder * d, const float * x, int32_t n_to
             break;
         }
         if (step + 1 >= max_new) break;
-        rc = decode_step(d, 1);
+        rc = decode_step(d, 1, step == 0);
         if (rc != QA_OK) return rc;
     }
     QA_HIP(hipStreamSynchronize(d->stream));
@@ -847,10 +864,8 @@ extern "C" int qa_decoder_decode_streams(qa_decoder * d, const int32_t * first_i
     if (rc != QA_OK) return rc;
     QA_HIP(hipMemcpyAsync(d->d_ids, first_ids, sizeof(int32_t) * S, hipMemcpyHostToDevice, d->stream));
     for (int32_t k = 0; k < n_steps; ++k) {
-        rc = decode_step(d, S);
+        rc = decode_step(d, S, k == 0, d->h_ids_dev + static_cast<size_t>(k) * S);
         if (rc != QA_OK) return rc;
-        QA_HIP(hipMemcpyAsync(d->h_ids + static_cast<size_t>(k) * S, d->d_ids, sizeof(int32_t) * S,
-                              hipMemcpyDeviceToHost, d->stream));
     }
     QA_HIP(hipStreamSynchronize(d->stream));
     std::memcpy(out_ids, d->h_ids, sizeof(int32_t) * static_cast<size_t>(n_steps) * S);

@@ -1003,7 +1003,7 @@ __device__ inline Cand wave_best(Cand c) {
 }
 
 __global__ __launch_bounds__(256) void argmax_kernel(const float * logits, int vocab, uint64_t * partial,
-                                                     uint32_t * counters, int32_t * ids) {
+                                                     uint32_t * counters, int32_t * ids, StepTail tail) {
     const int row = blockIdx.y;
     const int chunk = (vocab + kArgmaxBlocks - 1) / kArgmaxBlocks;
     const int lo = blockIdx.x * chunk;
@@ -1029,11 +1029,38 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float * logits, int v
         if (is_last) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (!is_last || threadIdx.x >= kArgmaxBlocks) return;
-    Cand b = unpack_cand(__hip_atomic_load(partial + row * kArgmaxBlocks + threadIdx.x, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT));
-    b = wave_best(b);
-    if (threadIdx.x == 0) ids[row] = b.i == kNoIndex ? -1 : b.i;
+    if (!is_last) return;
+    __shared__ int s_id;
+    if (threadIdx.x < kArgmaxBlocks) {
+        Cand b = unpack_cand(__hip_atomic_load(partial + row * kArgmaxBlocks + threadIdx.x, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT));
+        b = wave_best(b);
+        if (threadIdx.x == 0) {
+            const int id = b.i == kNoIndex ? -1 : b.i;
+            ids[row] = id;
+            s_id = id;
+            if (tail.host_ids) tail.host_ids[row] = id;
+            if (tail.lens) tail.lens[row] += 1;
+        }
+    }
+    if (!tail.embd) return;
+    // the next step's input: embed_rows_kernel's gather and row statistics, for the picked id
+    __syncthreads();
+    const int id = s_id;
+    const bool valid = id >= 0 && id < vocab;
+    const float * t = tail.embd + static_cast<int64_t>(valid ? id : 0) * tail.dim;
+    float * o = tail.x + static_cast<int64_t>(row) * tail.dim;
+    for (int i = threadIdx.x; i < tail.dim; i += 256) o[i] = valid ? t[i] : 0.0f;
+    if (tail.stats) {
+        for (int k = threadIdx.x; 32 * k < tail.dim; k += 256) {
+            double ss = 0.0;
+            for (int i = 32 * k; i < min(32 * k + 32, tail.dim); ++i) {
+                const float v = valid ? t[i] : 0.0f;
+                ss += static_cast<double>(v) * v;
+            }
+            tail.stats[32 * k + row] = ss;
+        }
+    }
 }
 
 }  // namespace
@@ -1206,12 +1233,15 @@ size_t argmax_workspace_bytes(int32_t rows) {
 }
 
 int argmax_launch(const float * logits, int32_t rows, int32_t vocab, int32_t * ids, void * workspace,
-                  hipStream_t stream) {
+                  hipStream_t stream, const StepTail & tail) {
     static_assert(sizeof(Cand) == sizeof(uint64_t), "a candidate is published as one 8-byte store");
+    if (tail.embd && (!tail.x || tail.dim <= 0 || (tail.stats && rows > 32))) {
+        return fail(QA_ERR_INVALID, "argmax: invalid embedding gather of the step tail");
+    }
     uint64_t * partial = static_cast<uint64_t *>(workspace);
     uint32_t * counters = reinterpret_cast<uint32_t *>(partial + static_cast<size_t>(rows) * kArgmaxBlocks);
     hipLaunchKernelGGL(argmax_kernel, dim3(kArgmaxBlocks, static_cast<unsigned>(rows)), dim3(256), 0, stream,
-                       logits, vocab, partial, counters, ids);
+                       logits, vocab, partial, counters, ids, tail);
     QA_LAUNCH_CHECK("argmax_kernel");
     return QA_OK;
 }

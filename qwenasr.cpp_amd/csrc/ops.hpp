@@ -38,8 +38,20 @@ int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int
                      void * workspace, size_t workspace_bytes, hipStream_t stream,
                      const GemmRowsFusion * fusion = nullptr, const uint16_t * W16 = nullptr);
 size_t argmax_workspace_bytes(int32_t rows);
+// What the decode step's last kernel does after picking row r's id (each part optional): lens[r] += 1,
+// host_ids[r] = id (a device-visible pointer into pinned host memory), and the picked token's
+// embedding row gathered into x[r] as the next step's input, exactly as embed_rows_launch gathers it
+// (with its 32-column sums of squares in stats when given; rows <= 32 then).
+struct StepTail {
+    int32_t * lens = nullptr;
+    int32_t * host_ids = nullptr;
+    const float * embd = nullptr;
+    float * x = nullptr;
+    double * stats = nullptr;
+    int32_t dim = 0;
+};
 int argmax_launch(const float * logits, int32_t rows, int32_t vocab, int32_t * ids, void * workspace,
-                  hipStream_t stream);
+                  hipStream_t stream, const StepTail & tail = StepTail{});
 // split (optional): write the rows as the three-part bf16 split of the prefill GEMM's input ([rows][3 dim],
 // see split_bf16x3_rows_launch) instead of f32 rows of y / a
 int rmsnorm_rows_launch(const float * x, const float * w, int32_t rows, int32_t dim, float eps, float * y,

@@ -534,24 +534,32 @@ constexpr int kG32LsB = kG32Blk + 8; // LDS row stride of bf16 weight rows (elem
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned int u4v __attribute__((ext_vector_type(4)));
 
-// the hi, mid, lo bf16 parts (x = hi + mid + lo exactly) of 8 floats, packed two per dword
+// The high halves of two dwords packed into one (lo's high half in bits 0-15, hi's in 16-31): one
+// v_perm_b32 (selector bytes 2, 3 of the second source, then 2, 3 of the first).
+__device__ inline uint32_t pack_high_halves(uint32_t lo, uint32_t hi) {
+    return __builtin_amdgcn_perm(hi, lo, 0x07060302u);
+}
+
+// the hi, mid, lo bf16 parts (x = hi + mid + lo exactly) of 8 floats, packed two per dword.  hi and mid
+// are truncations to the top 8 significant bits; the last remainder has at most 8 significant bits, so
+// its own high half is already the part (the packing keeps high halves only).
 __device__ inline void split_bf16x3(const v4f a, const v4f b, u4v & hi, u4v & mid, u4v & lo) {
     float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
     uint32_t h[8], m[8], l[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const uint32_t u = __float_as_uint(x[e]);
-        h[e] = u & 0xffff0000u;
-        const float r1 = x[e] - __uint_as_float(h[e]);
-        m[e] = __float_as_uint(r1) & 0xffff0000u;
-        const float r2 = r1 - __uint_as_float(m[e]);
-        l[e] = __float_as_uint(r2) & 0xffff0000u;
+        h[e] = u;
+        const float r1 = x[e] - __uint_as_float(u & 0xffff0000u);
+        const uint32_t v = __float_as_uint(r1);
+        m[e] = v;
+        l[e] = __float_as_uint(r1 - __uint_as_float(v & 0xffff0000u));
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        hi[j] = (h[2 * j] >> 16) | h[2 * j + 1];
-        mid[j] = (m[2 * j] >> 16) | m[2 * j + 1];
-        lo[j] = (l[2 * j] >> 16) | l[2 * j + 1];
+        hi[j] = pack_high_halves(h[2 * j], h[2 * j + 1]);
+        mid[j] = pack_high_halves(m[2 * j], m[2 * j + 1]);
+        lo[j] = pack_high_halves(l[2 * j], l[2 * j + 1]);
     }
 }
 

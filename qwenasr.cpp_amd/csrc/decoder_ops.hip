@@ -563,19 +563,25 @@ __device__ inline void split_bf16x3(const v4f a, const v4f b, u4v & hi, u4v & mi
     }
 }
 
-template <int P, bool B16>
+// T tiles of 32 weight rows per workgroup (T = 2 with bf16 weights): every X block is loaded, normalised
+// and split into its three bf16 parts once for all T tiles, whose MFMAs then share it.
+template <int P, bool B16, int T>
 __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
 #pragma clang fp contract(off)
-    __shared__ __attribute__((aligned(16))) float lw[4][kG32Rows * kG32Ls];
+    static_assert(T == 1 || (T == 2 && B16), "two tiles per workgroup with bf16 weights only");
+    // per wave: a block of f32 weight rows, or T blocks of bf16 weight rows; then reused for the cross-wave
+    // sums of T accumulator sets (4 waves x 16 entries x 64 lanes x T)
+    constexpr int kLw = kG32Rows * kG32Ls > T * kG32Rows * kG32LsB / 2 ? kG32Rows * kG32Ls : T * kG32Rows * kG32LsB / 2;
+    static_assert(4 * kLw >= 4 * 16 * kWave * T, "LDS for the cross-wave sums");
+    __shared__ __attribute__((aligned(16))) float lw[4][kLw];
     __shared__ __attribute__((aligned(16))) float lx[4][kG32Rows * kG32Ls];
     __shared__ double s_part[8][32];
     __shared__ float s_scale[32];
     __shared__ int s_last;
-    const int tile = static_cast<int>(blockIdx.x) / p.ks;
-    const int sl = static_cast<int>(blockIdx.x) - tile * p.ks;
+    const int grp = static_cast<int>(blockIdx.x) / p.ks;            // tiles T grp .. T grp + T - 1
+    const int sl = static_cast<int>(blockIdx.x) - grp * p.ks;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-    const int row0 = tile * kG32Rows;
     const int k_begin = sl * p.slice;
     const int k_len = min(p.slice, p.K - k_begin);                  // multiple of 64
     const int n_blk = k_len / kG32Blk;
@@ -598,13 +604,14 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
     // gate rows and the 16 matching up rows (W = [gate rows; up rows], N = 2 I).
     const int lr = lane >> 4, lc = 4 * (lane & 15);
     const float * wbase = p.W + k_begin + kG32Blk * wave + lc;
-    // bf16 rows: lane loads 8 elements, row 8 i + lane / 8 (i = 0..3), k 8 (lane % 8) .. + 7
+    // bf16 rows: lane loads 8 elements, row 8 i + lane / 8 (i = 0..3) of each tile, k 8 (lane % 8) .. + 7
     const int lr16 = lane >> 3, lc16 = 8 * (lane & 7);
     const uint16_t * wbase16 = p.W16 + k_begin + kG32Blk * wave + lc16;
     const float * xbase = p.X + k_begin + kG32Blk * wave + lc;
     const float * nbase = prenorm ? p.norm_w + k_begin + kG32Blk * wave + lc : nullptr;
-    auto weight_row = [&](int line) {
-        const int wr_row = p.swiglu ? (line < 16 ? 16 * tile + line : (p.N >> 1) + 16 * tile + line - 16) : row0 + line;
+    auto weight_row = [&](int tile, int line) {
+        const int wr_row = p.swiglu ? (line < 16 ? 16 * tile + line : (p.N >> 1) + 16 * tile + line - 16)
+                                    : tile * kG32Rows + line;
         return static_cast<int64_t>(min(wr_row, p.N - 1)) * p.K;
     };
     int64_t wrow[8];
@@ -612,11 +619,12 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int line = 4 * i + lr;
-        wrow[i] = B16 ? weight_row(8 * (i & 3) + lr16) : weight_row(line);
+        // B16: entry 4 t + j is row 8 j + lane / 8 of tile T grp + t
+        wrow[i] = B16 ? weight_row(T * grp + (i >> 2), 8 * (i & 3) + lr16) : weight_row(grp, line);
         xrow[i] = min(line, p.rows - 1) * p.K;
     }
     v4f wr[P][8], xr[P][8], nw[P];
-    u4v wb[P][4];
+    u4v wb[P][4 * T];
     auto load = [&](int u, int b) {
         const int o = min(b, last) * 4 * kG32Blk;
 #pragma unroll
@@ -624,7 +632,7 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
         if (prenorm) nw[u] = *reinterpret_cast<const v4f *>(nbase + o);
         if constexpr (B16) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) wb[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(wbase16 + wrow[i] + o));
+            for (int i = 0; i < 4 * T; ++i) wb[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(wbase16 + wrow[i] + o));
         } else {
 #pragma unroll
             for (int i = 0; i < 8; ++i) wr[u][i] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(wbase + wrow[i] + o));
@@ -659,7 +667,9 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
     float * myw = lw[wave];
     float * myx = lx[wave];
     const int r = lane & 31, h = lane >> 5;
-    v16f acc0 = {}, acc1 = {};
+    v16f acc0[T], acc1[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) { acc0[t] = v16f{}; acc1[t] = v16f{}; }
     uint16_t * myw16 = reinterpret_cast<uint16_t *>(myw);
     auto compute = [&](int u) {
 #pragma unroll
@@ -674,23 +684,29 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
         }
         if constexpr (B16) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) *reinterpret_cast<u4v *>(myw16 + (8 * i + lr16) * kG32LsB + lc16) = wb[u][i];
+            for (int i = 0; i < 4 * T; ++i) {
+                *reinterpret_cast<u4v *>(myw16 + ((i >> 2) * kG32Rows + 8 * (i & 3) + lr16) * kG32LsB + lc16) = wb[u][i];
+            }
         }
         // the block is read back by other lanes of this wave: LDS operations of a wave complete in order
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if constexpr (B16) {
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                // MFMA step s: k 16 s + 8 h + 0..7 for lane half h (A: weight row r, B: token r)
-                const u4v a = *reinterpret_cast<const u4v *>(myw16 + r * kG32LsB + 16 * s + 8 * h);
+                // MFMA step s: k 16 s + 8 h + 0..7 for lane half h (A: weight row r, B: token r); the split
+                // of X serves the T tiles
                 const v4f x0 = *reinterpret_cast<const v4f *>(myx + r * kG32Ls + 16 * s + 8 * h);
                 const v4f x1 = *reinterpret_cast<const v4f *>(myx + r * kG32Ls + 16 * s + 8 * h + 4);
                 u4v bh, bm, bl;
                 split_bf16x3(x0, x1, bh, bm, bl);
-                const bf16x8 av = __builtin_bit_cast(bf16x8, a);
-                acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bh), acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bm), acc1, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bl), acc1, 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    const u4v a = *reinterpret_cast<const u4v *>(myw16 + (t * kG32Rows + r) * kG32LsB + 16 * s + 8 * h);
+                    const bf16x8 av = __builtin_bit_cast(bf16x8, a);
+                    acc0[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bh), acc0[t], 0, 0, 0);
+                    acc1[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bm), acc1[t], 0, 0, 0);
+                    acc1[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bl), acc1[t], 0, 0, 0);
+                }
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             return;
@@ -705,8 +721,8 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
             const v4f b1 = *reinterpret_cast<const v4f *>(myx + r * kG32Ls + 16 * s + 8 + 4 * h);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], b0[j], acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], b1[j], acc1, 0, 0, 0);
+                acc0[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], b0[j], acc0[0], 0, 0, 0);
+                acc1[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[j], b1[j], acc1[0], 0, 0, 0);
             }
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -730,49 +746,61 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     // sum the 4 waves (wave order) through LDS: accumulator entry i of lane (r, h) is row
-    // 8 (i / 4) + 4 h + i % 4 of token r (32x32 MFMA output layout)
+    // 8 (i / 4) + 4 h + i % 4 of token r (32x32 MFMA output layout); tile t's sums at t 4096
     __syncthreads();
     float * red = &lw[0][0];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) red[(wave * 16 + i) * kWave + lane] = acc0[i] + acc1[i];
-    __syncthreads();
-    auto entry = [&](int i) {
-        float a = red[i * kWave + lane];
+    for (int t = 0; t < T; ++t) {
 #pragma unroll
-        for (int v = 1; v < 4; ++v) a += red[(v * 16 + i) * kWave + lane];
+        for (int i = 0; i < 16; ++i) red[((t * 4 + wave) * 16 + i) * kWave + lane] = acc0[t][i] + acc1[t][i];
+    }
+    __syncthreads();
+    auto entry = [&](int t, int i) {
+        float a = red[(t * 64 + i) * kWave + lane];
+#pragma unroll
+        for (int v = 1; v < 4; ++v) a += red[((t * 4 + v) * 16 + i) * kWave + lane];
         return a;
     };
-    const int t = r;
+    const int tk = r;   // token of this lane's outputs
     if (p.swiglu) {
         // one slice (ks = 1): waves 0 and 1 own gate rows 8 w + 4 h + 0..3 (entries 4 w + j) and their up
-        // rows 16 + 8 w + 4 h + 0..3 (entries 4 w + 8 + j); silu(gate) * up as text-decoder.cpp:602
-        if (wave < 2 && t < p.rows) {
+        // rows 16 + 8 w + 4 h + 0..3 (entries 4 w + 8 + j) of each tile; silu(gate) * up as
+        // text-decoder.cpp:602
+        if (wave < 2 && tk < p.rows) {
             const int I = p.N >> 1;
-            const int c = 16 * tile + 8 * wave + 4 * h;
-            float * y = p.Y + static_cast<int64_t>(t) * I + c;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float g = entry(4 * wave + j), u = entry(4 * wave + 8 + j);
-                if (c + j < I) y[j] = (g / (1.0f + expf(-g))) * u;
+            for (int t = 0; t < T; ++t) {
+                const int c = 16 * (T * grp + t) + 8 * wave + 4 * h;
+                float * y = p.Y + static_cast<int64_t>(tk) * I + c;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float g = entry(t, 4 * wave + j), u = entry(t, 4 * wave + 8 + j);
+                    if (c + j < I) y[j] = (g / (1.0f + expf(-g))) * u;
+                }
             }
         }
         return;
     }
-    // wave w owns entries 4 w .. 4 w + 3: rows 8 w + 4 h + 0..3 of token r
-    v4f s;
+    // wave w owns entries 4 w .. 4 w + 3 of each tile: rows 8 w + 4 h + 0..3 of token r
+    v4f sv[T];
+    int nr[T];
+    bool live[T];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) s[j] = entry(4 * wave + j);
-    const int nr = row0 + 8 * wave + 4 * h;
-    const bool live = t < p.rows && nr < p.N;
-    // store (or accumulate) the final values; with stats_out also the tile's per-token sum of squares of
-    // the stored values (a workgroup-uniform step: every thread of the workgroup calls it)
-    auto finish = [&](v4f v) {
+    for (int t = 0; t < T; ++t) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sv[t][j] = entry(t, 4 * wave + j);
+        nr[t] = (T * grp + t) * kG32Rows + 8 * wave + 4 * h;
+        live[t] = tk < p.rows && nr[t] < p.N;
+    }
+    // store (or accumulate) the final values of tile t; with stats_out also the tile's per-token sum of
+    // squares of the stored values (a workgroup-uniform step: every thread of the workgroup calls it)
+    auto finish = [&](int t, v4f v) {
         double ss = 0.0;
-        if (live) {
-            float * y = p.Y + static_cast<int64_t>(t) * p.N + nr;
+        if (live[t]) {
+            float * y = p.Y + static_cast<int64_t>(tk) * p.N + nr[t];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                if (nr + i < p.N) {
+                if (nr[t] + i < p.N) {
                     const float o = p.accumulate ? y[i] + v[i] : v[i];
                     y[i] = o;
                     ss += static_cast<double>(o) * o;
@@ -781,68 +809,77 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
         }
         if (p.stats_out) {
             double * sst = &s_part[0][0];                           // [4 waves][2 halves][32 tokens]
-            sst[(2 * wave + h) * 32 + t] = ss;
+            sst[(2 * wave + h) * 32 + tk] = ss;
             __syncthreads();
             if (threadIdx.x < 32) {
                 double tot = 0.0;
 #pragma unroll
                 for (int q = 0; q < 8; ++q) tot += sst[q * 32 + threadIdx.x];
-                p.stats_out[32 * tile + threadIdx.x] = tot;
+                p.stats_out[32 * (T * grp + t) + threadIdx.x] = tot;
             }
+            __syncthreads();   // sst is written again by the next tile's step
         }
     };
     if (p.ks == 1) {
-        finish(s);
+#pragma unroll
+        for (int t = 0; t < T; ++t) finish(t, sv[t]);
         return;
     }
-    // publish (partial rows padded to whole 4-row groups), then the last slice of the tile merges in
+    // publish (partial rows padded to whole 4-row groups), then the last slice of the tile group merges in
     // slice order -- the same protocol as gemm_rows_kernel
     const int np = (p.N + 3) / 4 * 4;
-    if (live) {
-        uint64_t * q = reinterpret_cast<uint64_t *>(p.partial + (static_cast<int64_t>(sl) * p.rows + t) * np + nr);
-        const uint64_t lo = static_cast<uint64_t>(__float_as_uint(s[0])) | (static_cast<uint64_t>(__float_as_uint(s[1])) << 32);
-        const uint64_t hi = static_cast<uint64_t>(__float_as_uint(s[2])) | (static_cast<uint64_t>(__float_as_uint(s[3])) << 32);
-        __hip_atomic_store(q, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(q + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        if (live[t]) {
+            uint64_t * q = reinterpret_cast<uint64_t *>(p.partial + (static_cast<int64_t>(sl) * p.rows + tk) * np + nr[t]);
+            const uint64_t lo = static_cast<uint64_t>(__float_as_uint(sv[t][0])) | (static_cast<uint64_t>(__float_as_uint(sv[t][1])) << 32);
+            const uint64_t hi = static_cast<uint64_t>(__float_as_uint(sv[t][2])) | (static_cast<uint64_t>(__float_as_uint(sv[t][3])) << 32);
+            __hip_atomic_store(q, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(q + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t * ctr = p.counters + static_cast<int64_t>(tile) * kGrCounterStride;
+        uint32_t * ctr = p.counters + static_cast<int64_t>(grp) * kGrCounterStride;
         const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = prev == static_cast<uint32_t>(p.ks - 1);
         if (s_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!s_last) return;
-    const int tt = min(t, p.rows - 1);
-    const int nn = min(nr, np - 4);
-    float sum[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < p.ks; k0 += 8) {
-        uint64_t v[8][2];
+    const int tt = min(tk, p.rows - 1);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int k = min(k0 + u, p.ks - 1);
-            const uint64_t * q = reinterpret_cast<const uint64_t *>(p.partial + (static_cast<int64_t>(k) * p.rows + tt) * np + nn);
-            v[u][0] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            v[u][1] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+    for (int t = 0; t < T; ++t) {
+        const int nn = min(nr[t], np - 4);
+        float sum[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int k0 = 0; k0 < p.ks; k0 += 8) {
+            uint64_t v[8][2];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            if (k0 + u >= p.ks) break;
-            sum[0] += __uint_as_float(static_cast<uint32_t>(v[u][0]));
-            sum[1] += __uint_as_float(static_cast<uint32_t>(v[u][0] >> 32));
-            sum[2] += __uint_as_float(static_cast<uint32_t>(v[u][1]));
-            sum[3] += __uint_as_float(static_cast<uint32_t>(v[u][1] >> 32));
+            for (int u = 0; u < 8; ++u) {
+                const int k = min(k0 + u, p.ks - 1);
+                const uint64_t * q = reinterpret_cast<const uint64_t *>(p.partial + (static_cast<int64_t>(k) * p.rows + tt) * np + nn);
+                v[u][0] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                v[u][1] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (k0 + u >= p.ks) break;
+                sum[0] += __uint_as_float(static_cast<uint32_t>(v[u][0]));
+                sum[1] += __uint_as_float(static_cast<uint32_t>(v[u][0] >> 32));
+                sum[2] += __uint_as_float(static_cast<uint32_t>(v[u][1]));
+                sum[3] += __uint_as_float(static_cast<uint32_t>(v[u][1] >> 32));
+            }
         }
+        finish(t, v4f{sum[0], sum[1], sum[2], sum[3]});
     }
-    finish(v4f{sum[0], sum[1], sum[2], sum[3]});
 }
 
 struct GemmRowsPlan {
     int ks, slice, tiles;
     bool rows32;     // gemm_rows32_kernel (else gemm_rows_kernel)
     int depth;       // blocks in flight per wave (gemm_rows32_kernel)
+    int tpw;         // tiles per workgroup (gemm_rows32_kernel: 2 with bf16 weights, an even tile count and > 1024 tiles)
 };
 
 // tuning overrides of the <= 32-row plan: QA_GR32_WGS (workgroup target, default 256) and QA_GR32_DEPTH
@@ -852,22 +889,27 @@ int env_int(const char * name, int fallback) {
     return e ? std::atoi(e) : fallback;
 }
 
-GemmRowsPlan gemm_rows_plan(int32_t N, int32_t K, int32_t rows, bool one_slice = false) {
+GemmRowsPlan gemm_rows_plan(int32_t N, int32_t K, int32_t rows, bool one_slice = false, bool b16 = false) {
     GemmRowsPlan pl{};
     static const int target_wgs = std::max(64, env_int("QA_GR32_WGS", 256));
     static const int forced_depth = env_int("QA_GR32_DEPTH", 0);
+    static const int forced_tpw = env_int("QA_GR32_TPW", 0);
     if (rows <= kG32Rows && K % kG32Blk == 0) {
         // ~256 workgroups at least (one per CU); a K slice keeps >= 4 blocks (one per wave) and at most
-        // 8 slices are merged.  Measured at 32 rows (1.7B shapes): q|k|v 2 slices, o and down 4, gate|up
-        // and the LM head 1.  Two blocks in flight per wave when the grid is one workgroup per CU (the
+        // 8 slices are merged.  Two blocks in flight per wave when the grid is one workgroup per CU (the
         // register file then holds 2 waves per SIMD either way), one when there are more workgroups.
+        // With bf16 weights and more than 1024 tiles (the LM head) a workgroup takes two tiles, which
+        // share each X block and its split (config-4 step: LM head 0.198 -> 0.171 ms); with fewer tiles
+        // the grid would drop below two workgroups per CU (layer projections 1.95 -> 2.40 ms per step).
         pl.rows32 = true;
         pl.tiles = (N + kG32Rows - 1) / kG32Rows;
-        int ks = std::max(1, std::min({(target_wgs + pl.tiles / 2) / pl.tiles, 8, K / (4 * kG32Blk)}));
-        if (pl.tiles > kGrMaxTiles || one_slice) ks = 1;           // counters exist for kGrMaxTiles tiles
+        pl.tpw = b16 && pl.tiles % 2 == 0 && (pl.tiles > 1024 || forced_tpw == 2) && forced_tpw != 1 ? 2 : 1;
+        const int groups = pl.tiles / pl.tpw;
+        int ks = std::max(1, std::min({(target_wgs + groups / 2) / groups, 8, K / (4 * kG32Blk)}));
+        if (groups > kGrMaxTiles || one_slice) ks = 1;             // counters exist for kGrMaxTiles groups
         pl.slice = ((K + ks - 1) / ks + kG32Blk - 1) / kG32Blk * kG32Blk;
         pl.ks = (K + pl.slice - 1) / pl.slice;
-        pl.depth = forced_depth == 1 || forced_depth == 2 ? forced_depth : pl.tiles * pl.ks <= 256 ? 2 : 1;
+        pl.depth = forced_depth == 1 || forced_depth == 2 ? forced_depth : groups * pl.ks <= 256 ? 2 : 1;
         return pl;
     }
     pl.tiles = (N + kGrTile - 1) / kGrTile;
@@ -1154,8 +1196,9 @@ int pack_bf16_launch(const float * src, int64_t n, uint16_t * dst, uint32_t * in
 
 size_t gemm_rows_workspace_bytes(int32_t N, int32_t K, int32_t rows) {
     if (N <= 0 || N > kGrMaxTiles * kGrTile || K <= 0 || rows <= 0 || rows > kGrMaxRows || K % 32 != 0) return 0;
-    const GemmRowsPlan pl = gemm_rows_plan(N, K, rows);
-    const size_t partial = pl.ks > 1 ? static_cast<size_t>(pl.ks) * rows * ((N + 3) / 4 * 4) * sizeof(float) : 0;
+    // the larger of the f32-weight and bf16-weight plans (their slice counts differ)
+    const int ks = std::max(gemm_rows_plan(N, K, rows).ks, gemm_rows_plan(N, K, rows, false, true).ks);
+    const size_t partial = ks > 1 ? static_cast<size_t>(ks) * rows * ((N + 3) / 4 * 4) * sizeof(float) : 0;
     return kGrCounterBytes + partial;
 }
 
@@ -1180,7 +1223,7 @@ int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int
             return fail(QA_ERR_INVALID, "gemm_rows: SwiGLU needs N = 2 I with I % 16 == 0 and a plain store");
         }
     }
-    const GemmRowsPlan pl = gemm_rows_plan(N, K, rows, fused && fusion->swiglu);
+    const GemmRowsPlan pl = gemm_rows_plan(N, K, rows, fused && fusion->swiglu, W16 != nullptr);
     if (!W && !pl.rows32) return fail(QA_ERR_INVALID, "gemm_rows: bf16 weights need rows <= 32 and K % 64 == 0");
     const size_t need = gemm_rows_workspace_bytes(N, K, rows);
     if (!workspace || workspace_bytes < need) return fail(QA_ERR_INVALID, "gemm_rows: workspace too small");
@@ -1209,14 +1252,17 @@ int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int
         p.swiglu = fusion->swiglu ? 1 : 0;
     }
     if (pl.rows32) {
-        const dim3 grid(static_cast<unsigned>(pl.tiles * pl.ks));
+        const dim3 grid(static_cast<unsigned>(pl.tiles / pl.tpw * pl.ks));
         p.W16 = W16;
-        if (W16) {
-            if (pl.depth == 2) hipLaunchKernelGGL((gemm_rows32_kernel<2, true>), grid, dim3(256), 0, stream, p);
-            else hipLaunchKernelGGL((gemm_rows32_kernel<1, true>), grid, dim3(256), 0, stream, p);
+        if (W16 && pl.tpw == 2) {
+            if (pl.depth == 2) hipLaunchKernelGGL((gemm_rows32_kernel<2, true, 2>), grid, dim3(256), 0, stream, p);
+            else hipLaunchKernelGGL((gemm_rows32_kernel<1, true, 2>), grid, dim3(256), 0, stream, p);
+        } else if (W16) {
+            if (pl.depth == 2) hipLaunchKernelGGL((gemm_rows32_kernel<2, true, 1>), grid, dim3(256), 0, stream, p);
+            else hipLaunchKernelGGL((gemm_rows32_kernel<1, true, 1>), grid, dim3(256), 0, stream, p);
         } else {
-            if (pl.depth == 2) hipLaunchKernelGGL((gemm_rows32_kernel<2, false>), grid, dim3(256), 0, stream, p);
-            else hipLaunchKernelGGL((gemm_rows32_kernel<1, false>), grid, dim3(256), 0, stream, p);
+            if (pl.depth == 2) hipLaunchKernelGGL((gemm_rows32_kernel<2, false, 1>), grid, dim3(256), 0, stream, p);
+            else hipLaunchKernelGGL((gemm_rows32_kernel<1, false, 1>), grid, dim3(256), 0, stream, p);
         }
         QA_LAUNCH_CHECK("gemm_rows32_kernel");
         return QA_OK;

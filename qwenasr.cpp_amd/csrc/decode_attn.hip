@@ -383,8 +383,16 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(DecodeParams p,
     // After the reduce-scatter lane `part` of row group `sub` holds the full score of value index
     // part / kDup, i.e. row row0 + 4 kk + sub and head hh; each score is then scaled, stored, and fed
     // to the statistics exactly once (kDup lanes hold a copy when 2 RPT < 16; only the first counts).
-    constexpr int kDup = 16 / (2 * RPT);
-    const float dot = reduce_scatter16<2 * RPT>(vdot, part);
+    // With more than 16 values per lane (RPT > 8) the first 16 are reduced as above and the remaining
+    // NB in a second reduce-scatter, whose scores (value index 16 + part / kDupB) each lane also holds.
+    constexpr int NA = 2 * RPT > 16 ? 16 : 2 * RPT;
+    constexpr int NB = 2 * RPT - NA;
+    static_assert(NB == 0 || NB == 2 || NB == 4 || NB == 8 || NB == 16, "rows per lane: 1, 2, 4, 8, 9, 10, 12 or 16");
+    constexpr int kDup = 16 / NA;
+    float va[NA];
+#pragma unroll
+    for (int i = 0; i < NA; ++i) va[i] = vdot[i];
+    const float dot = reduce_scatter16<NA>(va, part);
     const int idx = part / kDup;
     const int kk = idx >> 1, hh = idx & 1;
     const int j = row0 + kk * 4 + sub;
@@ -392,19 +400,49 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(DecodeParams p,
     const bool primary = part % kDup == 0;
     const float x = valid ? dot * p.scale : -INFINITY;
     if (valid && primary) (hh ? sc1 : sc0)[j] = x;
+    float x2 = -INFINITY;
+    int hh2 = 0;
+    bool use2 = false;
+    if constexpr (NB > 0) {
+        constexpr int kDupB = 16 / NB;
+        float vb[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) vb[i] = vdot[NA + i];
+        const float dot2 = reduce_scatter16<NB>(vb, part);
+        const int idx2 = NA + part / kDupB;
+        hh2 = idx2 & 1;
+        const int j2 = row0 + (idx2 >> 1) * 4 + sub;
+        const bool valid2 = j2 < L;
+        use2 = valid2 && part % kDupB == 0;
+        x2 = valid2 ? dot2 * p.scale : -INFINITY;
+        if (use2) (hh2 ? sc1 : sc0)[j2] = x2;
+    }
 
     __shared__ float s_max[kRep][4];
     __shared__ double s_sum[kRep][4];
-    float m0 = wave_max_lane63(hh == 0 ? x : -INFINITY);
-    float m1 = wave_max_lane63(hh == 1 ? x : -INFINITY);
+    float m0, m1;
+    if constexpr (NB > 0) {
+        m0 = wave_max_lane63(fmaxf(hh == 0 ? x : -INFINITY, hh2 == 0 ? x2 : -INFINITY));
+        m1 = wave_max_lane63(fmaxf(hh == 1 ? x : -INFINITY, hh2 == 1 ? x2 : -INFINITY));
+    } else {
+        m0 = wave_max_lane63(hh == 0 ? x : -INFINITY);
+        m1 = wave_max_lane63(hh == 1 ? x : -INFINITY);
+    }
     if (lane == kWave - 1) { s_max[0][wave] = m0; s_max[1][wave] = m1; }
     __syncthreads();
     m0 = fmaxf(fmaxf(s_max[0][0], s_max[0][1]), fmaxf(s_max[0][2], s_max[0][3]));
     m1 = fmaxf(fmaxf(s_max[1][0], s_max[1][1]), fmaxf(s_max[1][2], s_max[1][3]));
-    // sum of expf(x - max) per head: f32 within the wave (at most 32 terms), double across waves
+    // sum of expf(x - max) per head: f32 within the wave (at most 36 terms), double across waves
     const float e = valid && primary ? expf(x - (hh ? m1 : m0)) : 0.0f;
-    const float e0 = wave_sum_lane63(hh == 0 ? e : 0.0f);
-    const float e1 = wave_sum_lane63(hh == 1 ? e : 0.0f);
+    float e0, e1;
+    if constexpr (NB > 0) {
+        const float f = use2 ? expf(x2 - (hh2 ? m1 : m0)) : 0.0f;
+        e0 = wave_sum_lane63((hh == 0 ? e : 0.0f) + (hh2 == 0 ? f : 0.0f));
+        e1 = wave_sum_lane63((hh == 1 ? e : 0.0f) + (hh2 == 1 ? f : 0.0f));
+    } else {
+        e0 = wave_sum_lane63(hh == 0 ? e : 0.0f);
+        e1 = wave_sum_lane63(hh == 1 ? e : 0.0f);
+    }
     if (lane == kWave - 1) { s_sum[0][wave] = e0; s_sum[1][wave] = e1; }
     __syncthreads();
     if (threadIdx.x < kRep) {
@@ -658,7 +696,7 @@ struct Chunks {
 int env_chunk(const char * name) {
     const char * e = std::getenv(name);
     const int v = e ? std::atoi(e) : 0;
-    return v == 32 || v == 64 || v == 128 || v == 256 ? v : 0;
+    return v == 32 || v == 64 || v == 128 || v == 144 || v == 256 ? v : 0;
 }
 
 Chunks pick_chunks(int32_t n_streams, int32_t n_kv, int32_t capacity) {
@@ -667,7 +705,8 @@ Chunks pick_chunks(int32_t n_streams, int32_t n_kv, int32_t capacity) {
     Chunks ch{};
     // scores: the smallest chunk that keeps the grid at about one workgroup per CU, else 128 (measured
     // at batch 1: 32 is best up to ~1k positions, 64 at 2k, 128 from 4k on, 11.1 vs 12.2 us at 4186;
-    // 128 also for 32 streams)
+    // 128 also for 32 streams).  Where 128-position chunks would put a second workgroup on some CUs
+    // and 144 does not (8 units: capacities 4097 to 4608), 144: those CUs' 64 KB of K set the time.
     const int64_t units = static_cast<int64_t>(n_streams) * n_kv;
     ch.scores = 128;
     for (int c = 32; c < 128; c *= 2) {
@@ -676,11 +715,14 @@ Chunks pick_chunks(int32_t n_streams, int32_t n_kv, int32_t capacity) {
             break;
         }
     }
-    if (forced_s && forced_s <= 128) ch.scores = forced_s;
+    if (ch.scores == 128 && units * ((capacity + 127) / 128) > 256 && units * ((capacity + 143) / 144) <= 256) {
+        ch.scores = 144;
+    }
+    if (forced_s && forced_s <= 144) ch.scores = forced_s;
     int v = 32;
     while (v < 256 && (capacity + v - 1) / v > 16) v *= 2;
     ch.values = forced_v ? forced_v : v;
-    if (ch.values < ch.scores) ch.values = ch.scores;
+    if (ch.values < ch.scores) ch.values = ch.scores == 144 ? 256 : ch.scores;   // values chunks: 32 ... 256
     return ch;
 }
 
@@ -689,6 +731,7 @@ void launch_scores(int chunk, dim3 grid, const DecodeParams & p, const RopeTable
     switch (chunk) {
         case 32: hipLaunchKernelGGL((decode_scores_kernel<CT, R16, 32, FUSED>), grid, dim3(kThreads), 0, stream, p, rope); break;
         case 64: hipLaunchKernelGGL((decode_scores_kernel<CT, R16, 64, FUSED>), grid, dim3(kThreads), 0, stream, p, rope); break;
+        case 144: hipLaunchKernelGGL((decode_scores_kernel<CT, R16, 144, FUSED>), grid, dim3(kThreads), 0, stream, p, rope); break;
         default: hipLaunchKernelGGL((decode_scores_kernel<CT, R16, 128, FUSED>), grid, dim3(kThreads), 0, stream, p, rope); break;
     }
 }

@@ -122,7 +122,8 @@ def _decode(qa, q_dev, cache, lay, layer, lens, max_len, out, ws, ws_bytes):
 
 
 @pytest.mark.parametrize("f16", [True, False])
-@pytest.mark.parametrize("lens", [[1], [2], [63], [64], [65], [157], [1000], [4096], [156, 3913, 700, 1, 2048]])
+@pytest.mark.parametrize("lens", [[1], [2], [63], [64], [65], [157], [1000], [4096], [4186], [4500],
+                                  [156, 3913, 700, 1, 2048]])
 def test_decode_attention(qa, orc, f16, lens):
     S = len(lens)
     max_len = max(lens)
@@ -144,21 +145,24 @@ def test_decode_attention(qa, orc, f16, lens):
 
 
 @pytest.mark.parametrize("f16", [True, False])
-def test_decode_attention_growing_lengths_one_workspace(qa, orc, f16):
+@pytest.mark.parametrize("S", [1, 2])
+def test_decode_attention_growing_lengths_one_workspace(qa, orc, f16, S):
     """One workspace, never cleared between calls, while the prefix grows across chunk boundaries
-    (1 -> many chunks, and 32/64/128-row boundaries): every call must match the oracle, so the
-    merge counters stay where the capacity put them and are left at zero by each call."""
-    S, cap = 2, 4200
+    (1 -> many chunks, and 32/64/128/144-row boundaries; one stream at this capacity takes 144-row
+    scores chunks, two take 128): every call must match the oracle, so the merge counters stay where
+    the capacity put them and are left at zero by each call."""
+    cap = 4200
     lay = layout(qa, 1, S, cap, f16)
     cache = Cache(qa, lay)
     rng = np.random.default_rng(7)
-    vals = cache.fill(rng, 0, [cap, cap])
+    vals = cache.fill(rng, 0, [cap] * S)
     q = rng.standard_normal((S, 16, 128)).astype(np.float32)
     d_q, d_out = dev(qa, q), zeros(qa, (S, 2048))
     ws_bytes = qa.lib.qa_decode_attn_workspace_bytes(S, 16, cap)
     ws = zeros(qa, ws_bytes, np.uint8)
-    for lens in ([1, 3], [31, 33], [32, 64], [65, 63], [127, 129], [130, 1], [1023, 2047], [4096, 4100],
-                 [200, 4200], [5, 6]):
+    for lens2 in ([1, 3], [31, 33], [32, 64], [65, 63], [127, 129], [130, 1], [144, 145], [288, 289], [1023, 2047],
+                  [4096, 4100], [4200, 200], [5, 6]):
+        lens = lens2[:S]
         print(f"decode growing f16={f16} lens={lens}", flush=True)
         got = _decode(qa, d_q, cache, lay, 0, lens, max(lens), d_out, ws, ws_bytes)
         for s, L in enumerate(lens):
@@ -201,7 +205,7 @@ def test_decode_attention_rejects_small_workspace(qa):
 
 
 @pytest.mark.parametrize("f16", [True, False])
-@pytest.mark.parametrize("n_past", [[0], [31], [63], [64], [156], [4095], [156, 3912, 700, 0, 2047, 31]])
+@pytest.mark.parametrize("n_past", [[0], [31], [63], [64], [156], [4095], [4185], [156, 3912, 700, 0, 2047, 31]])
 def test_decode_step_fused_equals_append_then_attend(qa, orc, f16, n_past):
     """qa_decode_step_attn == qa_kv_append + qa_decode_attn at lens = n_past + 1: the whole cache and the
     output bit-exact (new row written, every other row untouched), and the output within the

@@ -563,8 +563,9 @@ __device__ inline void split_bf16x3(const v4f a, const v4f b, u4v & hi, u4v & mi
     }
 }
 
-// T tiles of 32 weight rows per workgroup (T = 2 with bf16 weights): every X block is loaded, normalised
-// and split into its three bf16 parts once for all T tiles, whose MFMAs then share it.
+// T tiles of 32 weight rows per workgroup (T = 2 with bf16 weights and more than 1024 tiles, i.e. the LM
+// head): every X block is loaded, normalised and split into its three bf16 parts once for all T tiles,
+// whose MFMAs then share it.
 template <int P, bool B16, int T>
 __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
 #pragma clang fp contract(off)

@@ -432,7 +432,7 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(DecodeParams p,
     __syncthreads();
     m0 = fmaxf(fmaxf(s_max[0][0], s_max[0][1]), fmaxf(s_max[0][2], s_max[0][3]));
     m1 = fmaxf(fmaxf(s_max[1][0], s_max[1][1]), fmaxf(s_max[1][2], s_max[1][3]));
-    // sum of expf(x - max) per head: f32 within the wave (at most 36 terms), double across waves
+    // sum of expf(x - max) per head: f32 within the wave (at most 64 terms), double across waves
     const float e = valid && primary ? expf(x - (hh ? m1 : m0)) : 0.0f;
     float e0, e1;
     if constexpr (NB > 0) {
@@ -696,7 +696,7 @@ struct Chunks {
 int env_chunk(const char * name) {
     const char * e = std::getenv(name);
     const int v = e ? std::atoi(e) : 0;
-    return v == 32 || v == 64 || v == 128 || v == 144 || v == 256 ? v : 0;
+    return v == 32 || v == 64 || v == 128 || v == 144 || v == 160 || v == 192 || v == 256 ? v : 0;
 }
 
 Chunks pick_chunks(int32_t n_streams, int32_t n_kv, int32_t capacity) {
@@ -706,7 +706,10 @@ Chunks pick_chunks(int32_t n_streams, int32_t n_kv, int32_t capacity) {
     // scores: the smallest chunk that keeps the grid at about one workgroup per CU, else 128 (measured
     // at batch 1: 32 is best up to ~1k positions, 64 at 2k, 128 from 4k on, 11.1 vs 12.2 us at 4186;
     // 128 also for 32 streams).  Where 128-position chunks would put a second workgroup on some CUs
-    // and 144 does not (8 units: capacities 4097 to 4608), 144: those CUs' 64 KB of K set the time.
+    // (8 units: capacities 4097 to 6144), the smallest of 144, 160 and 192 that keeps one workgroup per
+    // CU: the CUs holding two would set the time (measured at batch 1: 10.1 vs 10.5 us at 4186, 10.6 vs
+    // 11.2 at 5000, 10.9 vs 11.4 at 6000).  From 6145 on 128 stays: at 8000 a 256-position chunk (one
+    // workgroup per CU) times the same as 128 (about two on every CU).
     const int64_t units = static_cast<int64_t>(n_streams) * n_kv;
     ch.scores = 128;
     for (int c = 32; c < 128; c *= 2) {
@@ -715,14 +718,19 @@ Chunks pick_chunks(int32_t n_streams, int32_t n_kv, int32_t capacity) {
             break;
         }
     }
-    if (ch.scores == 128 && units * ((capacity + 127) / 128) > 256 && units * ((capacity + 143) / 144) <= 256) {
-        ch.scores = 144;
+    if (ch.scores == 128 && units * ((capacity + 127) / 128) > 256) {
+        for (const int c : {144, 160, 192}) {
+            if (units * ((capacity + c - 1) / c) <= 256) {
+                ch.scores = c;
+                break;
+            }
+        }
     }
-    if (forced_s && forced_s <= 144) ch.scores = forced_s;
+    if (forced_s) ch.scores = forced_s;
     int v = 32;
     while (v < 256 && (capacity + v - 1) / v > 16) v *= 2;
     ch.values = forced_v ? forced_v : v;
-    if (ch.values < ch.scores) ch.values = ch.scores == 144 ? 256 : ch.scores;   // values chunks: 32 ... 256
+    if (ch.values < ch.scores) ch.values = ch.scores > 128 ? 256 : ch.scores;   // values chunks: 32 ... 256
     return ch;
 }
 
@@ -732,6 +740,9 @@ void launch_scores(int chunk, dim3 grid, const DecodeParams & p, const RopeTable
         case 32: hipLaunchKernelGGL((decode_scores_kernel<CT, R16, 32, FUSED>), grid, dim3(kThreads), 0, stream, p, rope); break;
         case 64: hipLaunchKernelGGL((decode_scores_kernel<CT, R16, 64, FUSED>), grid, dim3(kThreads), 0, stream, p, rope); break;
         case 144: hipLaunchKernelGGL((decode_scores_kernel<CT, R16, 144, FUSED>), grid, dim3(kThreads), 0, stream, p, rope); break;
+        case 160: hipLaunchKernelGGL((decode_scores_kernel<CT, R16, 160, FUSED>), grid, dim3(kThreads), 0, stream, p, rope); break;
+        case 192: hipLaunchKernelGGL((decode_scores_kernel<CT, R16, 192, FUSED>), grid, dim3(kThreads), 0, stream, p, rope); break;
+        case 256: hipLaunchKernelGGL((decode_scores_kernel<CT, R16, 256, FUSED>), grid, dim3(kThreads), 0, stream, p, rope); break;
         default: hipLaunchKernelGGL((decode_scores_kernel<CT, R16, 128, FUSED>), grid, dim3(kThreads), 0, stream, p, rope); break;
     }
 }

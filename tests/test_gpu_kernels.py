@@ -122,8 +122,8 @@ def _decode(qa, q_dev, cache, lay, layer, lens, max_len, out, ws, ws_bytes):
 
 
 @pytest.mark.parametrize("f16", [True, False])
-@pytest.mark.parametrize("lens", [[1], [2], [63], [64], [65], [157], [1000], [4096], [4186], [4500],
-                                  [156, 3913, 700, 1, 2048]])
+@pytest.mark.parametrize("lens", [[1], [2], [63], [64], [65], [157], [1000], [4096], [4186], [4500], [5000], [6000],
+                                  [8000], [156, 3913, 700, 1, 2048]])
 def test_decode_attention(qa, orc, f16, lens):
     S = len(lens)
     max_len = max(lens)
@@ -205,7 +205,7 @@ def test_decode_attention_rejects_small_workspace(qa):
 
 
 @pytest.mark.parametrize("f16", [True, False])
-@pytest.mark.parametrize("n_past", [[0], [31], [63], [64], [156], [4095], [4185], [156, 3912, 700, 0, 2047, 31]])
+@pytest.mark.parametrize("n_past", [[0], [31], [63], [64], [156], [4095], [4185], [6100], [156, 3912, 700, 0, 2047, 31]])
 def test_decode_step_fused_equals_append_then_attend(qa, orc, f16, n_past):
     """qa_decode_step_attn == qa_kv_append + qa_decode_attn at lens = n_past + 1: the whole cache and the
     output bit-exact (new row written, every other row untouched), and the output within the

@@ -67,6 +67,12 @@ def test_noalloc_matches_workspace_entry_point_over_two_calls(qa, orc):
     step_pair(qa, orc, [90, 5], 120, False, 3)                         # and an f32 cache
 
 
+def test_noalloc_matches_at_long_single_stream_capacities(qa, orc):
+    # one stream at capacities 4600 and 6000: the scores kernel then takes 144- and 192-position chunks
+    step_pair(qa, orc, [4499], 4600, True, 4)
+    step_pair(qa, orc, [5900], 6000, True, 5)
+
+
 def test_noalloc_rejects_capacity_beyond_scratch(qa):
     lay = qa.KvLayout(1, 32, 8, 128, 8192, qa.QA_CACHE_F16)
     need = qa.lib.qa_decode_attn_workspace_bytes(32, 16, 8192)

@@ -2,22 +2,26 @@
 
     python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--config 3] [--no-cpu-baseline]
 
-Workload (config 3): Qwen3-ASR-1.7B decoder, seeded N(0, 0.02) weights, f16 KV cache, prefill of
-3913 positions (3900 audio rows + 13 random prompt ids), then greedy decode at ~4k context.  The
-weights are rounded to bf16 values and kept as f32 (--weights bf16-exact, the default): a checkpoint
-converted from the released bf16 weights holds exactly such values (convert.py:386-387 widens each
-bf16 tensor with tensor.float()).  The decoder then streams bf16 copies of them and computes the same
-f32 results; --weights f32 keeps unrounded draws (f32 weights streamed).  A short decode of the same
-model with the f32 weights streamed (QA_WEIGHTS_F32=1) is reported beside the main figure.
-A step is one decode token: embedding gather, 28 layers (q|k|v GEMV, fused K/V append + split-K
-attention, o / gate-up / down GEMVs), LM head and device argmax.  value = decode tokens/s over exactly
---steps steps, weights and cache resident in HBM, bracketed by device synchronisation.
+Workload (config 3): Qwen3-ASR-1.7B decoder, seeded N(0, 0.02) weights streamed as
+f32 (the reference's contract: every weight an f32 tensor, require_f32_tensor text-decoder.cpp:29-42),
+f16 KV cache, prefill of 3913 positions (3900 audio rows + 13 random prompt ids), then greedy decode at
+~4k context, batch 1.  A step is one decode token: embedding gather, 28 layers (q|k|v GEMV, fused K/V
+append + split-K attention, o / gate-up / down GEMVs), LM head and device argmax.  value = decode
+tokens/s over exactly --steps steps, weights and cache resident in HBM, bracketed by device
+synchronisation.
+
+Each decoder is sized for the legs it runs (capacity_plan).  The secondary legs record an "error"
+object instead of ending the run: the f32-cache attention roofline, the config-4 (32-stream)
+attention and decode step, the CPU baseline, and the same draws rounded to bf16 values
+(decode_bf16_exact_weights: what a checkpoint converted from the released bf16 weights holds,
+convert.py:386-387; the decoder then streams bf16 copies of them, with f32 products and sums).
 
 roofline: the decode-step attention of one layer (fused K/V append + split-K attention: the scores
 and values kernels).  Its average duration per layer is measured with HIP events on the decoder's
 stream around a back-to-back loop at the benchmark's context, rotating through all 28 layer caches
 so the 256 MB MALL cannot serve them (470 MB of KV per token).  Algorithmic bytes per launch =
-4096 * L + 16384 (K and V rows of L positions in f16, plus q in and o out in f32).
+4096 * L + 16384 (K and V rows of L positions in f16, plus q in and o out in f32); 8192 * L + 16384
+for the f32 cache (roofline_f32_cache).
 
 cpu_baseline: the CPU oracle (oracle/qa_oracle.c, a restatement of the reference's graph
 semantics, OpenMP) decoding a bounded number of tokens of the same model at the same context.
@@ -81,11 +85,12 @@ def cpu_baseline(model, length: int, steps: int):
                        f"weights and the cache prefix at {gbs:.0f} GB/s of host memory")
 
 
-def measured_traffic(bytes_per_launch: int):
+def measured_traffic(bytes_per_launch: int, kv_name: str = "f16"):
     """HBM bytes per decode-attention launch pair from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
-    measurement (scaled by the plain-copy calibration), carried to this run's context by the measured
-    traffic / algorithmic ratio; None when the measurement file is absent."""
-    path = os.path.join(ROOT, "profiles", "decode_attention_traffic.json")
+    measurement of that cache type (scaled by the plain-copy calibration), carried to this run's context
+    by the measured traffic / algorithmic ratio; None when the measurement file is absent."""
+    name = "decode_attention_traffic.json" if kv_name == "f16" else f"decode_attention_traffic_{kv_name}.json"
+    path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None, None
     with open(path) as f:
@@ -93,6 +98,62 @@ def measured_traffic(bytes_per_launch: int):
     ratio = t["traffic_bytes"] / t["algorithmic_bytes"]
     return round(ratio * bytes_per_launch), {"measured_at_positions": t["attended_positions"],
                                             "traffic_over_algorithmic": round(ratio, 4), "source": t["source"]}
+
+
+def f32_cache_roofline(qa, cfg, L: int, reps: int):
+    """Batch-1 decode-step attention over an f32 cache (the reference's cache dtype, text-decoder.cpp:
+    1451-1462, and the drop-in's default) at L attended positions, rotating 28 layer caches; algorithmic
+    bytes per launch pair = 8192 * L + 16384 (f32 K and V rows, q in, o out)."""
+    us = attn_pair_us(qa, cfg, L, qa.QA_CACHE_F32, reps)
+    nbytes = 8192 * L + 16384
+    achieved = nbytes / (us * 1e-6) / 1e9
+    traffic, note = measured_traffic(nbytes, "f32")
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": note,
+            "bytes_per_launch": nbytes, "attended_positions": L, "avg_launch_us": round(us, 3),
+            "kernel": "decode_scores_kernel (fused K/V append) + decode_values_kernel, f32 cache"}
+
+
+def attn_pair_us(qa, cfg, L: int, cache_type: int, reps: int) -> float:
+    """Average microseconds of one batch-1 qa_decode_step_attn call at L attended positions (append at
+    row L - 1), back to back over reps x 28 launches rotating the layer caches, HIP events on the null
+    stream.  The cache holds zeros: its contents do not change the bytes moved."""
+    import ctypes as C
+
+    import numpy as np
+
+    lay = qa.KvLayout(cfg.n_layers, 1, cfg.n_kv_heads, cfg.head_dim, L + 8, cache_type)
+    cache = qa.DeviceArray(qa.lib.qa_kv_cache_bytes(C.byref(lay)), np.uint8)
+    q_dim, kv_dim = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    qkv = qa.DeviceArray.from_numpy(np.random.default_rng(5).standard_normal((1, q_dim + 2 * kv_dim)).astype(np.float32))
+    ones = qa.DeviceArray.from_numpy(np.ones(cfg.head_dim, np.float32))
+    n_past = qa.DeviceArray.from_numpy(np.array([L - 1], np.int32))
+    out = qa.DeviceArray((1, q_dim))
+    wsb = qa.lib.qa_decode_attn_workspace_bytes(1, cfg.n_heads, lay.max_seq)
+    ws = qa.DeviceArray(wsb, np.uint8)
+    scale = 1.0 / (cfg.head_dim ** 0.5)
+
+    def launch(layer):
+        qa.check(qa.lib.qa_decode_step_attn(qkv.ptr, ones.ptr, ones.ptr, cache.ptr, C.byref(lay), layer, n_past.ptr, 1,
+                                            L, cfg.n_heads, cfg.rope_theta, cfg.rms_norm_eps, scale, out.ptr, ws.ptr,
+                                            wsb, None))
+
+    for layer in range(cfg.n_layers):
+        launch(layer)
+    qa.synchronize()
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    qa.check(qa.lib.qa_event_create(C.byref(e0)))
+    qa.check(qa.lib.qa_event_create(C.byref(e1)))
+    qa.check(qa.lib.qa_event_record(e0, None))
+    for _ in range(reps):
+        for layer in range(cfg.n_layers):
+            launch(layer)
+    qa.check(qa.lib.qa_event_record(e1, None))
+    ms = C.c_float()
+    qa.check(qa.lib.qa_event_elapsed_ms(e0, e1, C.byref(ms)))
+    qa.lib.qa_event_destroy(e0)
+    qa.lib.qa_event_destroy(e1)
+    return ms.value * 1e3 / (reps * cfg.n_layers)
 
 
 def attention_roofline(qa, dec, reps: int):
@@ -216,13 +277,15 @@ def multistream_roofline(qa, cfg, reps: int, lens=None, label: str = "config 4 s
                         f"(mean {float(lens.mean()) + 1:.0f}), one layer's decode-step attention per launch pair"}
 
 
-def kernel_only(which: str, reps: int):
+def kernel_only(which: str, reps: int, weights: str = "f32"):
     """One hot-path kernel on synthetic inputs at the config-3 shape, for rocprofv3 passes (the counters
     of every dispatch are then the kernel's alone).  append: the prefill K/V append of 3913 positions
     (q/k norm + RoPE, f16 cache write); prefill: causal prefill attention over 3913 positions of one
-    layer (f16 cache, n_past 0); decode-attn: the decode-step attention of one layer at L = 4186,
-    rotating 28 layer caches; multistream: the config-4 decode step of 32 streams (end to end);
-    multistream-attn: the decode-step attention of 32 streams at L = 4096 (reps x 28 launch pairs)."""
+    layer (f16 cache, n_past 0); decode-attn / decode-attn-f32: the decode-step attention of one layer
+    at L = 4186 over an f16 / f32 cache, rotating 28 layer caches; decode-step: config 3 end to end at
+    batch 1 (prefill once, then reps greedy decode tokens); multistream: the config-4 decode step of 32
+    streams (end to end); multistream-attn: the decode-step attention of 32 streams at L = 4096 (reps x
+    28 launch pairs).  weights: f32 or bf16-exact draws for the end-to-end modes."""
     if which == "multistream-attn":
         import qwenasr_amd as qa
 
@@ -235,8 +298,37 @@ def kernel_only(which: str, reps: int):
         from qwenasr_amd import configs
 
         w = configs.CONFIGS[4]
-        model = qa.Model(w.size, n_layers=w.n_layers, bf16=True)
-        print(json.dumps(dict(kernel=which, **multistream_decode(qa, model, reps))), flush=True)
+        model = qa.Model(w.size, n_layers=w.n_layers, bf16=weights == "bf16-exact")
+        print(json.dumps(dict(kernel=which, weights=weights, **multistream_decode(qa, model, reps))), flush=True)
+        return
+    if which == "decode-step":
+        import numpy as np
+        import qwenasr_amd as qa
+        from qwenasr_amd import configs
+
+        w = configs.CONFIGS[3]
+        model = qa.Model(w.size, n_layers=w.n_layers, bf16=weights == "bf16-exact")
+        x = qa.prompt_input(model, w.audio_tokens, w.prompt_tokens)
+        with qa.Decoder(model, 1, w.prompt + reps + 8, w.cache_type) as dec:
+            logits = dec.forward(x, 0)
+            ids = dec.decode_streams(np.array([int(np.argmax(logits))], np.int32), 2)
+            qa.synchronize()
+            t0 = time.perf_counter()
+            dec.decode_streams(np.array([int(ids[-1, 0])], np.int32), reps)
+            qa.synchronize()
+            dt = time.perf_counter() - t0
+            streamed = "bf16 copies" if dec.weights_bf16 else "f32"
+        print(json.dumps(dict(kernel=which, weights=weights, weights_streamed=streamed, steps=reps,
+                              ms_per_step=round(dt * 1e3 / reps, 4))), flush=True)
+        return
+    if which == "decode-attn-f32":
+        import qwenasr_amd as qa
+
+        cfg = qa.QWEN3_ASR_1_7B.config()
+        L = 4186
+        us = attn_pair_us(qa, cfg, L, qa.QA_CACHE_F32, max(1, reps // cfg.n_layers))
+        print(json.dumps(dict(kernel=which, avg_us=round(us, 3), algorithmic_bytes_per_launch=8192 * L + 16384)),
+              flush=True)
         return
     import ctypes as C
 
@@ -343,64 +435,40 @@ def multistream_decode(qa, model, steps: int):
                         f"lock-step greedy decode, f16 cache, {streamed} streamed"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
-    ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--config", type=int, default=3, choices=[2, 3])
-    ap.add_argument("--roofline-reps", type=int, default=20)
-    ap.add_argument("--profile-steps", type=int, default=8)
-    ap.add_argument("--multistream-steps", type=int, default=16)
-    ap.add_argument("--cpu-steps", type=int, default=192, help="oracle decode steps of the CPU baseline (~10-20 s)")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--weights", choices=["bf16-exact", "f32"], default="bf16-exact",
-                    help="bf16-exact: weights rounded to bf16 values (a converted bf16 checkpoint); f32: unrounded")
-    ap.add_argument("--kv-cache", choices=["f16", "f32"], default=None,
-                    help="cache type (default: the config's, f16 for configs 2 and 3; f32 is the drop-in's default)")
-    ap.add_argument("--f32-compare-steps", type=int, default=64,
-                    help="decode steps timed with the f32 weights streamed, on the same model (0: skip)")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="only run a 256 MiB device copy 10 times (reference for HBM traffic counters)")
-    ap.add_argument("--kernel", choices=["append", "prefill", "decode-attn", "multistream", "multistream-attn"],
-                    help="only run one hot-path kernel on synthetic inputs (short program for rocprofv3 passes)")
-    ap.add_argument("--kernel-reps", type=int, default=20)
-    args = ap.parse_args()
-    if args.kernel:
-        kernel_only(args.kernel, args.kernel_reps)
-        return
-    if args.copy_calibration:
-        copy_calibration()
-        return
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the KV-cache path would shard by "
-              "KV head or by stream); run with --gpus 1", file=sys.stderr)
-        sys.exit(2)
+def capacity_plan(prompt: int, warmup: int, steps: int, profile_steps: int, bf16_steps: int) -> dict:
+    """KV-cache capacity (positions per stream) of each decoder the bench creates, sized for the legs
+    that decoder runs.  main: the prefill, the warm-up and timed decode steps, the event-bracketed
+    profile steps, and the attention roofline, which appends at the context the decode left (row ctx)
+    and attends ctx + 1 positions.  bf16_exact: its own prefill, warm-up and timed steps.  One spare
+    position each, so a step count of zero still leaves the roofline a row to append."""
+    if min(prompt, warmup, steps, profile_steps, bf16_steps) < 0 or prompt < 1:
+        raise ValueError("capacity_plan: counts must be non-negative and the prompt non-empty")
+    return {"main": prompt + warmup + steps + profile_steps + 2,
+            "bf16_exact": prompt + warmup + bf16_steps + 2}
 
+
+def guarded(result: dict, key: str, fn):
+    """Runs one secondary leg; a failure is recorded under result[key] = {"error": ...} instead of ending
+    the run, so the measurements taken before it still reach the JSON line."""
+    try:
+        result[key] = fn()
+    except Exception as e:   # noqa: BLE001 - any failure of a secondary leg is reported, not raised
+        log(f"{key}: {type(e).__name__}: {e}")
+        result[key] = {"error": f"{type(e).__name__}: {e}"}
+    return result[key]
+
+
+def decode_leg(qa, model, x, cache_type, capacity: int, warmup: int, steps: int, profile_steps: int):
+    """Prefill the prompt twice (cold, then steady state), warm up, time `steps` greedy decode tokens and
+    split `profile_steps` more by kernel family.  Returns (decoder, figures); the caller closes it."""
     import numpy as np
-    import qwenasr_amd as qa
-    from qwenasr_amd import configs
 
-    assert qa.device_count() > 0, "bench.py needs a HIP device"
-    w = configs.CONFIGS[args.config]
-    t0 = time.perf_counter()
-    model = qa.Model(w.size, n_layers=w.n_layers, bf16=args.weights == "bf16-exact")
-    x = qa.prompt_input(model, w.audio_tokens, w.prompt_tokens)
-    log(f"synthetic {w.size.name} ({args.weights} weights) built in {time.perf_counter() - t0:.1f}s")
-    max_seq = w.prompt + args.warmup + args.steps + args.profile_steps + 2
-    if args.kv_cache:
-        import dataclasses
-        w = dataclasses.replace(w, cache_type=qa.QA_CACHE_F16 if args.kv_cache == "f16" else qa.QA_CACHE_F32)
-    kv_name = "f16" if w.cache_type == qa.QA_CACHE_F16 else "f32"
-    dec = qa.Decoder(model, 1, max_seq, w.cache_type)
-    weights_streamed = "bf16 copies of bf16-exact weights" if dec.weights_bf16 else "f32"
-    log(f"decoder ready (weights + {max_seq}-position {kv_name} cache on device; GEMVs stream {weights_streamed})")
-
-    # the first prefill also allocates the prompt-sized workspaces and loads rocBLAS's kernels; the
-    # second (same input, n_past 0 again: the cache rows are rewritten) is the steady-state time
+    dec = qa.Decoder(model, 1, capacity, cache_type)
+    # the first prefill also allocates the prompt-sized workspaces and loads the GEMM libraries' kernels;
+    # the second (same input, n_past 0 again: the cache rows are rewritten) is the steady-state time
     qa.check(qa.lib.qa_device_synchronize())
     t0 = time.perf_counter()
-    logits = dec.forward(x, 0)
+    dec.forward(x, 0, want_logits=False)
     prefill_cold_ms = (time.perf_counter() - t0) * 1e3
     t0 = time.perf_counter()
     logits = dec.forward(x, 0)
@@ -412,77 +480,107 @@ def main():
     dec.forward(x, 0, want_logits=False)
     prefill_fam = {f: round(dec.profile_read(f)[0], 2) for f in ("projections", "kv_append", "prefill_attn", "logits")}
     dec.profile(False)
-    log(f"prefill {w.prompt} positions: {prefill_ms:.1f} ms (first call {prefill_cold_ms:.1f} ms); "
-        f"device ms by family {prefill_fam}")
-
-    ids = dec.decode_streams(np.array([first], np.int32), args.warmup) if args.warmup else np.array([[first]])
-    last = int(ids[-1, 0])
+    ids = dec.decode_streams(np.array([first], np.int32), warmup) if warmup else np.array([[first]], np.int32)
     qa.check(qa.lib.qa_device_synchronize())
     ctx0 = dec.cur_len(0)
     t0 = time.perf_counter()
-    ids = dec.decode_streams(np.array([last], np.int32), args.steps)
+    ids = dec.decode_streams(np.array([int(ids[-1, 0])], np.int32), steps)
     qa.check(qa.lib.qa_device_synchronize())
     dt = time.perf_counter() - t0
-    log(f"timed {args.steps} decode steps at context {ctx0}..{ctx0 + args.steps}: {dt * 1e3:.1f} ms "
-        f"({dt * 1e3 / args.steps:.3f} ms/token)")
+    fam = None
+    if profile_steps > 0:
+        # per-step device time by kernel family (HIP events around each family; events add gaps, so these
+        # are upper bounds used only for the breakdown)
+        dec.profile(True)
+        dec.profile_reset()
+        dec.decode_streams(np.array([int(ids[-1, 0])], np.int32), profile_steps)
+        fam = {f: round(dec.profile_read(f)[0] / profile_steps, 4) for f in ("decode_attn", "projections", "logits")}
+        dec.profile(False)
+    return dec, {"steps": steps, "seconds": dt, "ctx0": ctx0, "ms_per_step": round(dt * 1e3 / steps, 4),
+                 "tok_s": round(steps / dt, 3), "prefill_ms": round(prefill_ms, 2),
+                 "prefill_first_call_ms": round(prefill_cold_ms, 2), "prefill_family_ms": prefill_fam,
+                 "family_ms_per_step": fam, "first_id": first}
 
-    # per-step device time by kernel family (HIP events around each family; events add gaps, so these
-    # are upper bounds used only for the breakdown)
-    dec.profile(True)
-    dec.profile_reset()
-    dec.decode_streams(np.array([int(ids[-1, 0])], np.int32), args.profile_steps)
-    fam = {f: dec.profile_read(f) for f in ("decode_attn", "projections", "logits")}
-    dec.profile(False)
-    log("per-step device time by family, event-bracketed (ms): " +
-        ", ".join(f"{k} {v[0] / args.profile_steps:.3f}" for k, v in fam.items()))
 
-    f32_cmp = None
-    if args.f32_compare_steps > 0 and dec.weights_bf16:
-        # the same model and context with the f32 weights streamed (the kernels the golden tests pin)
-        os.environ["QA_WEIGHTS_F32"] = "1"
-        d32 = qa.Decoder(model, 1, max_seq, w.cache_type)
-        del os.environ["QA_WEIGHTS_F32"]
-        d32.forward(x, 0, want_logits=False)
-        warm = d32.decode_streams(np.array([first], np.int32), args.warmup) if args.warmup else np.array([[first]])
-        qa.check(qa.lib.qa_device_synchronize())
-        t1 = time.perf_counter()
-        ids32 = d32.decode_streams(np.array([int(warm[-1, 0])], np.int32), args.f32_compare_steps)
-        qa.check(qa.lib.qa_device_synchronize())
-        dt32 = time.perf_counter() - t1
-        d32.close()
-        # the same arithmetic on the same values: the ids follow the main run's token for token
-        n_cmp = min(args.f32_compare_steps, args.steps)
-        same = bool(np.array_equal(ids32[:n_cmp, 0], ids[:n_cmp, 0]))
-        f32_cmp = {"steps": args.f32_compare_steps, "ms_per_step": round(dt32 * 1e3 / args.f32_compare_steps, 4),
-                   "tok_s": round(args.f32_compare_steps / dt32, 3), "ids_equal_to_main_run": same,
-                   "weight_bytes_per_token": None}
-        log(f"same model, f32 weights streamed: {f32_cmp['ms_per_step']:.3f} ms/token (ids equal: {same})")
+def weight_bytes(model, elem: int) -> int:
+    """Projection and LM-head weight bytes one decode token streams (elem: 4 for f32, 2 for bf16 copies)."""
+    c = model.cfg
+    n = sum(model.tensor(f"text.blk.{l}.{t}.weight").size for l in range(c.n_layers)
+            for t in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"))
+    return int(elem * (n + model.tensor("text.output.weight").size))
 
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--config", type=int, default=3, choices=[2, 3])
+    ap.add_argument("--roofline-reps", type=int, default=20)
+    ap.add_argument("--profile-steps", type=int, default=8)
+    ap.add_argument("--multistream-steps", type=int, default=16)
+    ap.add_argument("--cpu-steps", type=int, default=192, help="oracle decode steps of the CPU baseline (~10-20 s)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--weights", choices=["f32", "bf16-exact"], default="f32",
+                    help="f32: the seeded N(0, 0.02) draws as BASELINE states them (f32 weights streamed); "
+                         "bf16-exact: the same draws rounded to bf16 values (a converted bf16 checkpoint)")
+    ap.add_argument("--kv-cache", choices=["f16", "f32"], default=None,
+                    help="cache type (default: the config's, f16 for configs 2 and 3; f32 is the drop-in's default)")
+    ap.add_argument("--bf16-steps", type=int, default=64,
+                    help="decode steps timed on the same draws rounded to bf16 values, whose bf16 copies the "
+                         "decoder streams (a secondary object of the line; 0: skip)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 256 MiB device copy 10 times (reference for HBM traffic counters)")
+    ap.add_argument("--kernel", choices=["append", "prefill", "decode-attn", "decode-attn-f32", "multistream",
+                                         "multistream-attn", "decode-step"],
+                    help="only run one hot-path kernel on synthetic inputs (short program for rocprofv3 passes)")
+    ap.add_argument("--kernel-reps", type=int, default=20)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the KV-cache path would shard by "
+              "KV head or by stream); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if args.kernel:
+        kernel_only(args.kernel, args.kernel_reps, args.weights)
+        return
+    if args.copy_calibration:
+        copy_calibration()
+        return
+
+    import dataclasses
+
+    import qwenasr_amd as qa
+    from qwenasr_amd import configs
+
+    assert qa.device_count() > 0, "bench.py needs a HIP device"
+    w = configs.CONFIGS[args.config]
+    if args.kv_cache:
+        w = dataclasses.replace(w, cache_type=qa.QA_CACHE_F16 if args.kv_cache == "f16" else qa.QA_CACHE_F32)
+    kv_name = "f16" if w.cache_type == qa.QA_CACHE_F16 else "f32"
+    plan = capacity_plan(w.prompt, args.warmup, args.steps, args.profile_steps,
+                         args.bf16_steps if args.weights == "f32" else 0)
+    t0 = time.perf_counter()
+    model = qa.Model(w.size, n_layers=w.n_layers, bf16=args.weights == "bf16-exact")
+    x = qa.prompt_input(model, w.audio_tokens, w.prompt_tokens)
+    log(f"synthetic {w.size.name} ({args.weights} weights) built in {time.perf_counter() - t0:.1f}s; "
+        f"cache capacities {plan}")
+
+    # ---- headline: batch-1 greedy decode of the config (every failure here ends the run: no line)
+    dec, main_leg = decode_leg(qa, model, x, w.cache_type, plan["main"], args.warmup, args.steps, args.profile_steps)
+    weights_streamed = "bf16 copies of bf16-exact weights" if dec.weights_bf16 else "f32"
+    ctx0, dt = main_leg["ctx0"], main_leg["seconds"]
+    log(f"prefill {w.prompt} positions: {main_leg['prefill_ms']:.1f} ms (first call "
+        f"{main_leg['prefill_first_call_ms']:.1f} ms); device ms by family {main_leg['prefill_family_ms']}")
+    log(f"timed {args.steps} decode steps at context {ctx0}..{ctx0 + args.steps} ({weights_streamed} weights "
+        f"streamed): {dt * 1e3:.1f} ms ({main_leg['ms_per_step']:.4f} ms/token); per-step device ms by family "
+        f"{main_leg['family_ms_per_step']}")
+    wbytes = weight_bytes(model, 2 if dec.weights_bf16 else 4)
     attn_us, L, attn_bytes, n_launch = attention_roofline(qa, dec, args.roofline_reps)
-    achieved = attn_bytes / (attn_us * 1e-6) / 1e9
-    log(f"decode-step attention: {attn_us:.2f} us per launch over {n_launch} launches at L={L}: "
-        f"{achieved:.0f} GB/s")
-
     dec.close()
-    roof4 = multistream_roofline(qa, model.cfg, max(2, args.roofline_reps // 4))
-    log(f"config-4 multi-stream attention: {roof4['avg_launch_us']:.1f} us per layer, {roof4['achieved']:.0f} GB/s "
-        f"({100 * roof4['frac']:.1f}% of peak)")
-
-    roof4k = multistream_roofline(qa, model.cfg, max(2, args.roofline_reps // 4), lens=[4095] * 32,
-                                  label="32 streams at 4k context")
-    log(f"32 streams at 4k: {roof4k['avg_launch_us']:.1f} us per layer, {roof4k['achieved']:.0f} GB/s "
-        f"({100 * roof4k['frac']:.1f}% of peak)")
-    ms4 = multistream_decode(qa, model, args.multistream_steps)
-    log(f"config-4 decode, {ms4['streams']} streams: {ms4['ms_per_step']:.2f} ms per step, {ms4['tok_s']:.0f} tok/s "
-        f"(device ms per step by family: {ms4['family_ms_per_step']})")
-
-    traffic, traffic_note = measured_traffic(attn_bytes)
-    n_weights = int(sum(model.tensor(n).size for n in (
-        [f"text.blk.{l}.{t}.weight" for l in range(model.cfg.n_layers) for t in
-         ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")] + ["text.output.weight"])))
-    weight_bytes = n_weights * (2 if weights_streamed != "f32" else 4)
-    if f32_cmp is not None:
-        f32_cmp["weight_bytes_per_token"] = 4 * n_weights
+    achieved = attn_bytes / (attn_us * 1e-6) / 1e9
+    log(f"decode-step attention: {attn_us:.2f} us per launch pair over {n_launch} launches at L={L}: "
+        f"{achieved:.0f} GB/s")
+    traffic, traffic_note = measured_traffic(attn_bytes, kv_name)
     result = {
         "metric": METRIC,
         "value": round(args.steps / dt, 3),
@@ -490,12 +588,12 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(dt * 1e3 / args.steps, 4),
+        "ms_per_step": main_leg["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": (f"synthetic (seeded N(0,0.02) weights{', rounded to bf16 values as in a converted bf16 checkpoint' if args.weights == 'bf16-exact' else ''}, "
+        "data": (f"synthetic (seeded N(0,0.02) weights{', rounded to bf16 values as in a converted bf16 checkpoint' if args.weights == 'bf16-exact' else ' streamed as f32'}, "
                  f"N(0,1) audio rows, random prompt ids)"),
         "config": {"workload": f"config {args.config}: {w.size.name} decoder, prefill {w.prompt} positions, greedy "
                                f"decode of {args.steps} tokens at context {ctx0}..{ctx0 + args.steps}, {kv_name} KV cache, "
@@ -507,21 +605,72 @@ def main():
                      "kernel": "decode attention of one layer: decode_scores_kernel (fused K/V append) + "
                                "decode_values_kernel, launched back to back",
                      "bytes_per_launch": attn_bytes, "attended_positions": L, "avg_launch_us": round(attn_us, 3)},
-        "roofline_multistream": roof4,
-        "roofline_multistream_4k": roof4k,
-        "multistream_decode": ms4,
         "attn_us_per_layer": round(attn_us, 3),
-        "prefill_ms": round(prefill_ms, 2),
-        "prefill_first_call_ms": round(prefill_cold_ms, 2),
-        "prefill_family_ms": prefill_fam,
-        "weight_bytes_per_token": weight_bytes,
-        "weight_stream_gbs": round(weight_bytes / (dt / args.steps) / 1e9, 1),
-        "decode_f32_weights_streamed": f32_cmp,
+        "prefill_ms": main_leg["prefill_ms"],
+        "prefill_first_call_ms": main_leg["prefill_first_call_ms"],
+        "prefill_family_ms": main_leg["prefill_family_ms"],
+        "family_ms_per_step": main_leg["family_ms_per_step"],
+        "weight_bytes_per_token": wbytes,
+        "weight_stream_gbs": round(wbytes / (dt / args.steps) / 1e9, 1),
+        "capacity_plan": plan,
     }
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(model, ctx0, args.cpu_steps)
-    else:
+
+    # ---- secondary legs: each records its own error instead of ending the run
+    def f32_cache():
+        r = f32_cache_roofline(qa, model.cfg, L, max(2, args.roofline_reps // 2))
+        log(f"f32-cache decode attention at L={r['attended_positions']}: {r['avg_launch_us']:.2f} us, "
+            f"{r['achieved']:.0f} GB/s ({100 * r['frac']:.1f}% of peak)")
+        return r
+
+    def ms_roof():
+        r = multistream_roofline(qa, model.cfg, max(2, args.roofline_reps // 4))
+        log(f"config-4 multi-stream attention: {r['avg_launch_us']:.1f} us per layer, {r['achieved']:.0f} GB/s "
+            f"({100 * r['frac']:.1f}% of peak)")
+        return r
+
+    def ms_roof4k():
+        r = multistream_roofline(qa, model.cfg, max(2, args.roofline_reps // 4), lens=[4095] * 32,
+                                 label="32 streams at 4k context")
+        log(f"32 streams at 4k: {r['avg_launch_us']:.1f} us per layer, {r['achieved']:.0f} GB/s "
+            f"({100 * r['frac']:.1f}% of peak)")
+        return r
+
+    def ms_decode():
+        r = multistream_decode(qa, model, args.multistream_steps)
+        log(f"config-4 decode, {r['streams']} streams: {r['ms_per_step']:.2f} ms per step, {r['tok_s']:.0f} tok/s "
+            f"(device ms per step by family: {r['family_ms_per_step']})")
+        return r
+
+    guarded(result, "roofline_f32_cache", f32_cache)
+    guarded(result, "roofline_multistream", ms_roof)
+    guarded(result, "roofline_multistream_4k", ms_roof4k)
+    guarded(result, "multistream_decode", ms_decode)
+    if args.no_cpu_baseline:
         result["cpu_baseline"] = None
+    else:
+        guarded(result, "cpu_baseline", lambda: cpu_baseline(model, ctx0, args.cpu_steps))
+
+    if args.weights == "f32" and args.bf16_steps > 0:
+        def bf16_leg():
+            # the same draws rounded to bf16 values (in place: the f32 legs are done): the decoder streams
+            # its bf16 copies, half the weight bytes, with f32 products and sums
+            qa.check(qa.lib.qa_model_round_bf16(model.handle))
+            x16 = qa.prompt_input(model, w.audio_tokens, w.prompt_tokens)   # prompt rows of the rounded table
+            d16, leg = decode_leg(qa, model, x16, w.cache_type, plan["bf16_exact"], args.warmup, args.bf16_steps, 0)
+            streamed = bool(d16.weights_bf16)
+            d16.close()
+            leg.pop("seconds")
+            leg.pop("first_id")
+            leg["weights_streamed"] = "bf16 copies of bf16-exact weights" if streamed else "f32"
+            leg["weight_bytes_per_token"] = weight_bytes(model, 2 if streamed else 4)
+            log(f"bf16-exact weights: {leg['ms_per_step']:.4f} ms/token ({leg['tok_s']:.1f} tok/s), prefill "
+                f"{leg['prefill_ms']:.1f} ms")
+            r4 = multistream_decode(qa, model, max(4, args.multistream_steps // 2))
+            leg["multistream_decode"] = r4
+            log(f"bf16-exact weights, config-4 decode: {r4['ms_per_step']:.2f} ms per step")
+            return leg
+
+        guarded(result, "decode_bf16_exact_weights", bf16_leg)
     print(json.dumps(result), flush=True)
 
 

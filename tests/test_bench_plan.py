@@ -1,0 +1,111 @@
+"""bench.py's KV-cache capacity plan (CPU only).
+
+Each decoder the bench creates must hold every position its legs write.  The legs are replayed here
+against the decoder's capacity rule (qa_decoder_decode_streams refuses cur_len + n_steps > max_seq;
+a cached forward refuses n_past + T > max_seq, text-decoder.cpp:1652-1656), for the driver's command
+line (--steps 20 --warmup 5), the defaults, and edge cases.
+"""
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+import bench  # noqa: E402  (imports only the standard library at module level)
+
+
+class Slot:
+    """One stream's bookkeeping under the decoder's capacity rule."""
+
+    def __init__(self, cap):
+        self.cap, self.cur = cap, 0
+
+    def forward(self, n_past, t):
+        if n_past + t > self.cap:
+            raise OverflowError(f"forward {n_past}+{t} > {self.cap}")
+        self.cur = n_past + t
+
+    def decode(self, n):
+        if self.cur + n > self.cap:
+            raise OverflowError(f"decode {self.cur}+{n} > {self.cap}")
+        self.cur += n
+
+    def attend_roofline(self):
+        # attention_roofline appends at row cur and attends cur + 1 positions
+        if self.cur + 1 > self.cap:
+            raise OverflowError(f"roofline append at {self.cur} >= {self.cap}")
+
+
+def replay(prompt, warmup, steps, profile_steps, bf16_steps):
+    plan = bench.capacity_plan(prompt, warmup, steps, profile_steps, bf16_steps)
+    main = Slot(plan["main"])
+    for _ in range(3):                      # cold, steady-state and event-bracketed prefills
+        main.forward(0, prompt)
+    main.decode(warmup)
+    main.decode(steps)
+    main.decode(profile_steps)
+    main.attend_roofline()
+    if bf16_steps:
+        side = Slot(plan["bf16_exact"])
+        for _ in range(3):
+            side.forward(0, prompt)
+        side.decode(warmup)
+        side.decode(bf16_steps)
+    return plan
+
+
+@pytest.mark.parametrize("warmup,steps", [(5, 20), (8, 256), (0, 1), (0, 0), (5, 4096), (64, 1)])
+@pytest.mark.parametrize("bf16_steps", [0, 1, 64, 500])
+def test_plan_holds_every_leg(warmup, steps, bf16_steps):
+    # config 3's prompt (3913) and a short one
+    for prompt in (3913, 156, 1):
+        replay(prompt, warmup, steps, 8, bf16_steps)
+
+
+def test_driver_command_line():
+    """The driver runs `bench.py --gpus 1 --steps 20 --warmup 5`.  A side decoder given the main decoder's
+    capacity overflows there (its 64 steps exceed the main run's 20 + 8); each decoder has its own."""
+    plan = replay(3913, 5, 20, 8, 64)
+    assert plan["main"] >= 3913 + 5 + 20 + 8 + 1
+    assert plan["bf16_exact"] >= 3913 + 5 + 64
+
+
+def test_plan_is_not_oversized():
+    # one spare row beyond the roofline's append: a cache sized from the plan has no slack to hide a bug
+    plan = bench.capacity_plan(3913, 5, 20, 8, 64)
+    with pytest.raises(OverflowError):
+        s = Slot(plan["main"] - 2)
+        s.forward(0, 3913)
+        s.decode(5 + 20 + 8)
+        s.attend_roofline()
+
+
+def test_plan_rejects_bad_counts():
+    with pytest.raises(ValueError):
+        bench.capacity_plan(0, 5, 20, 8, 64)
+    with pytest.raises(ValueError):
+        bench.capacity_plan(3913, -1, 20, 8, 64)
+
+
+def test_guarded_records_errors():
+    out = {}
+
+    def boom():
+        raise RuntimeError("leg failed")
+
+    assert bench.guarded(out, "leg", boom) == {"error": "RuntimeError: leg failed"}
+    assert bench.guarded(out, "ok", lambda: {"v": 1}) == {"v": 1}
+    assert out == {"leg": {"error": "RuntimeError: leg failed"}, "ok": {"v": 1}}
+
+
+def test_parser_defaults_and_gpus_guard(capsys):
+    """The default weights are the BASELINE draws as f32; --gpus above 1 exits with a message."""
+    import subprocess
+
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr
+    src = open(os.path.join(ROOT, "bench.py")).read()
+    assert 'ap.add_argument("--weights", choices=["f32", "bf16-exact"], default="f32"' in src

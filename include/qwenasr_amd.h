@@ -170,6 +170,12 @@ int qa_decode_step_attn_noalloc(const float * qkv, const float * q_norm_w, const
                                 const qa_kv_layout * layout, int32_t layer, const int32_t * n_past, int32_t n_streams,
                                 int32_t max_len, int32_t n_heads, float rope_theta, float eps, float scale, float * out,
                                 void * stream);
+/* Set-up of qa_decode_step_attn_noalloc on the current device: resolves the device address of its
+ * scratch array (hipGetSymbolAddress), once per device.  No counterpart in the reference.  The entry
+ * point does this itself on a device's first call, but refuses a first call made while its stream is
+ * being captured (QA_ERR_INVALID), so callers that capture call this (or the entry point once) before
+ * capturing.  qa_decoder_create calls it for the device it runs on.                              */
+int qa_decode_noalloc_prepare(void);
 
 /* Causal prefill attention over the cache (row a7): the n_tokens queries of stream `stream_idx` at
  * positions n_past .. n_past + n_tokens - 1, query t attending keys [0, n_past + t].  Same

@@ -693,15 +693,18 @@ struct Chunks {
     int scores, values;
 };
 
-int env_chunk(const char * name) {
+// The scores kernel is instantiated for 32, 64, 128, 144, 160, 192 and 256 positions per workgroup, the
+// values kernel for 32, 64, 128 and 256; any other override value is ignored.
+int env_chunk(const char * name, bool values) {
     const char * e = std::getenv(name);
     const int v = e ? std::atoi(e) : 0;
-    return v == 32 || v == 64 || v == 128 || v == 144 || v == 160 || v == 192 || v == 256 ? v : 0;
+    if (v == 32 || v == 64 || v == 128 || v == 256) return v;
+    return !values && (v == 144 || v == 160 || v == 192) ? v : 0;
 }
 
 Chunks pick_chunks(int32_t n_streams, int32_t n_kv, int32_t capacity) {
-    static const int forced_s = env_chunk("QA_DECODE_CHUNK");
-    static const int forced_v = env_chunk("QA_DECODE_VCHUNK");
+    static const int forced_s = env_chunk("QA_DECODE_CHUNK", false);
+    static const int forced_v = env_chunk("QA_DECODE_VCHUNK", true);
     Chunks ch{};
     // scores: the smallest chunk that keeps the grid at about one workgroup per CU, else 128 (measured
     // at batch 1: 32 is best up to ~1k positions, 64 at 2k, 128 from 4k on, 11.1 vs 12.2 us at 4186;
@@ -764,18 +767,20 @@ void launch_values_mb(int sr, int mb, dim3 grid, const DecodeParams & p, hipStre
     else launch_values_sr<CT, R16, CHUNK, 40>(sr, grid, p, stream);
 }
 
+// false (nothing launched) for a chunk the values kernel is not instantiated for
 template <typename CT, bool R16>
-void launch_values(int chunk, int sr, int mb, dim3 grid, const DecodeParams & p, hipStream_t stream) {
+bool launch_values(int chunk, int sr, int mb, dim3 grid, const DecodeParams & p, hipStream_t stream) {
     switch (chunk) {
-        case 32: launch_values_mb<CT, R16, 32>(sr, mb, grid, p, stream); break;
-        case 64: launch_values_mb<CT, R16, 64>(sr, mb, grid, p, stream); break;
-        case 128: launch_values_mb<CT, R16, 128>(sr, mb, grid, p, stream); break;
-        default: launch_values_mb<CT, R16, 256>(sr, mb, grid, p, stream); break;
+        case 32: launch_values_mb<CT, R16, 32>(sr, mb, grid, p, stream); return true;
+        case 64: launch_values_mb<CT, R16, 64>(sr, mb, grid, p, stream); return true;
+        case 128: launch_values_mb<CT, R16, 128>(sr, mb, grid, p, stream); return true;
+        case 256: launch_values_mb<CT, R16, 256>(sr, mb, grid, p, stream); return true;
+        default: return false;
     }
 }
 
 template <typename CT, bool R16>
-void launch_both(const Chunks & ch, bool fused, int32_t n_kv, int32_t n_streams, DecodeParams p, const RopeTable & rope,
+bool launch_both(const Chunks & ch, bool fused, int32_t n_kv, int32_t n_streams, DecodeParams p, const RopeTable & rope,
                  hipStream_t stream) {
     p.stat_chunk = ch.scores;
     const dim3 gs(static_cast<unsigned>((p.max_len + ch.scores - 1) / ch.scores * n_kv), static_cast<unsigned>(n_streams));
@@ -790,12 +795,15 @@ void launch_both(const Chunks & ch, bool fused, int32_t n_kv, int32_t n_streams,
     // more workgroups in flight
     const int n_vchunks_cap = (p.max_seq + ch.values - 1) / ch.values;
     const int mb = n_vchunks_cap <= 16 ? 8 : n_vchunks_cap <= 32 ? 16 : 40;
-    launch_values<CT, R16>(ch.values, sr, mb, gv, p, stream);
+    return launch_values<CT, R16>(ch.values, sr, mb, gv, p, stream);
 }
 
 int launch_decode(DecodeParams p, bool fused, const RopeTable & rope, const qa_kv_layout & layout,
                   int32_t n_streams, void * workspace, size_t workspace_bytes, hipStream_t stream) {
     const Chunks ch = pick_chunks(layout.n_streams, layout.n_kv_heads, layout.max_seq);
+    if (ch.values != 32 && ch.values != 64 && ch.values != 128 && ch.values != 256) {
+        return fail(QA_ERR_INVALID, "decode attention: no values kernel for the chosen chunk");
+    }
     const Workspace w = workspace_layout(layout.n_streams, layout.n_kv_heads, layout.max_seq);
     if (!workspace || workspace_bytes < w.total) {
         return fail(QA_ERR_INVALID, "decode attention: workspace too small for the cache capacity");
@@ -810,8 +818,10 @@ int launch_decode(DecodeParams p, bool fused, const RopeTable & rope, const qa_k
     p.max_seq = layout.max_seq;
     p.max_chunks = (layout.max_seq + kMinChunk - 1) / kMinChunk;
     p.score_stride = p.max_chunks * kMinChunk;
-    if (layout.cache_type == QA_CACHE_F16) launch_both<_Float16, true>(ch, fused, layout.n_kv_heads, n_streams, p, rope, stream);
-    else launch_both<float, false>(ch, fused, layout.n_kv_heads, n_streams, p, rope, stream);
+    const bool ok = layout.cache_type == QA_CACHE_F16
+                        ? launch_both<_Float16, true>(ch, fused, layout.n_kv_heads, n_streams, p, rope, stream)
+                        : launch_both<float, false>(ch, fused, layout.n_kv_heads, n_streams, p, rope, stream);
+    if (!ok) return fail(QA_ERR_INVALID, "decode attention: no values kernel for the chosen chunk");
     QA_LAUNCH_CHECK("decode attention kernels");
     return QA_OK;
 }
@@ -889,11 +899,23 @@ constexpr int kMaxDevices = 64;
 void * noalloc_ptrs[kMaxDevices] = {};
 std::mutex noalloc_mutex;
 
-int noalloc_scratch(void ** out) {
+// The address is resolved on the device's first call, or earlier by qa_decode_noalloc_prepare (the
+// decoder calls it at creation).  A first call made while `stream` is being captured is refused, so the
+// lookup never runs inside a capture: callers that capture make one eager call (or the prepare call) first.
+int noalloc_scratch(void ** out, hipStream_t stream) {
     int device = 0;
     QA_HIP(hipGetDevice(&device));
     if (device < 0 || device >= kMaxDevices) return fail(QA_ERR_DEVICE, "decode attention: device index out of range");
     std::lock_guard<std::mutex> lock(noalloc_mutex);
+    if (!noalloc_ptrs[device] && stream) {
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        QA_HIP(hipStreamIsCapturing(stream, &st));
+        if (st != hipStreamCaptureStatusNone) {
+            return fail(QA_ERR_INVALID, "qa_decode_step_attn_noalloc: the scratch address of this device is not "
+                                        "resolved yet; call qa_decode_noalloc_prepare (or the entry point once) "
+                                        "outside stream capture first");
+        }
+    }
     if (!noalloc_ptrs[device]) {
         void * p = nullptr;
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
@@ -948,6 +970,11 @@ extern "C" int qa_decode_step_attn(const float * qkv, const float * q_norm_w, co
                                    rope_theta, eps, scale, out, workspace, workspace_bytes, as_stream(stream));
 }
 
+extern "C" int qa_decode_noalloc_prepare(void) {
+    void * base = nullptr;
+    return qa::noalloc_scratch(&base, nullptr);
+}
+
 extern "C" int qa_decode_step_attn_noalloc(const float * qkv, const float * q_norm_w, const float * k_norm_w,
                                            void * cache, const qa_kv_layout * layout, int32_t layer,
                                            const int32_t * n_past, int32_t n_streams, int32_t max_len, int32_t n_heads,
@@ -967,7 +994,7 @@ extern "C" int qa_decode_step_attn_noalloc(const float * qkv, const float * q_no
     int rc = check_shape(*layout, n_streams, max_len, n_heads, layer);
     if (rc != QA_OK) return rc;
     void * base = nullptr;
-    rc = noalloc_scratch(&base);
+    rc = noalloc_scratch(&base, as_stream(stream));
     if (rc != QA_OK) return rc;
     // A previous call may have used another capacity, whose partials now lie where this layout keeps
     // its merge counters: clear this layout's counters on every call.

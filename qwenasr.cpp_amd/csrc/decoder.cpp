@@ -621,6 +621,8 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
     }
     if (qa_device_count() <= 0) return fail(QA_ERR_NO_DEVICE, "no HIP device visible");
     QA_HIP(hipSetDevice(0));
+    // the allocation-free attention entry point's scratch address, resolved here, outside any capture
+    if (qa_decode_noalloc_prepare() != QA_OK) return QA_ERR_DEVICE;
 
     qa_decoder * d = new qa_decoder();
     d->cfg = *cfg;

@@ -100,6 +100,7 @@ SIGNATURES = {
                             vp, sz, vp),
     "qa_decode_step_attn_noalloc": (C.c_int, vp, vp, vp, vp, C.POINTER(KvLayout), i32, vp, i32, i32, i32, f32, f32,
                                     f32, vp, vp),
+    "qa_decode_noalloc_prepare": (C.c_int,),
     "qa_prefill_attn_workspace_bytes": (sz, i32, i32),
     "qa_prefill_attn": (C.c_int, vp, vp, C.POINTER(KvLayout), i32, i32, i32, i32, i32, f32, vp, vp, sz, vp),
     "qa_causal_attn_f32": (C.c_int, vp, vp, vp, i32, i32, i32, f32, vp, vp),

@@ -23,24 +23,36 @@ def pytest_configure(config):
     config.stash[_GREEDY] = []
 
 
+# Accepted near-tie divergences per tie group over a session.  Only paths whose projections sum in
+# another order than the f32 kernels (the bf16-MFMA skinny GEMM and the bf16 prefill GEMM over the
+# exact three-part split) name a group; everything else, the BASELINE configs with their f32 weights
+# included, must give identical ids.
+TIE_CAP = {"config 3 bf16-exact": 1, "config 4 bf16-exact": 1}
+
+
 class GreedyRecorder:
-    """Greedy-id comparisons of the session.  Ids must be identical; the one accepted difference is a
-    first divergence at an oracle near-tie (top-2 margin < TIE_EPS) where the HIP path picked the oracle's
-    runner-up.  After it the two sequences feed different tokens and are not compared further.  Every
-    comparison is recorded and the terminal summary lists each accepted divergence by name, so a run
-    record (pytest -q tail) shows which configs and streams, if any, used the exception."""
+    """Greedy-id comparisons of the session.  Ids must be identical.  The one exception is a comparison
+    that names a tie group (TIE_CAP): there a first divergence at an oracle near-tie (top-2 margin <
+    TIE_EPS) where the HIP path picked the oracle's runner-up is accepted, at most TIE_CAP[group] times
+    per session; after it the two sequences feed different tokens and are not compared further.  Every
+    comparison is recorded and the terminal summary prints the caps and the count per group."""
 
     def __init__(self, records: list):
         self.records = records
 
-    def match(self, got, ref, margins, runner_up, what):
+    def match(self, got, ref, margins, runner_up, what, tie_group=None):
         for i, (a, b) in enumerate(zip(got, ref)):
             if a != b:
+                assert tie_group is not None, (f"{what}: ids differ at step {i} (HIP {a}, oracle {b}, oracle "
+                                               f"margin {margins[i]:.3g}) on a path that allows no near-tie")
                 assert margins[i] < TIE_EPS and a == runner_up[i], (what, i, a, b, margins[i], runner_up[i])
-                self.records.append((what, len(ref), i, float(margins[i]), int(a), int(b)))
+                used = sum(1 for r in self.records if r[6] == tie_group and r[2] is not None)
+                assert used < TIE_CAP[tie_group], (f"{what}: near-tie cap of group '{tie_group}' "
+                                                   f"({TIE_CAP[tie_group]}) exceeded at step {i}")
+                self.records.append((what, len(ref), i, float(margins[i]), int(a), int(b), tie_group))
                 return i
         assert len(got) == len(ref), (what, len(got), len(ref))
-        self.records.append((what, len(ref), None, None, None, None))
+        self.records.append((what, len(ref), None, None, None, None, tie_group))
         return None
 
 
@@ -58,7 +70,13 @@ def pytest_terminal_summary(terminalreporter, exitstatus, config):
     terminalreporter.write_line(
         f"greedy ids: {len(recs)} sequences ({ids} ids) compared, {len(recs) - len(div)} identical, "
         f"{len(div)} accepted near-tie divergence(s) (oracle top-2 margin < {TIE_EPS:g}, runner-up taken)")
-    for what, n, i, m, a, b in div:
+    strict = [r for r in recs if r[6] is None]
+    terminalreporter.write_line(f"  strict (no near-tie allowed): {len(strict)} sequences, all identical")
+    for group, cap in TIE_CAP.items():
+        n = sum(1 for r in recs if r[6] == group)
+        used = sum(1 for r in div if r[6] == group)
+        terminalreporter.write_line(f"  tie group '{group}': {n} sequences, {used} of cap {cap} near-ties used")
+    for what, n, i, m, a, b, _ in div:
         terminalreporter.write_line(f"  near-tie: {what}: step {i} of {n}, oracle margin {m:.2e}, "
                                     f"HIP id {a} = oracle runner-up, oracle id {b}")
 

@@ -115,7 +115,8 @@ def test_config_greedy_matches_golden(qa, greedy, index, bf16):
     with qa.Decoder(model, 1, w.max_seq, w.cache_type) as dec:
         assert dec.weights_bf16 == bf16
         out = dec.generate(x, w.new_tokens, margins=True)
-        div = greedy.match(out["ids"], g["ids"], g["margins"], g["runner_up"], label)
+        div = greedy.match(out["ids"], g["ids"], g["margins"], g["runner_up"], label,
+                           tie_group="config 3 bf16-exact" if bf16 else None)
         if div is None:
             assert out["stopped"] == g["stopped"] and out["total_tokens"] == g["total_tokens"]
             assert dec.cur_len(0) == g["cur_len"]
@@ -148,7 +149,8 @@ def test_config4_ragged_streams_match_golden(qa, greedy, bf16):
         assert sorted(int(s) for s in g["streams"]) == list(range(w.streams))   # every stream has a golden
         for s, ref in g["streams"].items():
             greedy.match(ids[:, int(s)].tolist(), ref["ids"], ref["margins"], ref["runner_up"],
-                         f"config 4{' (bf16-exact weights)' if bf16 else ''} stream {s}")
+                         f"config 4{' (bf16-exact weights)' if bf16 else ''} stream {s}",
+                         tie_group="config 4 bf16-exact" if bf16 else None)
         assert dec.device_lens().tolist() == (lens + w.steps).tolist()
         assert [dec.cur_len(s) for s in range(w.streams)] == (lens + w.steps).tolist()
 

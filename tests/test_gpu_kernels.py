@@ -192,6 +192,61 @@ def test_decode_attention_long_context(qa, orc, f16, L):
         check_close(got[0], ref)
 
 
+_FORCED_CHUNK_CHILD = r"""
+import ctypes as C, os, sys
+import numpy as np
+root = sys.argv[1]
+sys.path[:0] = [os.path.join(root, "qwenasr.cpp_amd"), os.path.join(root, "oracle")]
+import qwenasr_amd as qa, qa_oracle as orc
+scale = 1.0 / np.sqrt(128.0)
+worst = 0.0
+for f16 in (True, False):
+    for lens in ([1000], [4186], [157, 3000]):
+        S, L = len(lens), max(lens)
+        lay = qa.KvLayout(1, S, 8, 128, L + 3, qa.QA_CACHE_F16 if f16 else qa.QA_CACHE_F32)
+        rng = np.random.default_rng(L + S)
+        host = np.zeros((1, 2, S, 8, L + 3, 128), np.float16 if f16 else np.float32)
+        for s, n in enumerate(lens):
+            host[0, :, s, :, :n] = rng.standard_normal((2, 8, n, 128))
+        q = rng.standard_normal((S, 16, 128)).astype(np.float32)
+        cache, d_q = qa.DeviceArray.from_numpy(host), qa.DeviceArray.from_numpy(q)
+        d_lens, out = qa.DeviceArray.from_numpy(np.array(lens, np.int32)), qa.DeviceArray((S, 2048))
+        wsb = qa.lib.qa_decode_attn_workspace_bytes(S, 16, lay.max_seq)
+        ws = qa.DeviceArray(wsb, np.uint8)
+        print(f"forced chunks f16={f16} lens={lens}", flush=True)
+        for rep in range(2):
+            qa.check(qa.lib.qa_decode_attn(d_q.ptr, cache.ptr, C.byref(lay), 0, d_lens.ptr, S, L, 16, scale, out.ptr,
+                                           ws.ptr, wsb, None))
+            got = out.numpy().reshape(S, 16, 128)
+            for s, n in enumerate(lens):
+                k = host[0, 0, s, :, :n].astype(np.float32)
+                v = host[0, 1, s, :, :n].astype(np.float32)
+                ref = orc.cache_attention(k, v, q[s:s + 1], n - 1, f16)[0]
+                err = float(np.abs(got[s] - ref).max())
+                rel = float(np.linalg.norm(got[s] - ref) / np.linalg.norm(ref))
+                assert err <= 2e-3 and rel <= 1e-3, (f16, lens, s, err, rel)
+                worst = max(worst, err)
+print(f"forced chunks ok, max abs err {worst:.2e}", flush=True)
+"""
+
+
+@pytest.mark.parametrize("chunk,vchunk", [("256", "0"), ("144", "144"), ("32", "256")])
+def test_decode_attention_forced_chunks(qa, chunk, vchunk):
+    """The tuning overrides QA_DECODE_CHUNK / QA_DECODE_VCHUNK (read once per process, so each case runs
+    in a child process): a forced 256-position scores chunk, and a values override the values kernel has
+    no instantiation for (144: ignored, the capacity's choice stays), both held to the oracle."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, QA_DECODE_CHUNK=chunk, QA_DECODE_VCHUNK=vchunk)
+    r = subprocess.run([sys.executable, "-c", _FORCED_CHUNK_CHILD, root], env=env, capture_output=True, text=True,
+                       timeout=110)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and "forced chunks ok" in r.stdout
+
+
 def test_decode_attention_rejects_small_workspace(qa):
     lay = layout(qa, 1, 1, 4096, True)
     cache = Cache(qa, lay)

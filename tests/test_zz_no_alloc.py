@@ -83,3 +83,10 @@ def test_noalloc_rejects_capacity_beyond_scratch(qa):
     assert rc == qa.QA_ERR_INVALID and b"maximum" in qa.lib.qa_last_error()
     fits = qa.lib.qa_decode_attn_workspace_bytes(32, 16, 4000)        # config 4's capacity fits
     assert fits <= qa.QA_NOALLOC_SCRATCH_BYTES
+
+
+def test_noalloc_prepare_is_idempotent(qa):
+    """The set-up call resolves the scratch address of the current device; later calls (and the decoder's
+    own call at creation) find it resolved."""
+    assert qa.lib.qa_decode_noalloc_prepare() == qa.QA_OK
+    assert qa.lib.qa_decode_noalloc_prepare() == qa.QA_OK

@@ -242,9 +242,12 @@ int launch_gemv_nr(int nr, const GemvParams & p, hipStream_t stream) {
     }
 }
 
-// default rows per wave: 16-32 KB of f32 weights per wave; bf16 rows at least 2 per wave (the 1.7B
+// default rows per wave: 8-32 KB of f32 weights per wave; bf16 rows at least 2 per wave (the 1.7B
 // decode step's bf16 GEMVs, traced at 1, 2 and 4 rows: 2 is fastest for every shape, by up to 20%
-// over 4 for o-proj, 10% over 1 for q|k|v)
+// over 4 for o-proj, 10% over 1 for q|k|v).  f32 rows at in_dim 2048 (the 1.7B q|k|v, o, gate|up and
+// LM head): one row per wave, i.e. twice the workgroups in flight (config-3 token with f32 weights:
+// 1.515-1.518 ms against 1.574-1.576 ms with 2 rows and 1.668 ms with 4).  A row's sum is the same
+// whatever the rows per wave, so the results do not change.
 template <int EPI, bool PRENORM, bool B16>
 int launch_gemv_in(const GemvParams & p, hipStream_t stream) {
     const int forced = gemv_rows_override();
@@ -252,7 +255,7 @@ int launch_gemv_in(const GemvParams & p, hipStream_t stream) {
     auto nr = [&](int f32_rows) { return forced ? forced : B16 ? std::max(2, f32_rows) : f32_rows; };
     switch (p.in_dim) {
         case 1024: return launch_gemv_nr<4, EPI, PRENORM, B16>(nr(sw ? 2 : 4), p, stream);
-        case 2048: return launch_gemv_nr<8, EPI, PRENORM, B16>(nr(2), p, stream);
+        case 2048: return launch_gemv_nr<8, EPI, PRENORM, B16>(nr(B16 ? 2 : 1), p, stream);
         case 3072: return launch_gemv_nr<12, EPI, PRENORM, B16>(nr(sw ? 1 : 2), p, stream);
         case 4096: return launch_gemv_nr<16, EPI, PRENORM, B16>(nr(sw ? 1 : 2), p, stream);
         case 6144: return launch_gemv_nr<24, EPI, PRENORM, B16>(nr(1), p, stream);

@@ -74,7 +74,7 @@ struct qa_decoder {
     hipblasLtHandle_t lt = nullptr;           // prefill GEMMs on bf16 copies
     void * lt_ws = nullptr;
     size_t lt_ws_bytes = 0;
-    std::map<std::tuple<int32_t, int32_t, int32_t>, LtPlan> lt_plans;   // (M, N, K)
+    std::map<std::tuple<int32_t, int32_t, int32_t, int32_t>, LtPlan> lt_plans;   // (M, N, K, ldb)
     std::vector<DevLayer> layers;
     float * embd = nullptr;
     float * out_norm = nullptr;
@@ -217,7 +217,7 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
         rc = dmalloc(d->act_allocs, n * sizeof(double), reinterpret_cast<void **>(&d->xstats));
     }
     // bf16 copies: longer GEMM inputs are split into three bf16 parts ([rows][3 in_dim]) for the bf16 GEMM
-    if (rc == QA_OK && rows > kSkinnyRows && !d->layers.empty() && d->layers[0].qkv3) {
+    if (rc == QA_OK && rows > kSkinnyRows && !d->layers.empty() && (d->layers[0].qkv3 || d->layers[0].qkv16)) {
         d->xsplit_elems = R * std::max({H, QD, I});
         rc = dmalloc_t(d->act_allocs, 3 * d->xsplit_elems, &d->xsplit);
     }
@@ -238,8 +238,8 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
     return QA_OK;
 }
 
-// C[N][M] (column-major M x N) = beta C + A^T B: A = [M][K] and B = [N][K] bf16 rows, f32 accumulation and
-// output, on hipBLASLt with the heuristic's first algorithm for the shape.
+// C[N][M] (column-major M x N) = beta C + A^T B: A = [M][K] and B = [N][K] bf16 rows (row stride ldb), f32
+// accumulation and output, on hipBLASLt with the heuristic's first algorithm for the shape.
 void lt_free(LtPlan & pl) {
     if (pl.a) hipblasLtMatrixLayoutDestroy(pl.a);
     if (pl.b) hipblasLtMatrixLayoutDestroy(pl.b);
@@ -248,10 +248,11 @@ void lt_free(LtPlan & pl) {
     pl = LtPlan{};
 }
 
-int lt_gemm(qa_decoder * d, int32_t M, int32_t N, int32_t K, const uint16_t * A, const uint16_t * B, float beta, float * C) {
+int lt_gemm(qa_decoder * d, int32_t M, int32_t N, int32_t K, const uint16_t * A, const uint16_t * B, int32_t ldb,
+            float beta, float * C) {
     // N is the prompt length: a serving loop meets many, so the plans are dropped once 256 have piled up
     // (a plan holds host-side descriptors only; the calls that used them were enqueued with their values)
-    const auto key = std::make_tuple(M, N, K);
+    const auto key = std::make_tuple(M, N, K, ldb);
     if (d->lt_plans.size() >= 256 && d->lt_plans.find(key) == d->lt_plans.end()) {
         for (auto & kv : d->lt_plans) lt_free(kv.second);
         d->lt_plans.clear();
@@ -263,7 +264,7 @@ int lt_gemm(qa_decoder * d, int32_t M, int32_t N, int32_t K, const uint16_t * A,
                   hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) == HIPBLAS_STATUS_SUCCESS &&
                   hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) == HIPBLAS_STATUS_SUCCESS &&
                   hipblasLtMatrixLayoutCreate(&pl.a, HIP_R_16BF, K, M, K) == HIPBLAS_STATUS_SUCCESS &&
-                  hipblasLtMatrixLayoutCreate(&pl.b, HIP_R_16BF, K, N, K) == HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatrixLayoutCreate(&pl.b, HIP_R_16BF, K, N, ldb) == HIPBLAS_STATUS_SUCCESS &&
                   hipblasLtMatrixLayoutCreate(&pl.c, HIP_R_32F, M, N, M) == HIPBLAS_STATUS_SUCCESS;
         hipblasLtMatmulPreference_t pref = nullptr;
         if (ok) {
@@ -301,28 +302,39 @@ bool skinny_path(const qa_decoder * d, int32_t rows, int32_t in_dim) {
 }
 
 // Whether sgemm runs the bf16 GEMM over the three-part split of its input (then the producer of the
-// input may write d->xsplit itself, see sgemm's x_split).
-bool split_path(const qa_decoder * d, int32_t rows, int32_t in_dim, const uint16_t * W3) {
-    return !skinny_path(d, rows, in_dim) && W3 && d->lt && d->xsplit &&
+// input may write d->xsplit itself, see sgemm's x_split).  W3: the tripled bf16 rows; W16: the bf16 rows.
+bool split_path(const qa_decoder * d, int32_t rows, int32_t in_dim, const uint16_t * W3, const uint16_t * W16) {
+    return !skinny_path(d, rows, in_dim) && (W3 || W16) && d->lt && d->xsplit &&
            static_cast<size_t>(rows) * in_dim <= d->xsplit_elems;
 }
 
 int sgemm(qa_decoder * d, const float * W, int32_t out_dim, int32_t in_dim, const float * X, int32_t rows, float * Y,
-          float beta, const uint16_t * W3 = nullptr, bool x_split = false) {
+          float beta, const uint16_t * W3 = nullptr, const uint16_t * W16 = nullptr, bool x_split = false) {
     // Y[rows][out] (+)= X[rows][in] * W[out][in]^T.  Up to kSkinnyRows rows (multi-stream decode, short
     // prefills) the weights are streamed once by the skinny MFMA GEMM; longer prefills use hipBLASLt on
     // the bf16 copies, or rocBLAS sgemm on f32 weights.  x_split: the producer of X already wrote its
     // three-part split into d->xsplit (only where split_path holds).
-    if (x_split && !split_path(d, rows, in_dim, W3)) return fail(QA_ERR_INVALID, "sgemm: split input without split path");
+    if (x_split && !split_path(d, rows, in_dim, W3, W16)) {
+        return fail(QA_ERR_INVALID, "sgemm: split input without split path");
+    }
     if (skinny_path(d, rows, in_dim)) {
         return gemm_rows_launch(W, out_dim, in_dim, X, rows, Y, beta != 0.0f, d->gr_ws, d->gr_ws_bytes, d->stream);
     }
-    if (split_path(d, rows, in_dim, W3)) {
-        // bf16-exact weights: each row of X split into three bf16 parts, X = hi + mid + lo exactly, and
-        // Y = [W W W] [hi; mid; lo]: one bf16 GEMM over 3 in_dim with f32 accumulation -- every product
-        // exact, the sums in f32, Y written once (three GEMMs of in_dim would read and write Y three times)
+    if (split_path(d, rows, in_dim, W3, W16)) {
+        // bf16-exact weights: each row of X split into three bf16 parts, X = hi + mid + lo exactly.  With the
+        // tripled rows, Y = [W W W] [hi; mid; lo]: one bf16 GEMM over 3 in_dim with f32 accumulation -- every
+        // product exact, the sums in f32, Y written once.  Without them (a decoder created with
+        // QA_PREFILL_TRIPLED=0), three GEMMs over the one bf16 copy, the second and third accumulating into Y
+        // (beta 1): the same exact products, Y written three times and read twice.
         const int rc = x_split ? QA_OK : split_bf16x3_rows_launch(X, rows, in_dim, d->xsplit, d->stream);
-        return rc != QA_OK ? rc : lt_gemm(d, out_dim, rows, 3 * in_dim, W3, d->xsplit, beta, Y);
+        if (rc != QA_OK) return rc;
+        if (W3) return lt_gemm(d, out_dim, rows, 3 * in_dim, W3, d->xsplit, 3 * in_dim, beta, Y);
+        int r = QA_OK;
+        for (int part = 0; part < 3 && r == QA_OK; ++part) {
+            r = lt_gemm(d, out_dim, rows, in_dim, W16, d->xsplit + static_cast<size_t>(part) * in_dim, 3 * in_dim,
+                        part == 0 ? beta : 1.0f, Y);
+        }
+        return r;
     }
     // column-major C(out x rows) = W^T(out x in) * X(in x rows)
     const float alpha = 1.0f;
@@ -392,9 +404,9 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
             rc = fused_gemm(d, L.qkv, W3, H, d->x, rows, d->qkv, false, norm_in(d, L.attn_norm), L.qkv16);
         } else {
             // the RMSNorm writes the GEMM's split input directly where the GEMM takes one
-            const bool sp = split_path(d, rows, H, L.qkv3);
+            const bool sp = split_path(d, rows, H, L.qkv3, L.qkv16);
             rc = rmsnorm_rows_launch(d->x, L.attn_norm, rows, H, c.rms_norm_eps, d->xn, s, sp ? d->xsplit : nullptr);
-            if (rc == QA_OK) rc = sgemm(d, L.qkv, W3, H, d->xn, rows, d->qkv, 0.0f, L.qkv3, sp);
+            if (rc == QA_OK) rc = sgemm(d, L.qkv, W3, H, d->xn, rows, d->qkv, 0.0f, L.qkv3, L.qkv16, sp);
         }
         if (rc != QA_OK) return rc;
     }
@@ -442,12 +454,12 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
         if (rc == QA_OK) rc = fused_gemm(d, L.gu, 2 * I, H, d->x, rows, d->act, false, gu, L.gu16);
         if (rc == QA_OK) rc = fused_gemm(d, L.down, H, I, d->act, rows, d->x, true, stats_out(d), L.down16);
     } else {
-        const bool sg = split_path(d, rows, H, L.gu3), sd = split_path(d, rows, I, L.down3);
-        rc = sgemm(d, L.o, H, QD, d->attn, rows, d->x, 1.0f, L.o3);
+        const bool sg = split_path(d, rows, H, L.gu3, L.gu16), sd = split_path(d, rows, I, L.down3, L.down16);
+        rc = sgemm(d, L.o, H, QD, d->attn, rows, d->x, 1.0f, L.o3, L.o16);
         if (rc == QA_OK) rc = rmsnorm_rows_launch(d->x, L.ffn_norm, rows, H, c.rms_norm_eps, d->xn, s, sg ? d->xsplit : nullptr);
-        if (rc == QA_OK) rc = sgemm(d, L.gu, 2 * I, H, d->xn, rows, d->gu, 0.0f, L.gu3, sg);
+        if (rc == QA_OK) rc = sgemm(d, L.gu, 2 * I, H, d->xn, rows, d->gu, 0.0f, L.gu3, L.gu16, sg);
         if (rc == QA_OK) rc = swiglu_rows_launch(d->gu, rows, I, d->act, s, sd ? d->xsplit : nullptr);
-        if (rc == QA_OK) rc = sgemm(d, L.down, H, I, d->act, rows, d->x, 1.0f, L.down3, sd);
+        if (rc == QA_OK) rc = sgemm(d, L.down, H, I, d->act, rows, d->x, 1.0f, L.down3, L.down16, sd);
     }
     return rc;
 }
@@ -576,8 +588,11 @@ int pack_weights_bf16(qa_decoder * d) {
                         hipStreamSynchronize(d->stream) != hipSuccess)) {
         rc = fail(QA_ERR_DEVICE, "bf16 weight check failed");
     }
-    if (rc == QA_OK && inexact == 0 && d->max_seq > kSkinnyRows) {
-        // prefill GEMMs: each bf16 row three times (see sgemm)
+    // prefill GEMMs: each bf16 row three times (see sgemm), unless QA_PREFILL_TRIPLED=0 asks for the one bf16
+    // copy only (three GEMMs per projection instead of one; 8.5 GB less for the 1.7B model)
+    const char * tr = std::getenv("QA_PREFILL_TRIPLED");
+    const bool tripled = !(tr && std::strcmp(tr, "0") == 0);
+    if (rc == QA_OK && inexact == 0 && d->max_seq > kSkinnyRows && tripled) {
         auto repeat3 = [&](const uint16_t * src, size_t N, size_t K, uint16_t ** dst) {
             if (rc != QA_OK) return;
             rc = dmalloc_t(d->b16_allocs, 3 * N * K, dst);
@@ -688,8 +703,8 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
     }
     if (rc != QA_OK) return bail(rc);
     rc = pack_weights_bf16(d);
-    if (rc == QA_OK && !d->layers.empty() && d->layers[0].qkv3) {
-        // hipBLASLt for the prefill GEMMs over the tripled bf16 rows (its workspace: 64 MiB)
+    if (rc == QA_OK && !d->layers.empty() && d->max_seq > kSkinnyRows && (d->layers[0].qkv3 || d->layers[0].qkv16)) {
+        // hipBLASLt for the prefill GEMMs over the bf16 rows, tripled or not (its workspace: 64 MiB)
         d->lt_ws_bytes = size_t(64) << 20;
         if (hipblasLtCreate(&d->lt) != HIPBLAS_STATUS_SUCCESS) {
             rc = fail(QA_ERR_DEVICE, "hipBLASLt handle creation failed");

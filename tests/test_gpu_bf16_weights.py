@@ -107,16 +107,21 @@ def test_pack_bf16_flags_inexact_values(qa, n):
     assert int(flag.numpy()[0]) == 1
 
 
-def _decoder(qa, model, max_seq, f32_weights):
-    old = os.environ.pop("QA_WEIGHTS_F32", None)
+def _decoder(qa, model, max_seq, f32_weights, tripled=True):
+    """A decoder created with QA_WEIGHTS_F32=1 (f32_weights) and/or QA_PREFILL_TRIPLED=0 (not tripled); both
+    are read at creation, so the environment is restored right after."""
+    saved = {k: os.environ.pop(k, None) for k in ("QA_WEIGHTS_F32", "QA_PREFILL_TRIPLED")}
     try:
         if f32_weights:
             os.environ["QA_WEIGHTS_F32"] = "1"
+        if not tripled:
+            os.environ["QA_PREFILL_TRIPLED"] = "0"
         return qa.Decoder(model, 1, max_seq, qa.QA_CACHE_F16)
     finally:
-        os.environ.pop("QA_WEIGHTS_F32", None)
-        if old is not None:
-            os.environ["QA_WEIGHTS_F32"] = old
+        for k, v in saved.items():
+            os.environ.pop(k, None)
+            if v is not None:
+                os.environ[k] = v
 
 
 def test_decoder_keeps_bf16_copies_only_for_exact_weights(qa):
@@ -259,10 +264,12 @@ def test_bf16_weights_multistream_equals_f32_weights_and_oracle(qa, orc, greedy,
                          f"bf16-exact weights ({name}), {n_streams}-stream step, stream {s}")
 
 
-def test_bf16_weights_long_prefill_matches_oracle(qa, orc, greedy):
+@pytest.mark.parametrize("tripled", [True, False])
+def test_bf16_weights_long_prefill_matches_oracle(qa, orc, greedy, tripled):
     """A 300-position prompt (longer than the 64 rows of the skinny GEMM): with bf16 copies each prefill
     projection is one hipBLASLt bf16 GEMM over the exact three-part split of its input against the tripled
-    weight rows (exact products, f32 sums).  Logits against the oracle and against the f32-weight decoder,
+    weight rows, or (QA_PREFILL_TRIPLED=0) three GEMMs over the one bf16 copy accumulating into the output
+    (exact products, f32 sums either way).  Logits against the oracle and against the f32-weight decoder,
     then greedy ids."""
     model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=3, bf16=True)
     om = orc.OracleModel.from_product_model(model)
@@ -272,7 +279,7 @@ def test_bf16_weights_long_prefill_matches_oracle(qa, orc, greedy):
     ref = om.generate(x, N, qa.STOP_IDS, om.cache(300 + N, True))
     logits = {}
     for f32_weights in (False, True):
-        with _decoder(qa, model, 300 + N, f32_weights) as dec:
+        with _decoder(qa, model, 300 + N, f32_weights, tripled) as dec:
             assert dec.weights_bf16 == (not f32_weights)
             logits[f32_weights] = dec.forward(x, 0)
             if not f32_weights:
@@ -283,7 +290,7 @@ def test_bf16_weights_long_prefill_matches_oracle(qa, orc, greedy):
         assert err <= 2e-3 and rel <= 1e-3, (err, rel)
     assert float(np.abs(logits[False].astype(np.float64) - logits[True]).max()) <= 2e-3
     assert greedy.match(out["ids"], ref["ids"], ref["margins"], ref["runner_up"],
-                        "bf16-exact weights, 300-position prompt") is None
+                        f"bf16-exact weights, 300-position prompt ({'tripled rows' if tripled else 'one bf16 copy'})") is None
 
 
 def test_bf16_prefill_many_prompt_lengths(qa, orc):

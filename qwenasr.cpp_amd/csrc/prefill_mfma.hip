@@ -43,6 +43,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 namespace qa {
@@ -77,7 +79,10 @@ constexpr int kPfMaxMerge = 8192;       // merge counters: one per (KV head, que
 constexpr int kPfCutUnits = 2048;       // (KV head, query tile) units up to which long tiles are cut
 constexpr size_t kPfQueueBytes = 2 * kPfMaxHeads * kPfCounterStride * sizeof(uint32_t);
 constexpr size_t kPfFixedBytes = kPfQueueBytes + static_cast<size_t>(kPfMaxMerge) * kPfCounterStride * sizeof(uint32_t);
-constexpr size_t kPfPartialFloats = kQB * 8 * kPfThreads * 4;    // one part's O: 16 float4 per thread
+constexpr size_t kPfOFloats = kQB * 8 * kPfThreads * 4;           // one part's O: 16 float4 per thread
+// one part's O, then (single pass) each thread's running max and sum of its two query columns: a float pair
+// (m, pad) and a double per block, 4 uint64 per thread
+constexpr size_t kPfPartialFloats = kPfOFloats + kPfThreads * 8;
 
 struct alignas(16) PrefillStat {
     float m;
@@ -234,11 +239,26 @@ __device__ inline void stats_update(const f4 (&S)[4], float c, float & m, double
     m = mn;
 }
 
+// O^T += V^T P^T for the P^T fragments pf[qb][ksv] (element e <-> key (2 ksv + e / 4) * 16 + g4 * 4 + e % 4 of
+// the tile).  Each V^T fragment is read once for both blocks.
+__device__ inline void pv_frags(const h8 (&pf)[kQB][2], const _Float16 * sV, int c16, int g4, f4 (&O)[kQB][8]) {
+#pragma unroll
+    for (int ksv = 0; ksv < 2; ++ksv) {
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            const h8 a = *reinterpret_cast<const h8 *>(sV + (db * 16 + c16) * kVS + ksv * 32 + g4 * 8);
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) {
+                O[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pf[qb][ksv], O[qb][db], 0, 0, 0);
+            }
+        }
+    }
+}
+
 // mc[qb] = (M scale - log2 S) log2 e for this lane's query column of block qb: p = exp2(s c - mc) =
-// exp(s scale - M) / S.  Each V^T fragment is read once for both blocks.
+// exp(s scale - M) / S.
 __device__ inline void pv_tile(const f4 (&S)[kQB][4], const _Float16 * sV, const float (&mc)[kQB], float c, int c16,
                                int g4, f4 (&O)[kQB][8]) {
-    // P^T fragments: pf[qb][ksv] element e <-> key (2 ksv + e / 4) * 16 + g4 * 4 + e % 4
     h8 pf[kQB][2];
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
@@ -251,17 +271,66 @@ __device__ inline void pv_tile(const f4 (&S)[kQB][4], const _Float16 * sV, const
             }
         }
     }
+    pv_frags(pf, sV, c16, g4, O);
+}
+
+// Rescale threshold of the single pass, in log2 units of the exponentials: a column's reference max is moved
+// up only when the tile's max exceeds it by more than this, so the exponentials stay below 2^8 (f16 holds
+// them with room) and the O accumulators are rescaled only when some column's max grows that much.
+constexpr float kLazyLog2 = 8.0f;
+
+// Single-pass (online softmax) update of one key tile: m[qb] is the reference max of this lane's query column
+// (raw score units, -inf while no key is attended), l[qb] the sum of exp(s - m) over the keys this lane
+// holds; e = exp(s - m) is rounded to f16 for the PV MFMA.
+__device__ inline void online_tile(const f4 (&S)[kQB][4], const _Float16 * sV, float c, int c16, int g4,
+                                   float (&m)[kQB], double (&l)[kQB], f4 (&O)[kQB][8]) {
+    float mn[kQB];
+    bool up[kQB];
+    bool any = false;
 #pragma unroll
-    for (int ksv = 0; ksv < 2; ++ksv) {
+    for (int qb = 0; qb < kQB; ++qb) {
+        float t = -INFINITY;
 #pragma unroll
-        for (int db = 0; db < 8; ++db) {
-            const h8 a = *reinterpret_cast<const h8 *>(sV + (db * 16 + c16) * kVS + ksv * 32 + g4 * 8);
+        for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) {
-                O[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pf[qb][ksv], O[qb][db], 0, 0, 0);
-            }
+            for (int i = 0; i < 4; ++i) t = fmaxf(t, S[qb][kb][i]);
+        }
+        // the column's 64 keys are held by lanes c16 + 16 g4, g4 = 0..3
+        t = fmaxf(t, __shfl_xor(t, 16, kWave));
+        t = fmaxf(t, __shfl_xor(t, 32, kWave));
+        mn[qb] = fmaxf(m[qb], t);
+        // -inf -> finite compares as +inf > threshold; -inf -> -inf gives NaN, which is no move
+        up[qb] = (mn[qb] - m[qb]) * c > kLazyLog2;
+        any = any || up[qb];
+    }
+    if (__any(any)) {
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) {
+            // lanes whose column keeps its max multiply by 1
+            const float f = up[qb] ? __builtin_amdgcn_exp2f((m[qb] - mn[qb]) * c) : 1.0f;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) O[qb][db] *= f;
+            l[qb] *= static_cast<double>(f);
+            if (up[qb]) m[qb] = mn[qb];
         }
     }
+    h8 pf[kQB][2];
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+        const float mc = m[qb] == -INFINITY ? INFINITY : m[qb] * c;   // nothing attended yet: every e is 0
+        float part = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float e = __builtin_amdgcn_exp2f(fmaf(S[qb][kb][i], c, -mc));
+                part += e;
+                pf[qb][kb >> 1][(kb & 1) * 4 + i] = static_cast<_Float16>(e);
+            }
+        }
+        l[qb] += static_cast<double>(part);
+    }
+    pv_frags(pf, sV, c16, g4, O);
 }
 
 // One work item: KV head g, part j of query tile qt, key tiles [kt0, kt1); cut says whether qt has
@@ -307,10 +376,12 @@ __device__ inline Item item_of(const MfmaParams & p, int g, int k) {
 // One work item.  PASS 1: the part's row statistics (max and sum of exp) of its kCols query columns.
 // PASS 2: p over the part's keys with the statistics of both parts of its query tile, and
 // O^T += V^T P^T; the two parts of a cut tile are added by whichever finishes second.
+// PASS 3 (single pass): online softmax over the part's keys (online_tile); the part's O, max and sum are
+// combined with the other part's by whichever finishes second, then O / sum is stored.
 template <int PASS>
 __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 (*sK)[kBK * kKS],
                                 _Float16 (*sV)[kHeadDim * kVS]) {
-    constexpr bool kWithV = PASS == 2;
+    constexpr bool kWithV = PASS != 1;
     const int g = it.g;
     const int t0 = it.qt * kBQ;
     const int lane = threadIdx.x & (kWave - 1);
@@ -407,11 +478,13 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
         if constexpr (PASS == 1) {
 #pragma unroll
             for (int qb = 0; qb < kQB; ++qb) stats_update(S[qb], c, m[qb], sum[qb]);
-        } else {
+        } else if constexpr (PASS == 2) {
             pv_tile(S, sV[b], mc, c, c16, g4, O);
+        } else {
+            online_tile(S, sV[b], c, c16, g4, m, sum, O);
         }
         if (kt + 1 < kt1) {
-            store_tile(regs, sK[b ^ 1], sV[PASS == 2 ? (b ^ 1) : 0], kWithV);
+            store_tile(regs, sK[b ^ 1], sV[PASS != 1 ? (b ^ 1) : 0], kWithV);
             if (kt + 2 < kt1) load_tile(kh, vh, kt + 2, kend, kWithV, regs);
         }
         __syncthreads();
@@ -435,10 +508,20 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
         return;
     }
 
+    // PASS 3: the column's sum over the 4 lanes that hold its keys (fixed order; every lane gets the same value)
+    double lt[kQB];
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+        lt[qb] = sum[qb];
+        if constexpr (PASS == 3) {
+            lt[qb] += __shfl_xor(lt[qb], 16, kWave);
+            lt[qb] += __shfl_xor(lt[qb], 32, kWave);
+        }
+    }
     if (it.cut) {
-        // Publish this part's O (thread-major: element e of every thread is 512 consecutive float4), then
-        // count; the second part to arrive adds the first's O to its own.  With two addends the sum is
-        // the same whichever part arrives second.
+        // Publish this part's O (thread-major: element e of every thread is 512 consecutive float4; with a single
+        // pass also the max and sum of the thread's columns), then count; the second part to arrive combines
+        // both, in part order, so the result is the same whichever part arrives second.
         const int64_t unit = static_cast<int64_t>(g) * (p.n_qt - p.qt_cut) + (it.qt - p.qt_cut);
         uint64_t * mine = reinterpret_cast<uint64_t *>(p.partial + (unit * 2 + it.j) * kPfPartialFloats);
         const uint64_t * other = reinterpret_cast<const uint64_t *>(p.partial + (unit * 2 + (it.j ^ 1)) * kPfPartialFloats);
@@ -453,6 +536,16 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
                                    __HIP_MEMORY_SCOPE_AGENT);
             }
         }
+        constexpr int kStatOff = static_cast<int>(kPfOFloats / 2);    // uint64 offset of the (m, sum) entries
+        if constexpr (PASS == 3) {
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) {
+                const int e = kStatOff + static_cast<int>(threadIdx.x) * 4 + 2 * qb;
+                __hip_atomic_store(mine + e, pack2(m[qb], 0.0f), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(mine + e + 1, static_cast<uint64_t>(__double_as_longlong(lt[qb])), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         __shared__ int s_last;
@@ -464,6 +557,24 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
         }
         __syncthreads();
         if (!s_last) return;
+        // factors of this part (fm) and the other (fo) in the combined state (PASS 3; 1 for PASS 2)
+        float fm[kQB], fo[kQB];
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) {
+            fm[qb] = 1.0f;
+            fo[qb] = 1.0f;
+            if constexpr (PASS == 3) {
+                const int e = kStatOff + static_cast<int>(threadIdx.x) * 4 + 2 * qb;
+                const float mo = lo_float(__hip_atomic_load(other + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+                const double lo = __longlong_as_double(static_cast<long long>(
+                    __hip_atomic_load(other + e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
+                const float M = fmaxf(m[qb], mo);
+                fm[qb] = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m[qb] - M) * c);
+                fo[qb] = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((mo - M) * c);
+                const double a = lt[qb] * static_cast<double>(fm[qb]), b = lo * static_cast<double>(fo[qb]);
+                lt[qb] = it.j == 0 ? a + b : b + a;
+            }
+        }
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) {
 #pragma unroll
@@ -471,8 +582,19 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
                 const int e = ((qb * 8 + db) * kPfThreads + static_cast<int>(threadIdx.x)) * 2;
                 const uint64_t lo = __hip_atomic_load(other + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 const uint64_t hi = __hip_atomic_load(other + e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                O[qb][db] += f4{lo_float(lo), hi_float(lo), lo_float(hi), hi_float(hi)};
+                const f4 ov = f4{lo_float(lo), hi_float(lo), lo_float(hi), hi_float(hi)} * fo[qb];
+                const f4 mv = O[qb][db] * fm[qb];
+                O[qb][db] = it.j == 0 ? mv + ov : ov + mv;
             }
+        }
+    }
+    if constexpr (PASS == 3) {
+        // O / sum, with the sum's reciprocal in f32 (the reference's soft_max multiplies by 1 / sum)
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) {
+            const float r = lt[qb] > 0.0 ? static_cast<float>(1.0 / lt[qb]) : 0.0f;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) O[qb][db] *= r;
         }
     }
 
@@ -499,7 +621,7 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
 template <int PASS>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_mfma_kernel(MfmaParams p) {
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][kBK * kKS];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[PASS == 2 ? 2 : 1][PASS == 2 ? kHeadDim * kVS : 8];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[PASS != 1 ? 2 : 1][PASS != 1 ? kHeadDim * kVS : 8];
     __shared__ int s_pull;
     const int g = static_cast<int>(blockIdx.x) % p.n_kv;
     // workgroups serving head g, hence pulls past the end of its queue
@@ -522,6 +644,18 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_mfma_kernel(MfmaParams 
 }
 
 }  // namespace
+
+// QA_PREFILL_EXACT=1: the two-pass kernels, which round the normalised probabilities to f16 before PV as
+// the reference's GGML graph does (soft_max_ext, then mul_mat converting p to the f16 dot type of V).  The
+// default single pass rounds exp(s - m) to f16 instead and divides by the sum at the end: same f32
+// accumulation, another rounding point of p, attention outputs within 1.2e-4 of the oracle at T = 3913.
+bool prefill_exact() {
+    static const bool v = [] {
+        const char * e = std::getenv("QA_PREFILL_EXACT");
+        return e && std::strcmp(e, "1") == 0;
+    }();
+    return v;
+}
 
 // Workgroups of one pass that fit on the device at once (the size of the pulling grid).
 template <int PASS>
@@ -591,6 +725,11 @@ int prefill_mfma_launch(const float * q, int32_t q_stride, const void * k, const
         return dim3(static_cast<unsigned>(std::min(total, gsz)));
     };
     p.queue = reinterpret_cast<uint32_t *>(base);
+    if (!prefill_exact()) {
+        hipLaunchKernelGGL(prefill_mfma_kernel<3>, grid_of(resident_grid<3>()), dim3(kPfThreads), 0, stream, p);
+        QA_LAUNCH_CHECK("prefill_mfma_kernel<3>");
+        return QA_OK;
+    }
     hipLaunchKernelGGL(prefill_mfma_kernel<1>, grid_of(resident_grid<1>()), dim3(kPfThreads), 0, stream, p);
     QA_LAUNCH_CHECK("prefill_mfma_kernel<1>");
     p.queue = reinterpret_cast<uint32_t *>(base) + kPfMaxHeads * kPfCounterStride;

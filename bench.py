@@ -641,10 +641,23 @@ def main():
             f"(device ms per step by family: {r['family_ms_per_step']})")
         return r
 
+    def ms_decode_packed():
+        # the opt-in packed f32 GEMMs (QA_GR_PACKED=1, read at decoder creation): q|k|v, o and the LM head on
+        # weights reordered for the f32 MFMA; another summation order than the default kernels
+        os.environ["QA_GR_PACKED"] = "1"
+        try:
+            r = multistream_decode(qa, model, args.multistream_steps)
+        finally:
+            del os.environ["QA_GR_PACKED"]
+        log(f"config-4 decode with the packed f32 GEMMs: {r['ms_per_step']:.2f} ms per step")
+        return r
+
     guarded(result, "roofline_f32_cache", f32_cache)
     guarded(result, "roofline_multistream", ms_roof)
     guarded(result, "roofline_multistream_4k", ms_roof4k)
     guarded(result, "multistream_decode", ms_decode)
+    if args.weights == "f32":
+        guarded(result, "multistream_decode_packed_f32", ms_decode_packed)
     if args.no_cpu_baseline:
         result["cpu_baseline"] = None
     else:

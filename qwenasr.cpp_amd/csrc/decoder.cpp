@@ -46,6 +46,10 @@ struct DevLayer {
     uint16_t * o3 = nullptr;
     uint16_t * gu3 = nullptr;
     uint16_t * down3 = nullptr;
+    // q|k|v and o f32 rows packed for the multi-stream step's MFMA GEMM (gemm_packed.hip): multi-stream
+    // decoders on f32 weights only
+    float * qkv_p = nullptr;
+    float * o_p = nullptr;
 };
 
 enum Kind { kDecode = 0, kPrefill = 1, kNoCache = 2 };
@@ -80,6 +84,7 @@ struct qa_decoder {
     float * out_norm = nullptr;
     float * out_w = nullptr;
     uint16_t * out_w16 = nullptr;
+    float * out_p = nullptr;            // the LM head packed like DevLayer::qkv_p
     std::vector<void *> weight_allocs;
     std::vector<void *> b16_allocs;     // the bf16 weight copies (freed again if the model is not exact)
     void * cache = nullptr;
@@ -101,7 +106,7 @@ struct qa_decoder {
     size_t gr_ws_bytes = 0;
     void * pf_ws = nullptr;      // prefill attention: row statistics, split partials, merge counters
     size_t pf_ws_bytes = 0;
-    double * xstats = nullptr;   // [hidden / 32][32] partial sums of squares of the rows of x (fused steps)
+    double * xstats = nullptr;   // [hidden / 16][32] partial sums of squares of the rows of x (fused steps)
     int32_t * d_ids = nullptr;
     int32_t * h_ids = nullptr;   // pinned
     int32_t * h_ids_dev = nullptr;   // the same memory as the device addresses it
@@ -213,7 +218,8 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
         if (rc == QA_OK) d->gr_ws_bytes = gr;
     }
     if (rc == QA_OK && rows >= 2) {
-        const size_t n = static_cast<size_t>((H + 31) / 32) * 32;
+        // room for 16-column partials (the packed o projection) as well as 32-column ones
+        const size_t n = static_cast<size_t>((H + 15) / 16) * 32;
         rc = dmalloc(d->act_allocs, n * sizeof(double), reinterpret_cast<void **>(&d->xstats));
     }
     // bf16 copies: longer GEMM inputs are split into three bf16 parts ([rows][3 in_dim]) for the bf16 GEMM
@@ -362,11 +368,13 @@ int fused_gemm(qa_decoder * d, const float * W, int32_t N, int32_t K, const floa
     return gemm_rows_launch(W, N, K, X, rows, Y, accumulate, d->gr_ws, d->gr_ws_bytes, d->stream, &f, W16);
 }
 
-GemmRowsFusion norm_in(const qa_decoder * d, const float * norm_w) {
+// cols: columns per partial sum of squares in d->xstats, as the producer of x wrote them (32: embedding gather,
+// pick tail, gemm_rows32_kernel; 16: the packed o projection)
+GemmRowsFusion norm_in(const qa_decoder * d, const float * norm_w, int32_t cols = 32) {
     GemmRowsFusion f;
     f.norm_w = norm_w;
     f.stats_in = d->xstats;
-    f.n_stats_in = (d->cfg.hidden + 31) / 32;
+    f.n_stats_in = (d->cfg.hidden + cols - 1) / cols;
     f.eps = d->cfg.rms_norm_eps;
     return f;
 }
@@ -401,7 +409,9 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
             rc = gemv_launch(kEpiStoreOp, true, L.qkv, W3, H, d->x, d->qkv, L.attn_norm, c.rms_norm_eps, s,
                              L.qkv16);
         } else if (fused) {
-            rc = fused_gemm(d, L.qkv, W3, H, d->x, rows, d->qkv, false, norm_in(d, L.attn_norm), L.qkv16);
+            const GemmRowsFusion f = norm_in(d, L.attn_norm);
+            rc = L.qkv_p ? gemm_packed_launch(L.qkv_p, W3, H, d->x, rows, d->qkv, false, &f, false, s)
+                         : fused_gemm(d, L.qkv, W3, H, d->x, rows, d->qkv, false, f, L.qkv16);
         } else {
             // the RMSNorm writes the GEMM's split input directly where the GEMM takes one
             const bool sp = split_path(d, rows, H, L.qkv3, L.qkv16);
@@ -448,9 +458,15 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
         }
         if (rc == QA_OK) rc = gemv_launch(kEpiAccumOp, false, L.down, H, I, d->act, d->x, nullptr, 0.0f, s, L.down16);
     } else if (fused) {
-        GemmRowsFusion gu = norm_in(d, L.ffn_norm);
+        // the packed o projection leaves 16-column partial sums of squares of x for the gate|up RMSNorm
+        GemmRowsFusion gu = norm_in(d, L.ffn_norm, L.o_p ? 16 : 32);
         gu.swiglu = true;
-        rc = fused_gemm(d, L.o, H, QD, d->attn, rows, d->x, true, stats_out(d), L.o16);
+        if (L.o_p) {
+            const GemmRowsFusion so = stats_out(d);
+            rc = gemm_packed_launch(L.o_p, H, QD, d->attn, rows, d->x, true, &so, false, s);
+        } else {
+            rc = fused_gemm(d, L.o, H, QD, d->attn, rows, d->x, true, stats_out(d), L.o16);
+        }
         if (rc == QA_OK) rc = fused_gemm(d, L.gu, 2 * I, H, d->x, rows, d->act, false, gu, L.gu16);
         if (rc == QA_OK) rc = fused_gemm(d, L.down, H, I, d->act, rows, d->x, true, stats_out(d), L.down16);
     } else {
@@ -477,8 +493,9 @@ int logits_and_pick(qa_decoder * d, int32_t first, int32_t rows, bool pick, bool
             rc = gemv_launch(kEpiStoreOp, true, d->out_w, c.vocab, c.hidden, xr, d->logits, d->out_norm,
                              c.rms_norm_eps, d->stream, d->out_w16);
         } else if (fused && first == 0) {
-            rc = fused_gemm(d, d->out_w, c.vocab, c.hidden, xr, rows, d->logits, false, norm_in(d, d->out_norm),
-                            d->out_w16);
+            const GemmRowsFusion f = norm_in(d, d->out_norm);
+            rc = d->out_p ? gemm_packed_launch(d->out_p, c.vocab, c.hidden, xr, rows, d->logits, false, &f, true, d->stream)
+                          : fused_gemm(d, d->out_w, c.vocab, c.hidden, xr, rows, d->logits, false, f, d->out_w16);
         } else {
             rc = rmsnorm_rows_launch(xr, d->out_norm, rows, c.hidden, c.rms_norm_eps, d->xn, d->stream);
             if (rc == QA_OK) rc = sgemm(d, d->out_w, c.vocab, c.hidden, d->xn, rows, d->logits, 0.0f);
@@ -614,6 +631,32 @@ int pack_weights_bf16(qa_decoder * d) {
     return rc;
 }
 
+// QA_GR_PACKED=1, multi-stream decoders on f32 weights: the q|k|v and o rows of every layer and the LM head
+// packed for gemm_packed.hip's MFMA GEMMs (2.65 GB beside the 6.88 GB of f32 weights for the 1.7B model).
+// Opt-in: they sum in another order than gemm_rows32_kernel, and on config 4 that order takes the oracle's
+// runner-up at one near-tie (stream 11, step 36, oracle top-2 margin 4.3e-4), where the default kernel agrees.
+int pack_weights_mfma(qa_decoder * d) {
+    if (d->n_streams < 2 || d->layers.empty() || d->layers[0].qkv16) return QA_OK;
+    const char * e = std::getenv("QA_GR_PACKED");
+    if (!e || std::strcmp(e, "1") != 0) return QA_OK;
+    const qa_text_config & c = d->cfg;
+    const int32_t H = c.hidden, QD = c.n_heads * kHeadDim, KD = c.n_kv_heads * kHeadDim;
+    int rc = QA_OK;
+    auto pack = [&](const float * src, int32_t N, int32_t K, float ** dst) {
+        if (rc != QA_OK) return;
+        rc = dmalloc_t(d->weight_allocs, static_cast<size_t>(N) * K, dst);
+        if (rc == QA_OK) rc = pack_f32_launch(src, N, K, *dst, d->stream);
+    };
+    if (packed_gemm_shape_ok(QD + 2 * KD, H, false) && packed_gemm_shape_ok(H, QD, false)) {
+        for (DevLayer & L : d->layers) {
+            pack(L.qkv, QD + 2 * KD, H, &L.qkv_p);
+            pack(L.o, H, QD, &L.o_p);
+        }
+    }
+    if (d->out_w && packed_gemm_shape_ok(c.vocab, H, true)) pack(d->out_w, c.vocab, H, &d->out_p);
+    return rc;
+}
+
 }  // namespace
 
 extern "C" int qa_decoder_weights_bf16(const qa_decoder * d) {
@@ -703,6 +746,7 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
     }
     if (rc != QA_OK) return bail(rc);
     rc = pack_weights_bf16(d);
+    if (rc == QA_OK) rc = pack_weights_mfma(d);
     if (rc == QA_OK && !d->layers.empty() && d->max_seq > kSkinnyRows && (d->layers[0].qkv3 || d->layers[0].qkv16)) {
         // hipBLASLt for the prefill GEMMs over the bf16 rows, tripled or not (its workspace: 64 MiB)
         d->lt_ws_bytes = size_t(64) << 20;

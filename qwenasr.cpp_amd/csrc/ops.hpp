@@ -37,6 +37,17 @@ bool gemm_rows_fusable(int32_t N, int32_t K, int32_t rows);
 int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int32_t rows, float * Y, bool accumulate,
                      void * workspace, size_t workspace_bytes, hipStream_t stream,
                      const GemmRowsFusion * fusion = nullptr, const uint16_t * W16 = nullptr);
+// f32 weights packed for the multi-stream projections (gemm_packed.hip): Wp = W [N][K] reordered into the
+// A-operand order of the f32 MFMA (N % 16 == 0, K % 32 == 0; same size as W).
+int pack_f32_launch(const float * W, int32_t N, int32_t K, float * Wp, hipStream_t stream);
+// Shapes the packed GEMM takes: layer projections N % 16 == 0 with K 1024 or 2048; the LM head N % 128 == 0 and
+// K % 256 == 0.
+bool packed_gemm_shape_ok(int32_t N, int32_t K, bool lm_head);
+// Y[rows][N] (+)= X[rows][K] W[N][K]^T from packed weights, 1..32 rows, with the fusion's RMSNorm input and
+// stats_out ([N / 16][32]: 16-column partial sums of squares of the stored rows).  lm_head: the 128-row kernel
+// (RMSNorm input, plain store).
+int gemm_packed_launch(const float * Wp, int32_t N, int32_t K, const float * X, int32_t rows, float * Y, bool accumulate,
+                       const GemmRowsFusion * fusion, bool lm_head, hipStream_t stream);
 size_t argmax_workspace_bytes(int32_t rows);
 // What the decode step's last kernel does after picking row r's id (each part optional): lens[r] += 1,
 // host_ids[r] = id (a device-visible pointer into pinned host memory), and the picked token's

@@ -155,8 +155,47 @@ def test_config4_ragged_streams_match_golden(qa, greedy, bf16):
         assert [dec.cur_len(s) for s in range(w.streams)] == (lens + w.steps).tolist()
 
 
+def _with_env(name, value, fn):
+    old = os.environ.get(name)
+    os.environ[name] = value
+    try:
+        return fn()
+    finally:
+        if old is None:
+            os.environ.pop(name, None)
+        else:
+            os.environ[name] = old
+
+
+def test_config4_packed_f32_gemms(qa, greedy):
+    """QA_GR_PACKED=1 (read at decoder creation): config 4 with the f32 weights on the packed multi-stream GEMMs
+    (q|k|v, o and LM head on weights reordered for the f32 MFMA, gemm_packed.hip).  They sum in another order
+    than the default kernels, so the comparison runs in its own tie group (at most one accepted near-tie), and the
+    bookkeeping stays exact."""
+    from qwenasr_amd import configs
+
+    g = golden(4, False)
+    w = configs.CONFIGS[4]
+    lens = configs.cfg4_lengths(w.streams)
+    first = configs.cfg4_first_ids(w.streams)
+    model = qa.Model(w.size, n_layers=w.n_layers)
+    dec = _with_env("QA_GR_PACKED", "1", lambda: qa.Decoder(model, w.streams, w.max_seq, w.cache_type))
+    with dec:
+        for s in range(w.streams):
+            k, v = configs.cfg4_stream_kv(s, int(lens[s]))
+            dec.fill_cache(s, k, v, int(lens[s]))
+            del k, v
+        print("config 4 (packed f32 GEMMs) caches filled", flush=True)
+        ids = dec.decode_streams(first, w.steps)
+        for s, ref in g["streams"].items():
+            greedy.match(ids[:, int(s)].tolist(), ref["ids"], ref["margins"], ref["runner_up"],
+                         f"config 4 (packed f32 GEMMs) stream {s}", tie_group="config 4 packed f32")
+        assert dec.device_lens().tolist() == (lens + w.steps).tolist()
+
+
 @pytest.mark.parametrize("n_streams", [2, 5, 32])
-def test_few_streams_match_oracle(qa, orc, greedy, n_streams):
+@pytest.mark.parametrize("packed", [False, True])
+def test_few_streams_match_oracle(qa, orc, greedy, n_streams, packed):
     """The multi-stream decode step at 2..32 streams (fused RMSNorm / SwiGLU skinny GEMMs, per-stream
     lengths) against the oracle decoding each stream alone: 0.6B shapes, 2 layers, f16 cache, ragged
     contexts, 4 greedy steps; ids identical up to an oracle near-tie."""
@@ -168,7 +207,8 @@ def test_few_streams_match_oracle(qa, orc, greedy, n_streams):
     lens = rng.integers(20, 180, n_streams)
     first = rng.integers(0, model.cfg.vocab, n_streams).astype(np.int32)
     steps, cap = 4, 200
-    with qa.Decoder(model, n_streams, cap, qa.QA_CACHE_F16) as dec:
+    dec = _with_env("QA_GR_PACKED", "1" if packed else "0", lambda: qa.Decoder(model, n_streams, cap, qa.QA_CACHE_F16))
+    with dec:
         refs = []
         for s in range(n_streams):
             k, v = configs.cfg4_stream_kv(1000 + s, int(lens[s]), n_layers=2)
@@ -180,7 +220,8 @@ def test_few_streams_match_oracle(qa, orc, greedy, n_streams):
         print(f"{n_streams} streams: oracle done", flush=True)
         got = dec.decode_streams(first, steps)
         for s in range(n_streams):
-            greedy.match(got[:, s].tolist(), *refs[s], f"{n_streams}-stream step, stream {s}")
+            greedy.match(got[:, s].tolist(), *refs[s],
+                         f"{n_streams}-stream step{' (packed f32 GEMMs)' if packed else ''}, stream {s}")
         assert dec.device_lens().tolist() == (lens + steps).tolist()
 
 

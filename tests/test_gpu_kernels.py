@@ -397,6 +397,55 @@ def test_prefill_attention_long_split_rows(qa, orc, f16):
         check_close(got[t], row)
 
 
+_EXACT_PREFILL_CHILD = r"""
+import ctypes as C, os, sys
+import numpy as np
+root = sys.argv[1]
+sys.path[:0] = [os.path.join(root, "qwenasr.cpp_amd"), os.path.join(root, "oracle")]
+import qwenasr_amd as qa, qa_oracle as orc
+scale = 1.0 / np.sqrt(128.0)
+for n_past, T in ((0, 5), (0, 300), (600, 700), (0, 3913)):
+    L = n_past + T
+    lay = qa.KvLayout(1, 1, 8, 128, L + 3, qa.QA_CACHE_F16)
+    rng = np.random.default_rng(L + 17)
+    host = np.zeros((1, 2, 1, 8, L + 3, 128), np.float16)
+    host[0, :, 0, :, :L] = rng.standard_normal((2, 8, L, 128))
+    k = host[0, 0, 0, :, :L].astype(np.float32)
+    v = host[0, 1, 0, :, :L].astype(np.float32)
+    q = rng.standard_normal((T, 16, 128)).astype(np.float32)
+    cache, d_q, out = qa.DeviceArray.from_numpy(host), qa.DeviceArray.from_numpy(q), qa.DeviceArray((T, 2048))
+    wsb = qa.lib.qa_prefill_attn_workspace_bytes(T, 16)
+    ws = qa.DeviceArray(wsb, np.uint8)
+    print(f"exact prefill n_past={n_past} T={T}", flush=True)
+    qa.check(qa.lib.qa_prefill_attn(d_q.ptr, cache.ptr, C.byref(lay), 0, 0, n_past, T, 16, scale, out.ptr, ws.ptr,
+                                    wsb, None))
+    got = out.numpy().reshape(T, 16, 128).astype(np.float64)
+    ref = orc.cache_attention(k, v, q, n_past, True).astype(np.float64)
+    err = np.abs(got - ref).reshape(T, -1).max(axis=1)
+    rel = np.linalg.norm((got - ref).reshape(T, -1), axis=1) / np.linalg.norm(ref.reshape(T, -1), axis=1)
+    # the two passes round p where the oracle does: an order of magnitude inside the 2e-3 / 1e-3 bar
+    assert err.max() <= 2e-4 and rel.max() <= 2e-4, (n_past, T, err.max(), rel.max())
+    print(f"  max abs {err.max():.2e}, max rel L2 {rel.max():.2e}", flush=True)
+print("exact prefill ok", flush=True)
+"""
+
+
+def test_prefill_attention_exact_two_pass(qa):
+    """QA_PREFILL_EXACT=1 (read once per process, so in a child process): the two-pass kernels, which round the
+    normalised probabilities to f16 where the reference does, on every row against the oracle at a bar ten times
+    tighter than the path's (2e-4), including the config-3 shape with cut tiles and a prefix of cached keys."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, QA_PREFILL_EXACT="1")
+    r = subprocess.run([sys.executable, "-c", _EXACT_PREFILL_CHILD, root], env=env, capture_output=True, text=True,
+                       timeout=110)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and "exact prefill ok" in r.stdout
+
+
 # fixed region of the prefill workspace: queue counters (4 KB) + 8192 merge counters of 256 bytes
 PF_FIXED = 4096 + 8192 * 256
 

@@ -237,6 +237,14 @@ int qa_gemm_rows_fused_bf16(const uint16_t * W_bf16, int32_t out_dim, int32_t in
                             float * y, int32_t accumulate, const float * norm_w, const double * stats_in,
                             int32_t n_stats_in, float eps, double * stats_out, int32_t swiglu,
                             void * workspace, size_t workspace_bytes, void * stream);
+/* The prefill GEMM on bf16-exact weights (T > 32 rows), replacing linear_ggml (text-decoder.cpp:83-90)  *
+ * there: x_split = [rows][3 in_dim] bf16 bits, each row the three-part split [hi | mid | lo] of an f32  *
+ * input row (x = hi + mid + lo exactly), and y[rows][out_dim] (+)= sum of the three parts times W^T:    *
+ * exact f32 products, f32 sums (bf16 MFMA).  in_dim % 64 == 0, out_dim % 256 == 0.  With act_split    *
+ * != NULL (y NULL, accumulate 0) W_bf16 = [gate rows; up rows] (2 out_dim rows, out_dim % 128 == 0)    *
+ * and act_split[rows][3 out_dim] receives the split of silu(gate) * up (text-decoder.cpp:602).         */
+int qa_gemm_split3_bf16(const uint16_t * W_bf16, int32_t out_dim, int32_t in_dim, const uint16_t * x_split,
+                        int32_t rows, float * y, int32_t accumulate, uint16_t * act_split, void * stream);
 
 /* y[r][o] = sum_i W[o][i] * x[r][i]  (+ y[r][o] when accumulate != 0); rows small (decode).     */
 int qa_gemv(const float * W, int32_t out_dim, int32_t in_dim, const float * x, int32_t rows,

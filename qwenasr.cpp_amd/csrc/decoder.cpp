@@ -7,16 +7,13 @@
 //   greedy generate 2209-2311 (prefill, then argmax / stop check / break before the last forward)
 // with the data path replaced by the kernels of this library.
 #include <hip/hip_runtime.h>
-#include <hipblaslt/hipblaslt.h>
 #include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
-#include <map>
 #include <string>
-#include <tuple>
 #include <vector>
 
 #include "ops.hpp"
@@ -40,12 +37,6 @@ struct DevLayer {
     uint16_t * o16 = nullptr;
     uint16_t * gu16 = nullptr;
     uint16_t * down16 = nullptr;
-    // each bf16 row three times ([N][3 K]), for the prefill GEMMs over the three-part split of their
-    // input (decoders whose capacity allows prefills longer than the skinny GEMM's rows)
-    uint16_t * qkv3 = nullptr;
-    uint16_t * o3 = nullptr;
-    uint16_t * gu3 = nullptr;
-    uint16_t * down3 = nullptr;
     // q|k|v and o f32 rows packed for the multi-stream step's MFMA GEMM (gemm_packed.hip): multi-stream
     // decoders on f32 weights only
     float * qkv_p = nullptr;
@@ -61,24 +52,11 @@ const char * kFamNames[kFamCount] = {"kv_append", "decode_attn", "prefill_attn",
 
 }  // namespace
 
-// One hipBLASLt GEMM shape of the prefill projections: descriptors and the algorithm the library's
-// heuristic ranks first (a fixed choice per shape, so a prompt's results do not depend on timing).
-struct LtPlan {
-    hipblasLtMatmulDesc_t desc = nullptr;
-    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
-    hipblasLtMatmulAlgo_t algo{};
-    bool ok = false;
-};
-
 struct qa_decoder {
     qa_text_config cfg{};
     int32_t n_streams = 0, max_seq = 0, cache_type = 0;
     hipStream_t stream = nullptr;
     rocblas_handle blas = nullptr;
-    hipblasLtHandle_t lt = nullptr;           // prefill GEMMs on bf16 copies
-    void * lt_ws = nullptr;
-    size_t lt_ws_bytes = 0;
-    std::map<std::tuple<int32_t, int32_t, int32_t, int32_t>, LtPlan> lt_plans;   // (M, N, K, ldb)
     std::vector<DevLayer> layers;
     float * embd = nullptr;
     float * out_norm = nullptr;
@@ -97,6 +75,7 @@ struct qa_decoder {
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *qrot = nullptr, *attn = nullptr, *gu = nullptr, *act = nullptr;
     uint16_t * xsplit = nullptr;   // [rows][3 in_dim] bf16: three-part split of a GEMM input (bf16 copies)
     size_t xsplit_elems = 0;       // a third of its size: rows x max in_dim
+    uint16_t * actsplit = nullptr; // [rows][3 intermediate] bf16: split of silu(gate) * up (fused SwiGLU)
     float * logits = nullptr;    // [n_streams][vocab]
     void * attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
@@ -176,6 +155,7 @@ void free_acts(qa_decoder * d) {
     d->xstats = nullptr;
     d->xsplit = nullptr;
     d->xsplit_elems = 0;
+    d->actsplit = nullptr;
 }
 
 // Workspace of the skinny GEMM for the layer projections at up to `rows` token rows and the LM head at
@@ -222,10 +202,12 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
         const size_t n = static_cast<size_t>((H + 15) / 16) * 32;
         rc = dmalloc(d->act_allocs, n * sizeof(double), reinterpret_cast<void **>(&d->xstats));
     }
-    // bf16 copies: longer GEMM inputs are split into three bf16 parts ([rows][3 in_dim]) for the bf16 GEMM
-    if (rc == QA_OK && rows > kSkinnyRows && !d->layers.empty() && (d->layers[0].qkv3 || d->layers[0].qkv16)) {
+    // bf16 copies: longer GEMM inputs are split into three bf16 parts ([rows][3 in_dim]) for the bf16 GEMM,
+    // and the fused SwiGLU writes its split output beside the gate|up input
+    if (rc == QA_OK && rows > kSkinnyRows && !d->layers.empty() && d->layers[0].qkv16) {
         d->xsplit_elems = R * std::max({H, QD, I});
         rc = dmalloc_t(d->act_allocs, 3 * d->xsplit_elems, &d->xsplit);
+        rc = rc ? rc : dmalloc_t(d->act_allocs, 3 * R * I, &d->actsplit);
     }
     // prefill attention over up to `rows` tokens (counters cleared once; every call leaves them zero)
     const size_t pf = rows >= 2 ? qa_prefill_attn_workspace_bytes(rows, d->cfg.n_heads) : 0;
@@ -244,103 +226,39 @@ int ensure_rows(qa_decoder * d, int32_t rows) {
     return QA_OK;
 }
 
-// C[N][M] (column-major M x N) = beta C + A^T B: A = [M][K] and B = [N][K] bf16 rows (row stride ldb), f32
-// accumulation and output, on hipBLASLt with the heuristic's first algorithm for the shape.
-void lt_free(LtPlan & pl) {
-    if (pl.a) hipblasLtMatrixLayoutDestroy(pl.a);
-    if (pl.b) hipblasLtMatrixLayoutDestroy(pl.b);
-    if (pl.c) hipblasLtMatrixLayoutDestroy(pl.c);
-    if (pl.desc) hipblasLtMatmulDescDestroy(pl.desc);
-    pl = LtPlan{};
-}
-
-int lt_gemm(qa_decoder * d, int32_t M, int32_t N, int32_t K, const uint16_t * A, const uint16_t * B, int32_t ldb,
-            float beta, float * C) {
-    // N is the prompt length: a serving loop meets many, so the plans are dropped once 256 have piled up
-    // (a plan holds host-side descriptors only; the calls that used them were enqueued with their values)
-    const auto key = std::make_tuple(M, N, K, ldb);
-    if (d->lt_plans.size() >= 256 && d->lt_plans.find(key) == d->lt_plans.end()) {
-        for (auto & kv : d->lt_plans) lt_free(kv.second);
-        d->lt_plans.clear();
-    }
-    LtPlan & pl = d->lt_plans[key];
-    if (!pl.ok) {
-        const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-        bool ok = hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
-                  hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) == HIPBLAS_STATUS_SUCCESS &&
-                  hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) == HIPBLAS_STATUS_SUCCESS &&
-                  hipblasLtMatrixLayoutCreate(&pl.a, HIP_R_16BF, K, M, K) == HIPBLAS_STATUS_SUCCESS &&
-                  hipblasLtMatrixLayoutCreate(&pl.b, HIP_R_16BF, K, N, ldb) == HIPBLAS_STATUS_SUCCESS &&
-                  hipblasLtMatrixLayoutCreate(&pl.c, HIP_R_32F, M, N, M) == HIPBLAS_STATUS_SUCCESS;
-        hipblasLtMatmulPreference_t pref = nullptr;
-        if (ok) {
-            const uint64_t wsb = d->lt_ws_bytes;
-            ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
-                 hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
-                                                       sizeof(wsb)) == HIPBLAS_STATUS_SUCCESS;
-        }
-        if (ok) {
-            hipblasLtMatmulHeuristicResult_t res[1];
-            int got = 0;
-            ok = hipblasLtMatmulAlgoGetHeuristic(d->lt, pl.desc, pl.a, pl.b, pl.c, pl.c, pref, 1, res, &got) ==
-                     HIPBLAS_STATUS_SUCCESS &&
-                 got >= 1 && res[0].state == HIPBLAS_STATUS_SUCCESS && res[0].workspaceSize <= d->lt_ws_bytes;
-            if (ok) pl.algo = res[0].algo;
-        }
-        if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-        if (!ok) {
-            lt_free(pl);
-            d->lt_plans.erase(key);
-            return fail(QA_ERR_DEVICE, "hipBLASLt: no algorithm for the prefill GEMM");
-        }
-        pl.ok = true;
-    }
-    const float alpha = 1.0f;
-    if (hipblasLtMatmul(d->lt, pl.desc, &alpha, A, pl.a, B, pl.b, &beta, C, pl.c, C, pl.c, &pl.algo, d->lt_ws,
-                        d->lt_ws_bytes, d->stream) != HIPBLAS_STATUS_SUCCESS) {
-        return fail(QA_ERR_DEVICE, "hipblasLtMatmul failed");
-    }
-    return QA_OK;
-}
-
 bool skinny_path(const qa_decoder * d, int32_t rows, int32_t in_dim) {
     return rows <= kSkinnyRows && in_dim % 32 == 0 && d->gr_ws;
 }
 
 // Whether sgemm runs the bf16 GEMM over the three-part split of its input (then the producer of the
-// input may write d->xsplit itself, see sgemm's x_split).  W3: the tripled bf16 rows; W16: the bf16 rows.
-bool split_path(const qa_decoder * d, int32_t rows, int32_t in_dim, const uint16_t * W3, const uint16_t * W16) {
-    return !skinny_path(d, rows, in_dim) && (W3 || W16) && d->lt && d->xsplit &&
-           static_cast<size_t>(rows) * in_dim <= d->xsplit_elems;
+// input may write d->xsplit itself, see sgemm's x_split).  W16: the bf16 rows; swiglu: the fused SwiGLU
+// GEMM (out_dim = intermediate, W16 = [gate rows; up rows]).
+bool split_path(const qa_decoder * d, int32_t rows, int32_t out_dim, int32_t in_dim, const uint16_t * W16,
+                bool swiglu = false) {
+    return !skinny_path(d, rows, in_dim) && W16 && d->xsplit && static_cast<size_t>(rows) * in_dim <= d->xsplit_elems &&
+           gemm_split3_shape_ok(out_dim, in_dim, swiglu);
 }
 
 int sgemm(qa_decoder * d, const float * W, int32_t out_dim, int32_t in_dim, const float * X, int32_t rows, float * Y,
-          float beta, const uint16_t * W3 = nullptr, const uint16_t * W16 = nullptr, bool x_split = false) {
+          float beta, const uint16_t * W16 = nullptr, const uint16_t * x_split = nullptr) {
     // Y[rows][out] (+)= X[rows][in] * W[out][in]^T.  Up to kSkinnyRows rows (multi-stream decode, short
-    // prefills) the weights are streamed once by the skinny MFMA GEMM; longer prefills use hipBLASLt on
+    // prefills) the weights are streamed once by the skinny MFMA GEMM; longer prefills run gemm_split3 on
     // the bf16 copies, or rocBLAS sgemm on f32 weights.  x_split: the producer of X already wrote its
-    // three-part split into d->xsplit (only where split_path holds).
-    if (x_split && !split_path(d, rows, in_dim, W3, W16)) {
+    // three-part split there (only where split_path holds).
+    if (x_split && !split_path(d, rows, out_dim, in_dim, W16)) {
         return fail(QA_ERR_INVALID, "sgemm: split input without split path");
     }
     if (skinny_path(d, rows, in_dim)) {
         return gemm_rows_launch(W, out_dim, in_dim, X, rows, Y, beta != 0.0f, d->gr_ws, d->gr_ws_bytes, d->stream);
     }
-    if (split_path(d, rows, in_dim, W3, W16)) {
-        // bf16-exact weights: each row of X split into three bf16 parts, X = hi + mid + lo exactly.  With the
-        // tripled rows, Y = [W W W] [hi; mid; lo]: one bf16 GEMM over 3 in_dim with f32 accumulation -- every
-        // product exact, the sums in f32, Y written once.  Without them (a decoder created with
-        // QA_PREFILL_TRIPLED=0), three GEMMs over the one bf16 copy, the second and third accumulating into Y
-        // (beta 1): the same exact products, Y written three times and read twice.
+    if (split_path(d, rows, out_dim, in_dim, W16)) {
+        // bf16-exact weights: each row of X split into three bf16 parts, X = hi + mid + lo exactly, and one
+        // bf16 MFMA GEMM over the one bf16 copy uses every W tile for the three parts: every product exact,
+        // the sums in f32 (gemm_split3.hip)
         const int rc = x_split ? QA_OK : split_bf16x3_rows_launch(X, rows, in_dim, d->xsplit, d->stream);
         if (rc != QA_OK) return rc;
-        if (W3) return lt_gemm(d, out_dim, rows, 3 * in_dim, W3, d->xsplit, 3 * in_dim, beta, Y);
-        int r = QA_OK;
-        for (int part = 0; part < 3 && r == QA_OK; ++part) {
-            r = lt_gemm(d, out_dim, rows, in_dim, W16, d->xsplit + static_cast<size_t>(part) * in_dim, 3 * in_dim,
-                        part == 0 ? beta : 1.0f, Y);
-        }
-        return r;
+        return gemm_split3_launch(W16, out_dim, in_dim, x_split ? x_split : d->xsplit, rows, Y, beta != 0.0f, nullptr,
+                                  d->stream);
     }
     // column-major C(out x rows) = W^T(out x in) * X(in x rows)
     const float alpha = 1.0f;
@@ -414,9 +332,9 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
                          : fused_gemm(d, L.qkv, W3, H, d->x, rows, d->qkv, false, f, L.qkv16);
         } else {
             // the RMSNorm writes the GEMM's split input directly where the GEMM takes one
-            const bool sp = split_path(d, rows, H, L.qkv3, L.qkv16);
+            const bool sp = split_path(d, rows, W3, H, L.qkv16);
             rc = rmsnorm_rows_launch(d->x, L.attn_norm, rows, H, c.rms_norm_eps, d->xn, s, sp ? d->xsplit : nullptr);
-            if (rc == QA_OK) rc = sgemm(d, L.qkv, W3, H, d->xn, rows, d->qkv, 0.0f, L.qkv3, L.qkv16, sp);
+            if (rc == QA_OK) rc = sgemm(d, L.qkv, W3, H, d->xn, rows, d->qkv, 0.0f, L.qkv16, sp ? d->xsplit : nullptr);
         }
         if (rc != QA_OK) return rc;
     }
@@ -470,12 +388,19 @@ int run_layer(qa_decoder * d, int32_t l, int32_t rows, int kind, int32_t n_past,
         if (rc == QA_OK) rc = fused_gemm(d, L.gu, 2 * I, H, d->x, rows, d->act, false, gu, L.gu16);
         if (rc == QA_OK) rc = fused_gemm(d, L.down, H, I, d->act, rows, d->x, true, stats_out(d), L.down16);
     } else {
-        const bool sg = split_path(d, rows, H, L.gu3, L.gu16), sd = split_path(d, rows, I, L.down3, L.down16);
-        rc = sgemm(d, L.o, H, QD, d->attn, rows, d->x, 1.0f, L.o3, L.o16);
+        rc = sgemm(d, L.o, H, QD, d->attn, rows, d->x, 1.0f, L.o16);
+        const bool sd = split_path(d, rows, H, I, L.down16) && d->actsplit;
+        // bf16 copies: gate|up with the SwiGLU in its epilogue, writing the split input of down directly
+        const bool fuse = sd && split_path(d, rows, I, H, L.gu16, true);
+        const bool sg = fuse || split_path(d, rows, 2 * I, H, L.gu16);
         if (rc == QA_OK) rc = rmsnorm_rows_launch(d->x, L.ffn_norm, rows, H, c.rms_norm_eps, d->xn, s, sg ? d->xsplit : nullptr);
-        if (rc == QA_OK) rc = sgemm(d, L.gu, 2 * I, H, d->xn, rows, d->gu, 0.0f, L.gu3, L.gu16, sg);
-        if (rc == QA_OK) rc = swiglu_rows_launch(d->gu, rows, I, d->act, s, sd ? d->xsplit : nullptr);
-        if (rc == QA_OK) rc = sgemm(d, L.down, H, I, d->act, rows, d->x, 1.0f, L.down3, L.down16, sd);
+        if (fuse) {
+            if (rc == QA_OK) rc = gemm_split3_launch(L.gu16, I, H, d->xsplit, rows, nullptr, false, d->actsplit, s);
+        } else {
+            if (rc == QA_OK) rc = sgemm(d, L.gu, 2 * I, H, d->xn, rows, d->gu, 0.0f, L.gu16, sg ? d->xsplit : nullptr);
+            if (rc == QA_OK) rc = swiglu_rows_launch(d->gu, rows, I, d->act, s, sd ? d->actsplit : nullptr);
+        }
+        if (rc == QA_OK) rc = sgemm(d, L.down, H, I, d->act, rows, d->x, 1.0f, L.down16, sd ? d->actsplit : nullptr);
     }
     return rc;
 }
@@ -605,27 +530,10 @@ int pack_weights_bf16(qa_decoder * d) {
                         hipStreamSynchronize(d->stream) != hipSuccess)) {
         rc = fail(QA_ERR_DEVICE, "bf16 weight check failed");
     }
-    // prefill GEMMs: each bf16 row three times (see sgemm), unless QA_PREFILL_TRIPLED=0 asks for the one bf16
-    // copy only (three GEMMs per projection instead of one; 8.5 GB less for the 1.7B model)
-    const char * tr = std::getenv("QA_PREFILL_TRIPLED");
-    const bool tripled = !(tr && std::strcmp(tr, "0") == 0);
-    if (rc == QA_OK && inexact == 0 && d->max_seq > kSkinnyRows && tripled) {
-        auto repeat3 = [&](const uint16_t * src, size_t N, size_t K, uint16_t ** dst) {
-            if (rc != QA_OK) return;
-            rc = dmalloc_t(d->b16_allocs, 3 * N * K, dst);
-            if (rc == QA_OK) rc = repeat3_rows_launch(src, static_cast<int64_t>(N), static_cast<int32_t>(K), *dst, d->stream);
-        };
-        for (DevLayer & L : d->layers) {
-            repeat3(L.qkv16, QD + 2 * KD, H, &L.qkv3);
-            repeat3(L.o16, H, QD, &L.o3);
-            repeat3(L.gu16, 2 * I, H, &L.gu3);
-            repeat3(L.down16, H, I, &L.down3);
-        }
-    }
     if (rc != QA_OK || inexact != 0) {
         for (void * p : d->b16_allocs) (void)hipFree(p);
         d->b16_allocs.clear();
-        for (DevLayer & L : d->layers) L.qkv16 = L.o16 = L.gu16 = L.down16 = L.qkv3 = L.o3 = L.gu3 = L.down3 = nullptr;
+        for (DevLayer & L : d->layers) L.qkv16 = L.o16 = L.gu16 = L.down16 = nullptr;
         d->out_w16 = nullptr;
     }
     return rc;
@@ -747,15 +655,6 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
     if (rc != QA_OK) return bail(rc);
     rc = pack_weights_bf16(d);
     if (rc == QA_OK) rc = pack_weights_mfma(d);
-    if (rc == QA_OK && !d->layers.empty() && d->max_seq > kSkinnyRows && (d->layers[0].qkv3 || d->layers[0].qkv16)) {
-        // hipBLASLt for the prefill GEMMs over the bf16 rows, tripled or not (its workspace: 64 MiB)
-        d->lt_ws_bytes = size_t(64) << 20;
-        if (hipblasLtCreate(&d->lt) != HIPBLAS_STATUS_SUCCESS) {
-            rc = fail(QA_ERR_DEVICE, "hipBLASLt handle creation failed");
-        } else if (hipMalloc(&d->lt_ws, d->lt_ws_bytes) != hipSuccess) {
-            rc = fail(QA_ERR_ALLOC, "hipBLASLt workspace allocation failed");
-        }
-    }
     if (rc != QA_OK) return bail(rc);
 
     d->layout.n_layers = cfg->n_layers;
@@ -809,9 +708,6 @@ extern "C" void qa_decoder_destroy(qa_decoder * d) {
     if (d->cache) (void)hipFree(d->cache);
     if (d->h_ids) (void)hipHostFree(d->h_ids);
     if (d->blas) rocblas_destroy_handle(d->blas);
-    for (auto & kv : d->lt_plans) lt_free(kv.second);
-    if (d->lt) hipblasLtDestroy(d->lt);
-    if (d->lt_ws) (void)hipFree(d->lt_ws);
     if (d->stream) (void)hipStreamDestroy(d->stream);
     delete d;
 }

@@ -12,6 +12,7 @@
 // read a bf16 copy (the high halves) and widen each value back to the same f32 in registers: the
 // products and sums are the f32 kernel's, operation for operation, at half the bytes.
 #include "ops.hpp"
+#include "split3.hpp"
 #include "wave.hpp"
 
 #include <algorithm>
@@ -930,19 +931,6 @@ GemmRowsPlan gemm_rows_plan(int32_t N, int32_t K, int32_t rows, bool one_slice =
 }
 
 // ---------------------------------------------------------------- row RMSNorm (T > 1 paths)
-// The exact three-part bf16 split of v (v = hi + mid + lo: truncations to 8 significant bits, then the
-// same of the remainder; the last remainder has at most 8 significant bits), stored as bf16 bits at
-// o[0], o[K], o[2 K]: the layout of one row of the prefill GEMM's split input.
-__device__ inline void store_split3(uint16_t * o, int64_t K, float v) {
-    const uint32_t h = __float_as_uint(v) & 0xffff0000u;
-    const float r1 = v - __uint_as_float(h);
-    const uint32_t m = __float_as_uint(r1) & 0xffff0000u;
-    const float r2 = r1 - __uint_as_float(m);
-    o[0] = static_cast<uint16_t>(h >> 16);
-    o[K] = static_cast<uint16_t>(m >> 16);
-    o[2 * K] = static_cast<uint16_t>(__float_as_uint(r2) >> 16);
-}
-
 // y = RMSNorm(x) w per row, as f32 rows of y or (split != null) as the three-part split rows of the
 // prefill GEMM's input ([rows][3 dim] bf16 bits)
 __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float * x, const float * w, int dim, float eps,
@@ -1163,29 +1151,6 @@ int split_bf16x3_rows_launch(const float * x, int64_t rows, int32_t K, uint16_t 
         hipLaunchKernelGGL(split_bf16x3_rows_kernel, grid, dim3(256), 0, stream, x + r0 * K, K, out + r0 * 3 * K);
         QA_LAUNCH_CHECK("split_bf16x3_rows_kernel");
     }
-    return QA_OK;
-}
-
-// dst row n = [src row n | src row n | src row n] (N rows of K bf16 values)
-__global__ __launch_bounds__(256) void repeat3_rows_kernel(const uint16_t * src, int64_t N, int32_t K, uint16_t * dst) {
-    const int64_t n = N * K;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) {
-        const int64_t r = i / K, k = i - r * K;
-        const uint16_t v = src[i];
-        uint16_t * o = dst + r * 3 * K + k;
-        o[0] = v;
-        o[K] = v;
-        o[2 * K] = v;
-    }
-}
-
-int repeat3_rows_launch(const uint16_t * src, int64_t N, int32_t K, uint16_t * dst, hipStream_t stream) {
-    if (!src || !dst || N < 0 || K <= 0) return fail(QA_ERR_INVALID, "repeat3_rows: invalid arguments");
-    if (N == 0) return QA_OK;
-    const int64_t blocks = std::min<int64_t>((N * K + 255) / 256, 8192);
-    hipLaunchKernelGGL(repeat3_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, src, N, K, dst);
-    QA_LAUNCH_CHECK("repeat3_rows_kernel");
     return QA_OK;
 }
 

@@ -12,8 +12,12 @@ int gemv_launch(int epi, bool prenorm, const float * W, int32_t out_dim, int32_t
                 const float * norm_w, float eps, hipStream_t stream, const uint16_t * W16 = nullptr);
 // out[t] = [hi | mid | lo] of x[t] (rows x K): the exact three-part bf16 split, x = hi + mid + lo (bf16 bits)
 int split_bf16x3_rows_launch(const float * x, int64_t rows, int32_t K, uint16_t * out, hipStream_t stream);
-// dst[n] = [src[n] | src[n] | src[n]] (N x K bf16 bits)
-int repeat3_rows_launch(const uint16_t * src, int64_t N, int32_t K, uint16_t * dst, hipStream_t stream);
+// Prefill GEMM on bf16-exact weights over the three-part split input (gemm_split3.hip):
+// Y[M][N] (+)= sum_p Xs[M][p K .. p K + K) W16[N][K]^T, f32 products and sums; with act != nullptr (Y null,
+// no accumulate) W16 = [gate rows; up rows] (2 N rows) and act[M][3 N] = split of silu(gate) * up.
+bool gemm_split3_shape_ok(int32_t N, int32_t K, bool swiglu);
+int gemm_split3_launch(const uint16_t * W16, int32_t N, int32_t K, const uint16_t * Xs, int32_t M, float * Y,
+                       bool accumulate, uint16_t * act, hipStream_t stream);
 // dst = high halves of src; *inexact |= 1 if any low half of src is non-zero
 int pack_bf16_launch(const float * src, int64_t n, uint16_t * dst, uint32_t * inexact, hipStream_t stream);
 // Y[rows][N] (+)= X[rows][K] W[N][K]^T for 1..64 rows (K a multiple of 32), f32 MFMA.

@@ -135,6 +135,7 @@ SIGNATURES = {
     "qa_gemm_rows": (C.c_int, vp, i32, i32, vp, i32, vp, i32, vp, sz, vp),
     "qa_gemm_rows_fused": (C.c_int, vp, i32, i32, vp, i32, vp, i32, vp, vp, i32, f32, vp, i32, vp, sz, vp),
     "qa_gemm_rows_fused_bf16": (C.c_int, vp, i32, i32, vp, i32, vp, i32, vp, vp, i32, f32, vp, i32, vp, sz, vp),
+    "qa_gemm_split3_bf16": (C.c_int, vp, i32, i32, vp, i32, vp, i32, vp, vp),
     "qa_model_weights_view": (C.c_int, vp, C.POINTER(LayerWeights), i32, C.POINTER(ModelWeights)),
     "qa_decoder_create": (C.c_int, C.POINTER(TextConfig), C.POINTER(ModelWeights), i32, i32, i32, C.POINTER(vp)),
     "qa_decoder_destroy": (None, vp),

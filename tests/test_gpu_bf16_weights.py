@@ -107,15 +107,13 @@ def test_pack_bf16_flags_inexact_values(qa, n):
     assert int(flag.numpy()[0]) == 1
 
 
-def _decoder(qa, model, max_seq, f32_weights, tripled=True):
-    """A decoder created with QA_WEIGHTS_F32=1 (f32_weights) and/or QA_PREFILL_TRIPLED=0 (not tripled); both
-    are read at creation, so the environment is restored right after."""
-    saved = {k: os.environ.pop(k, None) for k in ("QA_WEIGHTS_F32", "QA_PREFILL_TRIPLED")}
+def _decoder(qa, model, max_seq, f32_weights):
+    """A decoder created with QA_WEIGHTS_F32=1 (f32_weights), which is read at creation, so the environment
+    is restored right after."""
+    saved = {k: os.environ.pop(k, None) for k in ("QA_WEIGHTS_F32",)}
     try:
         if f32_weights:
             os.environ["QA_WEIGHTS_F32"] = "1"
-        if not tripled:
-            os.environ["QA_PREFILL_TRIPLED"] = "0"
         return qa.Decoder(model, 1, max_seq, qa.QA_CACHE_F16)
     finally:
         for k, v in saved.items():
@@ -226,6 +224,70 @@ def test_gemm_rows_bf16_rejects_unsupported_shapes(qa):
                                                 ws.ptr, 1 << 20, None))
 
 
+def split3(a):
+    """The exact three-part bf16 split of f32 values (a = hi + mid + lo), as bf16 bits [hi, mid, lo]."""
+    a = np.ascontiguousarray(a, np.float32)
+    hi = (a.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+    r1 = (a - hi).astype(np.float32)
+    mid = (r1.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+    lo = (r1 - mid).astype(np.float32)
+    assert np.array_equal((hi + mid) + lo, a)
+    return [high_halves(v) for v in (hi, mid, lo)]
+
+
+@pytest.mark.parametrize("rows,out_dim,in_dim,mode", [
+    (1, 256, 64, "store"), (73, 2048, 2048, "accumulate"), (300, 4096, 2048, "store"), (200, 1024, 3072, "swiglu"),
+    (3913, 4096, 2048, "store"), (3913, 2048, 6144, "accumulate"), (3913, 6144, 2048, "swiglu")])
+def test_gemm_split3_bf16_matches_float64(qa, rows, out_dim, in_dim, mode):
+    """The prefill GEMM on bf16-exact weights (rows > 32): bf16 MFMAs over the three-part split of each
+    input row against the one bf16 copy of W, every product exact, sums in f32.  Against float64 of the same
+    f32 inputs, at the 1.7B prefill shapes (T = 3913: q|k|v, down, gate|up) and at ragged row counts (the
+    last 128-row tile partly filled; 1 row).  Store, accumulate (the residual add of o and down) and the
+    SwiGLU epilogue, which writes the split of silu(gate) * up: its parts are checked bit for bit against
+    the split of the kernel's own values, and the values against float64."""
+    rng = np.random.default_rng(rows + out_dim + in_dim)
+    n_w = 2 * out_dim if mode == "swiglu" else out_dim
+    w = bf16_round(rng.standard_normal((n_w, in_dim)) * 0.02)
+    x = rng.standard_normal((rows, in_dim)).astype(np.float32)
+    xs = np.concatenate(split3(x), axis=1)                      # [rows][3 in_dim]
+    ref = x.astype(np.float64) @ w.T.astype(np.float64)
+    d_w = qa.DeviceArray.from_numpy(high_halves(w))
+    d_xs = qa.DeviceArray.from_numpy(xs)
+    print(f"gemm_split3 rows={rows} {out_dim}x{in_dim} {mode}", flush=True)
+    if mode == "swiglu":
+        d_a = qa.DeviceArray.from_numpy(np.zeros((rows, 3 * out_dim), np.uint16))
+        qa.check(qa.lib.qa_gemm_split3_bf16(d_w.ptr, out_dim, in_dim, d_xs.ptr, rows, None, 0, d_a.ptr, None))
+        qa.synchronize()
+        a = d_a.numpy()
+        parts = [(a[:, p * out_dim:(p + 1) * out_dim].astype(np.uint32) << 16).view(np.float32) for p in range(3)]
+        v = (parts[0] + parts[1]) + parts[2]
+        assert all(np.array_equal(got, want) for got, want in
+                   zip((a[:, p * out_dim:(p + 1) * out_dim] for p in range(3)), split3(v)))
+        g, u = ref[:, :out_dim], ref[:, out_dim:]
+        np.testing.assert_allclose(v, g / (1.0 + np.exp(-g)) * u, rtol=1e-5, atol=1e-5)
+        return
+    y0 = rng.standard_normal((rows, out_dim)).astype(np.float32)
+    d_y = qa.DeviceArray.from_numpy(y0 if mode == "accumulate" else np.zeros_like(y0))
+    qa.check(qa.lib.qa_gemm_split3_bf16(d_w.ptr, out_dim, in_dim, d_xs.ptr, rows, d_y.ptr,
+                                        int(mode == "accumulate"), None, None))
+    qa.synchronize()
+    want = ref + y0 if mode == "accumulate" else ref
+    np.testing.assert_allclose(d_y.numpy(), want, rtol=1e-5, atol=1e-5)
+
+
+def test_gemm_split3_bf16_rejects_unsupported_shapes(qa):
+    d = qa.DeviceArray((1 << 16,), np.float32)
+    for args in ((d.ptr, 300, 64, d.ptr, 130, d.ptr, 0, None),      # out_dim % 256
+                 (d.ptr, 256, 96, d.ptr, 130, d.ptr, 0, None),      # in_dim % 64
+                 (None, 256, 64, d.ptr, 130, d.ptr, 0, None),       # no weights
+                 (d.ptr, 256, 64, d.ptr, 0, d.ptr, 0, None),        # no rows
+                 (d.ptr, 256, 64, d.ptr, 130, d.ptr, 0, d.ptr),     # SwiGLU writes the split, not y
+                 (d.ptr, 192, 64, d.ptr, 130, None, 0, d.ptr)):     # SwiGLU: out_dim % 128
+        with pytest.raises(qa.QaError) as e:
+            qa.check(qa.lib.qa_gemm_split3_bf16(*args, None))
+        assert e.value.code == qa.QA_ERR_INVALID
+
+
 @pytest.mark.parametrize("n_streams", [5, 32])
 def test_bf16_weights_multistream_equals_f32_weights_and_oracle(qa, orc, greedy, n_streams):
     """The multi-stream decode step with bf16-exact weights: the bf16-copy decoder (bf16 MFMAs) and the
@@ -264,13 +326,11 @@ def test_bf16_weights_multistream_equals_f32_weights_and_oracle(qa, orc, greedy,
                          f"bf16-exact weights ({name}), {n_streams}-stream step, stream {s}")
 
 
-@pytest.mark.parametrize("tripled", [True, False])
-def test_bf16_weights_long_prefill_matches_oracle(qa, orc, greedy, tripled):
+def test_bf16_weights_long_prefill_matches_oracle(qa, orc, greedy):
     """A 300-position prompt (longer than the 64 rows of the skinny GEMM): with bf16 copies each prefill
-    projection is one hipBLASLt bf16 GEMM over the exact three-part split of its input against the tripled
-    weight rows, or (QA_PREFILL_TRIPLED=0) three GEMMs over the one bf16 copy accumulating into the output
-    (exact products, f32 sums either way).  Logits against the oracle and against the f32-weight decoder,
-    then greedy ids."""
+    projection is one bf16 MFMA GEMM (gemm_split3) over the exact three-part split of its input and the one
+    bf16 copy of the weights, gate|up with the SwiGLU fused (exact products, f32 sums).  Logits against the
+    oracle and against the f32-weight decoder, then greedy ids."""
     model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=3, bf16=True)
     om = orc.OracleModel.from_product_model(model)
     x = qa.prompt_input(model, 290, 10)
@@ -279,7 +339,7 @@ def test_bf16_weights_long_prefill_matches_oracle(qa, orc, greedy, tripled):
     ref = om.generate(x, N, qa.STOP_IDS, om.cache(300 + N, True))
     logits = {}
     for f32_weights in (False, True):
-        with _decoder(qa, model, 300 + N, f32_weights, tripled) as dec:
+        with _decoder(qa, model, 300 + N, f32_weights) as dec:
             assert dec.weights_bf16 == (not f32_weights)
             logits[f32_weights] = dec.forward(x, 0)
             if not f32_weights:
@@ -290,13 +350,13 @@ def test_bf16_weights_long_prefill_matches_oracle(qa, orc, greedy, tripled):
         assert err <= 2e-3 and rel <= 1e-3, (err, rel)
     assert float(np.abs(logits[False].astype(np.float64) - logits[True]).max()) <= 2e-3
     assert greedy.match(out["ids"], ref["ids"], ref["margins"], ref["runner_up"],
-                        f"bf16-exact weights, 300-position prompt ({'tripled rows' if tripled else 'one bf16 copy'})") is None
+                        "bf16-exact weights, 300-position prompt") is None
 
 
 def test_bf16_prefill_many_prompt_lengths(qa, orc):
-    """More distinct prompt lengths than the decoder keeps GEMM plans for (256; one per length): every
-    prefill of lengths 65..334 runs, and the last-row logits of lengths before and after the plans are
-    dropped match the oracle's at the prefill tolerance."""
+    """Every prompt length 65..334: the prefill GEMM's 128-row token tiles end at every possible
+    remainder (its rows past the prompt are clamped on load and skipped on store).  Each prefill runs, and
+    the last-row logits of lengths 65, 200, 320 and 334 match the oracle's at the prefill tolerance."""
     model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=1, bf16=True)
     om = orc.OracleModel.from_product_model(model)
     x_all = qa.prompt_input(model, 324, 10)

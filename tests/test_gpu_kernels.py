@@ -668,6 +668,32 @@ def test_argmax_rows_rule(qa, orc):
         assert d_ids.numpy().tolist() == [orc.argmax(r) for r in rows] == [int(np.argmax(rows[0])), 5, 77777, -1]
 
 
+@pytest.mark.parametrize("V", [151936, 200000, 1000])
+def test_argmax_ties_within_one_thread(qa, orc, V):
+    """Each thread scans its elements (256 apart) in batches of loads; ties between elements of one thread, in
+    one batch and across batches (V = 200000: 13 elements per thread), keep the lowest index, and a larger value
+    in a later batch still wins.  V = 1000: most threads have no element (clamped loads are skipped)."""
+    rng = np.random.default_rng(V)
+    chunk = (V + 63) // 64
+    base = 3 * chunk + 7                                        # thread 7 of block 3
+    a = rng.standard_normal(V).astype(np.float32)
+    b = rng.standard_normal(V).astype(np.float32)
+    if V >= 100000:
+        a[[base, base + 256 * 4]] = 40.0                        # one batch
+        b[[base + 256 * 2, base + 256 * 11 if V > 160000 else base + 256 * 9]] = [40.0, 41.0]
+        want = [base, base + 256 * 11 if V > 160000 else base + 256 * 9]
+    else:
+        a[[3, 700]] = 40.0
+        b[999] = 40.0
+        want = [3, 999]
+    d_l, d_ids = dev(qa, np.stack([a, b])), zeros(qa, 2, np.int32)
+    ws_bytes = qa.lib.qa_argmax_workspace_bytes(2)
+    ws = zeros(qa, ws_bytes, np.uint8)
+    qa.check(qa.lib.qa_argmax_rows(d_l.ptr, 2, V, d_ids.ptr, ws.ptr, ws_bytes, NULL_STREAM))
+    qa.synchronize()
+    assert d_ids.numpy().tolist() == [orc.argmax(a), orc.argmax(b)] == want
+
+
 def test_embed_and_lens(qa):
     table = np.arange(10 * 2048, dtype=np.float32).reshape(10, 2048)
     d_t, d_ids = dev(qa, table), dev(qa, np.array([3, -1, 9, 10], np.int32))

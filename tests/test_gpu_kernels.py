@@ -557,11 +557,12 @@ def _row_stats(y, n_out):
 
 
 @pytest.mark.parametrize("out_dim,in_dim,rows", [(4096, 2048, 32), (2048, 2048, 7), (12288, 2048, 32),
-                                                  (2048, 6144, 32), (1056, 1024, 5)])
+                                                  (2048, 6144, 32), (1056, 1024, 5), (34816, 2048, 32)])
 def test_gemm_rows_fused(qa, out_dim, in_dim, rows):
     """Fused skinny GEMM against float64: RMSNorm input from partial sums of squares (the normalised
     row computed in f32 as the RMSNorm kernel does), accumulate + sums of squares of the stored rows,
-    and the SwiGLU epilogue over [gate rows; up rows]."""
+    and the SwiGLU epilogue over [gate rows; up rows].  34816 rows: more than 1024 tiles of 32 rows (the LM
+    head's regime)."""
     rng = np.random.default_rng(out_dim * 3 + in_dim + rows)
     eps = np.float32(1e-6)
     w = (rng.standard_normal((out_dim, in_dim)) * 0.02).astype(np.float32)

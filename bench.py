@@ -39,6 +39,7 @@ sys.path[:0] = [os.path.join(ROOT, "qwenasr.cpp_amd")]
 
 METRIC = "decode tok/s + KV-attn HBM GB/s (% of peak), Qwen3-ASR-1.7B decoder, 1 GPU"
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0   # dense f16 / bf16 MFMA, MI355X
 
 
 def log(msg: str):
@@ -447,6 +448,34 @@ def capacity_plan(prompt: int, warmup: int, steps: int, profile_steps: int, bf16
             "bf16_exact": prompt + warmup + bf16_steps + 2}
 
 
+def prefill_attn_roofline(cfg, T: int, fam_ms: dict):
+    """Causal prefill attention on f16 MFMA from the prefill's event-bracketed family time: useful FLOPs
+    4 n_heads head_dim T (T + 1) / 2 per layer (QK^T and PV over the unmasked half)."""
+    flop = 4.0 * cfg.n_heads * cfg.head_dim * T * (T + 1) / 2 * cfg.n_layers
+    ms = fam_ms["prefill_attn"]
+    tf = flop / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+            "kernel": "prefill_mfma_kernel (f16 MFMA, single pass), all layers of one prefill",
+            "flop_per_layer": round(flop / cfg.n_layers), "positions": T, "ms": ms}
+
+
+def prefill_gemm_roofline(cfg, T: int, fam_ms: dict):
+    """The bf16-exact prefill projections (gemm_split3: bf16 MFMA over the three-part split of each input, so
+    3 x 2 T params FLOPs of MFMA work per layer) from the projection family's time, which also holds the
+    RMSNorm and split passes: a lower bound on the GEMM's own rate."""
+    H, QD, KD, I = cfg.hidden, cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim, cfg.intermediate
+    params = (QD + 2 * KD) * H + H * QD + 2 * I * H + H * I
+    flop = 3.0 * 2.0 * T * params * cfg.n_layers
+    ms = fam_ms["projections"]
+    tf = flop / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+            "kernel": "gemm_split3_kernel (bf16 MFMA over the split input, SwiGLU fused), the prefill's projection "
+                      "family (with its RMSNorm and split passes)", "flop_per_layer": round(flop / cfg.n_layers),
+            "positions": T, "ms": ms}
+
+
 def guarded(result: dict, key: str, fn):
     """Runs one secondary leg; a failure is recorded under result[key] = {"error": ...} instead of ending
     the run, so the measurements taken before it still reach the JSON line."""
@@ -652,6 +681,7 @@ def main():
         log(f"config-4 decode with the packed f32 GEMMs: {r['ms_per_step']:.2f} ms per step")
         return r
 
+    guarded(result, "roofline_prefill_attn", lambda: prefill_attn_roofline(model.cfg, w.prompt, main_leg["prefill_family_ms"]))
     guarded(result, "roofline_f32_cache", f32_cache)
     guarded(result, "roofline_multistream", ms_roof)
     guarded(result, "roofline_multistream_4k", ms_roof4k)
@@ -678,6 +708,8 @@ def main():
             leg["weight_bytes_per_token"] = weight_bytes(model, 2 if streamed else 4)
             log(f"bf16-exact weights: {leg['ms_per_step']:.4f} ms/token ({leg['tok_s']:.1f} tok/s), prefill "
                 f"{leg['prefill_ms']:.1f} ms")
+            if streamed and leg.get("prefill_family_ms"):
+                leg["roofline_prefill_gemm"] = prefill_gemm_roofline(model.cfg, w.prompt, leg["prefill_family_ms"])
             r4 = multistream_decode(qa, model, max(4, args.multistream_steps // 2))
             leg["multistream_decode"] = r4
             log(f"bf16-exact weights, config-4 decode: {r4['ms_per_step']:.2f} ms per step")

@@ -109,3 +109,20 @@ def test_parser_defaults_and_gpus_guard(capsys):
     assert r.returncode == 2 and "one GPU" in r.stderr
     src = open(os.path.join(ROOT, "bench.py")).read()
     assert 'ap.add_argument("--weights", choices=["f32", "bf16-exact"], default="f32"' in src
+
+
+def test_prefill_rooflines():
+    """The prefill MFMA roofline objects: causal attention FLOPs at T = 3913 are BASELINE's 62.73 GFLOP per
+    layer (4 x 16 x 128 x T (T + 1) / 2), the split-input GEMM does 3 x 2 T params per layer (50.33 M params
+    per 1.7B layer), and the rate is FLOPs over the family's milliseconds."""
+    import types
+
+    cfg = types.SimpleNamespace(n_heads=16, head_dim=128, n_layers=28, hidden=2048, n_kv_heads=8, intermediate=6144)
+    a = bench.prefill_attn_roofline(cfg, 3913, {"prefill_attn": 28 * 62.732214272e9 / 1e15 * 1e3})   # 1 PFLOP/s
+    assert a["flop_per_layer"] == 62732214272
+    assert abs(a["achieved"] - 1000.0) < 0.1 and a["bound"] == "mfma" and abs(a["frac"] - 0.4) < 1e-4
+    params = (2048 + 2 * 1024) * 2048 + 2048 * 2048 + 2 * 6144 * 2048 + 2048 * 6144
+    assert params == 50331648
+    g = bench.prefill_gemm_roofline(cfg, 3913, {"projections": 30.0})
+    assert g["flop_per_layer"] == 6 * 3913 * params
+    assert abs(g["achieved"] - 28 * 6 * 3913 * params / 30e-3 / 1e12) < 0.1

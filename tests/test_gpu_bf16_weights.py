@@ -237,12 +237,14 @@ def split3(a):
 
 @pytest.mark.parametrize("rows,out_dim,in_dim,mode", [
     (1, 256, 64, "store"), (73, 2048, 2048, "accumulate"), (300, 4096, 2048, "store"), (200, 1024, 3072, "swiglu"),
+    (300, 768, 128, "accumulate"), (129, 384, 192, "swiglu"),
     (3913, 4096, 2048, "store"), (3913, 2048, 6144, "accumulate"), (3913, 6144, 2048, "swiglu")])
 def test_gemm_split3_bf16_matches_float64(qa, rows, out_dim, in_dim, mode):
     """The prefill GEMM on bf16-exact weights (rows > 32): bf16 MFMAs over the three-part split of each
     input row against the one bf16 copy of W, every product exact, sums in f32.  Against float64 of the same
     f32 inputs, at the 1.7B prefill shapes (T = 3913: q|k|v, down, gate|up) and at ragged row counts (the
-    last 128-row tile partly filled; 1 row).  Store, accumulate (the residual add of o and down) and the
+    last 128-row tile partly filled; 1 row); 768 and 384 output columns split into 3 column tiles, which take
+    the plain tile order instead of the per-XCD one.  Store, accumulate (the residual add of o and down) and the
     SwiGLU epilogue, which writes the split of silu(gate) * up: its parts are checked bit for bit against
     the split of the kernel's own values, and the values against float64."""
     rng = np.random.default_rng(rows + out_dim + in_dim)

@@ -644,6 +644,8 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
         }
     };
     if (my > 0) {
+        // (a wave with fewer than P blocks re-reads its last one: no branch around a load here, which would
+        // leave the wait counts of the loop below unknown)
 #pragma unroll
         for (int u = 0; u < P; ++u) load(u, u);
     }
@@ -732,22 +734,29 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };
-    if (my > 0) {
-        const int full = my / P * P;
-        for (int b0 = 0; b0 < full; b0 += P) {
+    // block b is computed from register set b % P; the loads of block b + P follow its arithmetic.  Only
+    // blocks of this wave are loaded, so nothing is in flight when the accumulators are summed.
+    const int full = my / P * P;
+    for (int b0 = 0; b0 + P < full; b0 += P) {
 #pragma unroll
-            for (int u = 0; u < P; ++u) {
-                compute(u);
-                load(u, b0 + P + u);
-                // keep the loads of block b + P right behind the arithmetic of block b
-                __builtin_amdgcn_sched_barrier(0);
-            }
+        for (int u = 0; u < P; ++u) {
+            compute(u);
+            load(u, b0 + P + u);
+            // keep the loads of block b + P right behind the arithmetic of block b
+            __builtin_amdgcn_sched_barrier(0);
         }
-        const int rem = my - full;
+    }
+    if (full > 0) {
+        // the last whole group of P blocks loads only the remaining my - full blocks
 #pragma unroll
-        for (int u = 0; u < P - 1; ++u) {
-            if (u < rem) compute(u);
+        for (int u = 0; u < P; ++u) {
+            compute(u);
+            if (u < my - full) load(u, full + u);
         }
+    }
+#pragma unroll
+    for (int u = 0; u < P - 1; ++u) {
+        if (u < my - full) compute(u);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     // sum the 4 waves (wave order) through LDS: accumulator entry i of lane (r, h) is row

@@ -426,7 +426,21 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
     for (int tb = 0; tb < TB; ++tb) acc[tb] += acc2[tb];
     // acc[tb][i] = sum for W row n0 + 4 g + i and token 16 tb + lane % 16
     const int nr = n0 + 4 * g;
+    // the old values of this lane's outputs (accumulate): loads issued together, addresses clamped to the
+    // matrix and no branch, so that they cost one round trip
+    auto old_values = [&](int tb) {
+        v4f o = v4f{};
+        if (p.accumulate) {
+            const float * y = p.Y + static_cast<int64_t>(min(16 * tb + (lane & 15), p.rows - 1)) * p.N;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = y[min(nr + i, p.N - 1)];
+        }
+        return o;
+    };
     if (p.ks == 1) {
+        v4f old[TB];
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) old[tb] = old_values(tb);
 #pragma unroll
         for (int tb = 0; tb < TB; ++tb) {
             const int t = 16 * tb + (lane & 15);
@@ -434,7 +448,7 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
             float * y = p.Y + static_cast<int64_t>(t) * p.N + nr;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                if (nr + i < p.N) y[i] = p.accumulate ? y[i] + acc[tb][i] : acc[tb][i];
+                if (nr + i < p.N) y[i] = p.accumulate ? old[tb][i] + acc[tb][i] : acc[tb][i];
             }
         }
         return;
@@ -500,6 +514,9 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
             }
         }
     }
+    v4f old[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) old[tb] = old_values(tb);
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) {
         const int t = 16 * tb + (lane & 15);
@@ -507,7 +524,7 @@ __global__ __launch_bounds__(256) void gemm_rows_kernel(GemmRowsParams p) {
         float * y = p.Y + static_cast<int64_t>(t) * p.N + nr;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if (nr + i < p.N) y[i] = p.accumulate ? y[i] + sum[tb][i] : sum[tb][i];
+            if (nr + i < p.N) y[i] = p.accumulate ? old[tb][i] + sum[tb][i] : sum[tb][i];
         }
     }
 }
@@ -534,6 +551,7 @@ constexpr int kG32Rows = 32;         // weight rows per workgroup (one MFMA bloc
 constexpr int kG32Blk = 64;          // k per block
 constexpr int kG32Ls = kG32Blk + 4;  // LDS row stride (floats)
 constexpr int kG32LsB = kG32Blk + 8; // LDS row stride of bf16 weight rows (elements: 144 B, 16 B aligned)
+constexpr int kG32MaxSlices = 8;     // K slices merged per tile group at most (gemm_rows_plan)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned int u4v __attribute__((ext_vector_type(4)));
@@ -808,14 +826,25 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
     }
     // store (or accumulate) the final values of tile t; with stats_out also the tile's per-token sum of
     // squares of the stored values (a workgroup-uniform step: every thread of the workgroup calls it)
-    auto finish = [&](int t, v4f v) {
+    // the old values of tile t's 4 outputs of this lane (accumulate), read by 4 loads issued together
+    // (addresses clamped to the matrix, no branch), so that they cost one round trip
+    auto old_values = [&](int t) {
+        v4f o = v4f{};
+        if (p.accumulate) {
+            const float * y = p.Y + static_cast<int64_t>(min(tk, p.rows - 1)) * p.N;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = y[min(nr[t] + i, p.N - 1)];
+        }
+        return o;
+    };
+    auto finish = [&](int t, v4f v, v4f old) {
         double ss = 0.0;
         if (live[t]) {
             float * y = p.Y + static_cast<int64_t>(tk) * p.N + nr[t];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 if (nr[t] + i < p.N) {
-                    const float o = p.accumulate ? y[i] + v[i] : v[i];
+                    const float o = p.accumulate ? old[i] + v[i] : v[i];
                     y[i] = o;
                     ss += static_cast<double>(o) * o;
                 }
@@ -835,8 +864,11 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
         }
     };
     if (p.ks == 1) {
+        v4f old[T];
 #pragma unroll
-        for (int t = 0; t < T; ++t) finish(t, sv[t]);
+        for (int t = 0; t < T; ++t) old[t] = old_values(t);
+#pragma unroll
+        for (int t = 0; t < T; ++t) finish(t, sv[t], old[t]);
         return;
     }
     // publish (partial rows padded to whole 4-row groups), then the last slice of the tile group merges in
@@ -866,26 +898,27 @@ __global__ __launch_bounds__(256) void gemm_rows32_kernel(GemmRowsParams p) {
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         const int nn = min(nr[t], np - 4);
-        float sum[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int k0 = 0; k0 < p.ks; k0 += 8) {
-            uint64_t v[8][2];
+        // one round of loads: the plan merges at most kG32MaxSlices slices; no loop, whose back edge would
+        // make the compiler wait for earlier loads before reusing their registers
+        uint64_t v[kG32MaxSlices][2];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int k = min(k0 + u, p.ks - 1);
-                const uint64_t * q = reinterpret_cast<const uint64_t *>(p.partial + (static_cast<int64_t>(k) * p.rows + tt) * np + nn);
-                v[u][0] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                v[u][1] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                if (k0 + u >= p.ks) break;
-                sum[0] += __uint_as_float(static_cast<uint32_t>(v[u][0]));
-                sum[1] += __uint_as_float(static_cast<uint32_t>(v[u][0] >> 32));
-                sum[2] += __uint_as_float(static_cast<uint32_t>(v[u][1]));
-                sum[3] += __uint_as_float(static_cast<uint32_t>(v[u][1] >> 32));
-            }
+        for (int u = 0; u < kG32MaxSlices; ++u) {
+            const int k = min(u, p.ks - 1);
+            const uint64_t * q = reinterpret_cast<const uint64_t *>(p.partial + (static_cast<int64_t>(k) * p.rows + tt) * np + nn);
+            v[u][0] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            v[u][1] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        finish(t, v4f{sum[0], sum[1], sum[2], sum[3]});
+        const v4f old = old_values(t);   // issued behind the partials' loads, waited for with them
+        float sum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < kG32MaxSlices; ++u) {
+            if (u >= p.ks) break;
+            sum[0] += __uint_as_float(static_cast<uint32_t>(v[u][0]));
+            sum[1] += __uint_as_float(static_cast<uint32_t>(v[u][0] >> 32));
+            sum[2] += __uint_as_float(static_cast<uint32_t>(v[u][1]));
+            sum[3] += __uint_as_float(static_cast<uint32_t>(v[u][1] >> 32));
+        }
+        finish(t, v4f{sum[0], sum[1], sum[2], sum[3]}, old);
     }
 }
 
@@ -919,7 +952,7 @@ GemmRowsPlan gemm_rows_plan(int32_t N, int32_t K, int32_t rows, bool one_slice =
         pl.tiles = (N + kG32Rows - 1) / kG32Rows;
         pl.tpw = b16 && pl.tiles % 2 == 0 && (pl.tiles > 1024 || forced_tpw == 2) && forced_tpw != 1 ? 2 : 1;
         const int groups = pl.tiles / pl.tpw;
-        int ks = std::max(1, std::min({(target_wgs + groups / 2) / groups, 8, K / (4 * kG32Blk)}));
+        int ks = std::max(1, std::min({(target_wgs + groups / 2) / groups, kG32MaxSlices, K / (4 * kG32Blk)}));
         if (groups > kGrMaxTiles || one_slice) ks = 1;             // counters exist for kGrMaxTiles groups
         pl.slice = ((K + ks - 1) / ks + kG32Blk - 1) / kG32Blk * kG32Blk;
         pl.ks = (K + pl.slice - 1) / pl.slice;

@@ -159,11 +159,13 @@ __global__ __launch_bounds__(kPkThreads) void gemm_packed_kernel(PackedParams p)
     const int tok = 16 * wave + r16;
     const bool live = tok < p.rows;
     float * y = p.Y + static_cast<int64_t>(min(tok, p.rows - 1)) * p.N + 16 * t + 4 * g;
+    // the 4 old values in one 16-byte load (N is a multiple of 16)
+    const f4 old = p.accumulate ? *reinterpret_cast<const f4 *>(y) : f4{};
     double ss = 0.0;
     if (live) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float o = p.accumulate ? y[i] + v[i] : v[i];
+            const float o = p.accumulate ? old[i] + v[i] : v[i];
             y[i] = o;
             ss += static_cast<double>(o) * o;
         }

@@ -284,7 +284,8 @@ def kernel_only(which: str, reps: int, weights: str = "f32"):
     (q/k norm + RoPE, f16 cache write); prefill: causal prefill attention over 3913 positions of one
     layer (f16 cache, n_past 0); decode-attn / decode-attn-f32: the decode-step attention of one layer
     at L = 4186 over an f16 / f32 cache, rotating 28 layer caches; decode-step: config 3 end to end at
-    batch 1 (prefill once, then reps greedy decode tokens); multistream: the config-4 decode step of 32
+    batch 1 (prefill once, then reps greedy decode tokens), decode-step-persistent the same with every
+    layer of a token in one persistent launch; multistream: the config-4 decode step of 32
     streams (end to end); multistream-attn: the decode-step attention of 32 streams at L = 4096 (reps x
     28 launch pairs).  weights: f32 or bf16-exact draws for the end-to-end modes."""
     if which == "multistream-attn":
@@ -302,7 +303,7 @@ def kernel_only(which: str, reps: int, weights: str = "f32"):
         model = qa.Model(w.size, n_layers=w.n_layers, bf16=weights == "bf16-exact")
         print(json.dumps(dict(kernel=which, weights=weights, **multistream_decode(qa, model, reps))), flush=True)
         return
-    if which == "decode-step":
+    if which in ("decode-step", "decode-step-persistent"):
         import numpy as np
         import qwenasr_amd as qa
         from qwenasr_amd import configs
@@ -311,6 +312,8 @@ def kernel_only(which: str, reps: int, weights: str = "f32"):
         model = qa.Model(w.size, n_layers=w.n_layers, bf16=weights == "bf16-exact")
         x = qa.prompt_input(model, w.audio_tokens, w.prompt_tokens)
         with qa.Decoder(model, 1, w.prompt + reps + 8, w.cache_type) as dec:
+            if which == "decode-step-persistent":
+                dec.set_persistent(True)
             logits = dec.forward(x, 0)
             ids = dec.decode_streams(np.array([int(np.argmax(logits))], np.int32), 2)
             qa.synchronize()
@@ -436,16 +439,19 @@ def multistream_decode(qa, model, steps: int):
                         f"lock-step greedy decode, f16 cache, {streamed} streamed"}
 
 
-def capacity_plan(prompt: int, warmup: int, steps: int, profile_steps: int, bf16_steps: int) -> dict:
+def capacity_plan(prompt: int, warmup: int, steps: int, profile_steps: int, bf16_steps: int,
+                  persistent_steps: int = 0) -> dict:
     """KV-cache capacity (positions per stream) of each decoder the bench creates, sized for the legs
     that decoder runs.  main: the prefill, the warm-up and timed decode steps, the event-bracketed
     profile steps, and the attention roofline, which appends at the context the decode left (row ctx)
-    and attends ctx + 1 positions.  bf16_exact: its own prefill, warm-up and timed steps.  One spare
-    position each, so a step count of zero still leaves the roofline a row to append."""
-    if min(prompt, warmup, steps, profile_steps, bf16_steps) < 0 or prompt < 1:
+    and attends ctx + 1 positions.  bf16_exact: its own prefill, warm-up and timed steps; persistent: the
+    same for the persistent decode step.  One spare position each, so a step count of zero still leaves
+    the roofline a row to append."""
+    if min(prompt, warmup, steps, profile_steps, bf16_steps, persistent_steps) < 0 or prompt < 1:
         raise ValueError("capacity_plan: counts must be non-negative and the prompt non-empty")
     return {"main": prompt + warmup + steps + profile_steps + 2,
-            "bf16_exact": prompt + warmup + bf16_steps + 2}
+            "bf16_exact": prompt + warmup + bf16_steps + 2,
+            "persistent": prompt + warmup + persistent_steps + 2}
 
 
 def prefill_attn_roofline(cfg, T: int, fam_ms: dict):
@@ -510,12 +516,14 @@ def decode_leg(qa, model, x, cache_type, capacity: int, warmup: int, steps: int,
     prefill_fam = {f: round(dec.profile_read(f)[0], 2) for f in ("projections", "kv_append", "prefill_attn", "logits")}
     dec.profile(False)
     ids = dec.decode_streams(np.array([first], np.int32), warmup) if warmup else np.array([[first]], np.int32)
+    all_ids = ids[:, 0].tolist() if warmup else []
     qa.check(qa.lib.qa_device_synchronize())
     ctx0 = dec.cur_len(0)
     t0 = time.perf_counter()
     ids = dec.decode_streams(np.array([int(ids[-1, 0])], np.int32), steps)
     qa.check(qa.lib.qa_device_synchronize())
     dt = time.perf_counter() - t0
+    all_ids += ids[:, 0].tolist()
     fam = None
     if profile_steps > 0:
         # per-step device time by kernel family (HIP events around each family; events add gaps, so these
@@ -528,7 +536,7 @@ def decode_leg(qa, model, x, cache_type, capacity: int, warmup: int, steps: int,
     return dec, {"steps": steps, "seconds": dt, "ctx0": ctx0, "ms_per_step": round(dt * 1e3 / steps, 4),
                  "tok_s": round(steps / dt, 3), "prefill_ms": round(prefill_ms, 2),
                  "prefill_first_call_ms": round(prefill_cold_ms, 2), "prefill_family_ms": prefill_fam,
-                 "family_ms_per_step": fam, "first_id": first}
+                 "family_ms_per_step": fam, "first_id": first, "ids": all_ids}
 
 
 def weight_bytes(model, elem: int) -> int:
@@ -558,10 +566,13 @@ def main():
     ap.add_argument("--bf16-steps", type=int, default=64,
                     help="decode steps timed on the same draws rounded to bf16 values, whose bf16 copies the "
                          "decoder streams (a secondary object of the line; 0: skip)")
+    ap.add_argument("--persistent-steps", type=int, default=32,
+                    help="decode steps timed with the persistent decode step (qa_decoder_set_persistent: every "
+                         "layer of a token in one launch), a secondary object of the line; 0: skip")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 10 times (reference for HBM traffic counters)")
     ap.add_argument("--kernel", choices=["append", "prefill", "decode-attn", "decode-attn-f32", "multistream",
-                                         "multistream-attn", "decode-step"],
+                                         "multistream-attn", "decode-step", "decode-step-persistent"],
                     help="only run one hot-path kernel on synthetic inputs (short program for rocprofv3 passes)")
     ap.add_argument("--kernel-reps", type=int, default=20)
     args = ap.parse_args()
@@ -587,7 +598,7 @@ def main():
         w = dataclasses.replace(w, cache_type=qa.QA_CACHE_F16 if args.kv_cache == "f16" else qa.QA_CACHE_F32)
     kv_name = "f16" if w.cache_type == qa.QA_CACHE_F16 else "f32"
     plan = capacity_plan(w.prompt, args.warmup, args.steps, args.profile_steps,
-                         args.bf16_steps if args.weights == "f32" else 0)
+                         args.bf16_steps if args.weights == "f32" else 0, args.persistent_steps)
     t0 = time.perf_counter()
     model = qa.Model(w.size, n_layers=w.n_layers, bf16=args.weights == "bf16-exact")
     x = qa.prompt_input(model, w.audio_tokens, w.prompt_tokens)
@@ -688,6 +699,37 @@ def main():
     guarded(result, "multistream_decode", ms_decode)
     if args.weights == "f32":
         guarded(result, "multistream_decode_packed_f32", ms_decode_packed)
+    def persistent_leg():
+        # the same decode with every layer of a token in one persistent launch (LM head and pick separate)
+        import numpy as np
+
+        d = qa.Decoder(model, 1, plan["persistent"], w.cache_type)
+        try:
+            d.set_persistent(True)
+            first = int(np.argmax(d.forward(x, 0)))
+            ids = d.decode_streams(np.array([first], np.int32), args.warmup) if args.warmup else np.array([[first]], np.int32)
+            got = ids[:, 0].tolist() if args.warmup else []
+            qa.check(qa.lib.qa_device_synchronize())
+            t0 = time.perf_counter()
+            ids = d.decode_streams(np.array([int(ids[-1, 0])], np.int32), args.persistent_steps)
+            qa.check(qa.lib.qa_device_synchronize())
+            dt_p = time.perf_counter() - t0
+            got += ids[:, 0].tolist()
+        finally:
+            d.close()
+        n = min(len(got), len(main_leg["ids"]))
+        r = {"steps": args.persistent_steps, "ms_per_step": round(dt_p * 1e3 / args.persistent_steps, 4),
+             "tok_s": round(args.persistent_steps / dt_p, 3),
+             "over_eager": round(dt_p / args.persistent_steps / (dt / args.steps), 3),
+             "ids_equal_eager": got[:n] == main_leg["ids"][:n], "ids_compared": n,
+             "mechanism": "one cooperative launch of 256 resident workgroups per token for all layers (grid "
+                          "barriers between the six phases of a layer), then the LM head and the pick"}
+        log(f"persistent decode step: {r['ms_per_step']:.4f} ms/token ({r['over_eager']:.2f}x the eager step), "
+            f"ids equal to the eager run: {r['ids_equal_eager']} ({n} compared)")
+        return r
+
+    if args.persistent_steps > 0:
+        guarded(result, "decode_persistent", persistent_leg)
     if args.no_cpu_baseline:
         result["cpu_baseline"] = None
     else:
@@ -704,6 +746,7 @@ def main():
             d16.close()
             leg.pop("seconds")
             leg.pop("first_id")
+            leg.pop("ids")
             leg["weights_streamed"] = "bf16 copies of bf16-exact weights" if streamed else "f32"
             leg["weight_bytes_per_token"] = weight_bytes(model, 2 if streamed else 4)
             log(f"bf16-exact weights: {leg['ms_per_step']:.4f} ms/token ({leg['tok_s']:.1f} tok/s), prefill "

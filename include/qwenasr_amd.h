@@ -419,6 +419,18 @@ int qa_decoder_generate(qa_decoder * dec, const float * x, int32_t n_tokens, int
 int qa_decoder_decode_streams(qa_decoder * dec, const int32_t * first_ids, int32_t n_steps,
                               int32_t * out_ids);
 
+/* Decode-step capture without a graph (text-decoder.cpp:1658-1739 rebuilds and schedules a graph per
+ * token): with enable = 1, every batch-1 decode step of this decoder (generate, and cached forwards of
+ * one token) runs all its layers as ONE persistent cooperative launch, whose resident workgroups walk
+ * the layers' six phases behind grid barriers, driven by the device-side length; the LM head and the
+ * pick follow as two launches.  Results are bit-identical to the eager step (same device code per
+ * phase).  QA_ERR_INVALID if no persistent kernel is instantiated for the decoder's shapes (streams,
+ * hidden/intermediate size, weight copies, cache dtype and the capacity's attention tiling); the decoder
+ * then stays eager.  Every barrier wait is bounded (200 ms): an abandoned launch makes the call that
+ * ran it return QA_ERR_DEVICE, and the decoder clears its barrier and merge state.  enable = 0 returns to
+ * the eager step.                                                                                  */
+int qa_decoder_set_persistent(qa_decoder * dec, int32_t enable);
+
 /* Copies host K/V rows into stream `stream`'s cache slot for every layer (config 4 prefill of
  * random K/V).  k, v: [n_layers][n_kv_heads][len][head_dim] f32 (cast to the cache dtype).      */
 int qa_decoder_fill_cache(qa_decoder * dec, int32_t stream, const float * k, const float * v, int32_t len);

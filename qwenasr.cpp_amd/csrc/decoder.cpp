@@ -47,8 +47,10 @@ enum Kind { kDecode = 0, kPrefill = 1, kNoCache = 2 };
 
 constexpr int32_t kSkinnyRows = 64;   // token rows up to which projections use the skinny MFMA GEMM
 
-enum Family { kFamAppend = 0, kFamDecodeAttn, kFamPrefillAttn, kFamProj, kFamLogits, kFamCount };
-const char * kFamNames[kFamCount] = {"kv_append", "decode_attn", "prefill_attn", "projections", "logits"};
+enum Family { kFamAppend = 0, kFamDecodeAttn, kFamPrefillAttn, kFamProj, kFamLogits, kFamLayers, kFamCount };
+// decode_layers: the persistent step's single launch (every layer's projections and attention)
+const char * kFamNames[kFamCount] = {"kv_append", "decode_attn", "prefill_attn", "projections", "logits",
+                                     "decode_layers"};
 
 }  // namespace
 
@@ -92,6 +94,21 @@ struct qa_decoder {
     float * staging = nullptr;
     size_t staging_bytes = 0;
     float scale = 0.0f;
+    // persistent decode step (qa_decoder_set_persistent): resident grid, barrier state, device layer table
+    bool persist = false;
+    bool persist_ran = false;          // a persistent launch since the last check of the error word
+    int32_t persist_grid = 0;
+    uint64_t persist_wait_ticks = 20000000;   // 200 ms; QA_PERSIST_WAIT_TICKS at enable time overrides it
+    uint32_t * persist_sync = nullptr;
+    size_t persist_sync_bytes = 0;
+    PersistLayer * persist_layers = nullptr;
+    // its per-layer activations and attention workspaces (every address written once per launch)
+    float * persist_xbuf = nullptr;
+    float * persist_qkv = nullptr;
+    float * persist_attn = nullptr;
+    float * persist_act = nullptr;
+    void * persist_ws = nullptr;
+    size_t persist_ws_bytes = 0;
     // profiling
     bool prof = false;
     struct Rec { int fam; hipEvent_t a, b; };
@@ -431,6 +448,63 @@ int logits_and_pick(qa_decoder * d, int32_t first, int32_t rows, bool pick, bool
     return argmax_launch(d->logits, rows, c.vocab, d->d_ids, d->am_ws, d->stream, tail);
 }
 
+PersistPlanIn persist_plan_in(const qa_decoder * d) {
+    PersistPlanIn in;
+    in.layout = d->layout;
+    in.hidden = d->cfg.hidden;
+    in.q_dim = d->cfg.n_heads * kHeadDim;
+    in.inter = d->cfg.intermediate;
+    in.b16 = !d->layers.empty() && d->layers[0].qkv16;
+    return in;
+}
+
+// Every layer of one batch-1 token (stream 0, position d_lens[0]) as one persistent launch; x holds the
+// token's input row and ends with the last layer's output, as after the eager layers.
+int persist_layers(qa_decoder * d, int32_t max_len) {
+    const qa_text_config & c = d->cfg;
+    PersistLaunch a;
+    a.plan = persist_plan_in(d);
+    a.grid = d->persist_grid;
+    a.layers = d->persist_layers;
+    a.n_layers = c.n_layers;
+    a.x = d->x;
+    a.xbuf = d->persist_xbuf;
+    a.qkv = d->persist_qkv;
+    a.attn = d->persist_attn;
+    a.act = d->persist_act;
+    a.cache = d->cache;
+    a.lens = d->d_lens;
+    a.max_len = max_len;
+    a.n_heads = c.n_heads;
+    a.eps = c.rms_norm_eps;
+    a.scale = d->scale;
+    a.rope_theta = c.rope_theta;
+    a.attn_ws = d->persist_ws;
+    a.attn_ws_bytes = d->persist_ws_bytes;
+    a.sync = d->persist_sync;
+    a.wait_ticks = d->persist_wait_ticks;
+    Prof pr(d, kFamLayers);
+    const int rc = persist_layers_launch(a, d->stream);
+    if (rc == QA_OK) d->persist_ran = true;
+    return rc;
+}
+
+// After a call that ran persistent launches: QA_ERR_DEVICE if one of them abandoned a barrier wait (its
+// results are invalid), after clearing the barrier state and the attention merge counters it left behind.
+int persist_check(qa_decoder * d) {
+    if (!d->persist_ran) return QA_OK;
+    d->persist_ran = false;
+    uint32_t err = 0;
+    QA_HIP(hipMemcpyAsync(&err, d->persist_sync + persist_error_word_offset(d->persist_grid), sizeof(err),
+                          hipMemcpyDeviceToHost, d->stream));
+    QA_HIP(hipStreamSynchronize(d->stream));
+    if (err == 0) return QA_OK;
+    QA_HIP(hipMemsetAsync(d->persist_sync, 0, d->persist_sync_bytes, d->stream));
+    QA_HIP(hipMemsetAsync(d->persist_ws, 0, d->persist_ws_bytes, d->stream));
+    QA_HIP(hipStreamSynchronize(d->stream));
+    return fail(QA_ERR_DEVICE, "persistent decode step: a grid barrier wait ran out, the call's results are invalid");
+}
+
 int check_forward(const qa_decoder * d, int32_t n_tokens, int32_t n_past) {
     if (n_tokens <= 0 || n_past < 0 || n_past + n_tokens > d->max_seq) {
         return fail(n_past + n_tokens > d->max_seq ? QA_ERR_CAPACITY : QA_ERR_INVALID,
@@ -445,9 +519,14 @@ int forward_device(qa_decoder * d, int32_t n_tokens, int32_t n_past, bool pick) 
     if (rc != QA_OK) return rc;
     d->cur_len[0] = n_past;
     const int kind = n_tokens == 1 ? kDecode : kPrefill;
-    for (int32_t l = 0; l < d->cfg.n_layers; ++l) {
-        rc = run_layer(d, l, n_tokens, kind, n_past);
+    if (d->persist && n_tokens == 1) {
+        rc = persist_layers(d, n_past + 1);
         if (rc != QA_OK) return rc;
+    } else {
+        for (int32_t l = 0; l < d->cfg.n_layers; ++l) {
+            rc = run_layer(d, l, n_tokens, kind, n_past);
+            if (rc != QA_OK) return rc;
+        }
     }
     rc = logits_and_pick(d, n_tokens - 1, 1, pick);
     if (rc != QA_OK) return rc;
@@ -468,8 +547,12 @@ int decode_step_ops(qa_decoder * d, int32_t rows, int32_t max_len, bool embed, i
         rc = embed_rows_launch(d->embd, d->cfg.vocab, d->cfg.hidden, d->d_ids, rows, d->x, d->stream,
                                fused ? d->xstats : nullptr);
     }
-    for (int32_t l = 0; l < d->cfg.n_layers && rc == QA_OK; ++l) {
-        rc = run_layer(d, l, rows, kDecode, 0, max_len, fused);
+    if (d->persist && rows == 1) {
+        if (rc == QA_OK) rc = persist_layers(d, max_len);
+    } else {
+        for (int32_t l = 0; l < d->cfg.n_layers && rc == QA_OK; ++l) {
+            rc = run_layer(d, l, rows, kDecode, 0, max_len, fused);
+        }
     }
     StepTail tail;
     tail.lens = d->d_lens;
@@ -754,7 +837,7 @@ extern "C" int qa_decoder_forward(qa_decoder * d, const float * x, int32_t n_tok
         QA_HIP(hipMemcpyAsync(logits, d->logits, sizeof(float) * d->cfg.vocab, hipMemcpyDeviceToHost, d->stream));
     }
     QA_HIP(hipStreamSynchronize(d->stream));
-    return QA_OK;
+    return persist_check(d);
 }
 
 extern "C" int qa_decoder_generate(qa_decoder * d, const float * x, int32_t n_tokens, int32_t max_new,
@@ -786,7 +869,10 @@ extern "C" int qa_decoder_generate(qa_decoder * d, const float * x, int32_t n_to
         }
         QA_HIP(hipStreamSynchronize(d->stream));
         const int32_t id = d->h_ids[0];
-        if (id < 0 || id >= V) return fail(QA_ERR_RANGE, "generated token id is out of range");
+        if (id < 0 || id >= V) {
+            rc = persist_check(d);
+            return rc != QA_OK ? rc : fail(QA_ERR_RANGE, "generated token id is out of range");
+        }
         if (margins) margins[step] = top2_margin(host_logits, id);
         out_ids[(*n_out)++] = id;
         *total_tokens = n_tokens + *n_out;
@@ -801,7 +887,7 @@ extern "C" int qa_decoder_generate(qa_decoder * d, const float * x, int32_t n_to
         if (rc != QA_OK) return rc;
     }
     QA_HIP(hipStreamSynchronize(d->stream));
-    return QA_OK;
+    return persist_check(d);
 }
 
 extern "C" int qa_decoder_decode_streams(qa_decoder * d, const int32_t * first_ids, int32_t n_steps, int32_t * out_ids) {
@@ -825,7 +911,71 @@ extern "C" int qa_decoder_decode_streams(qa_decoder * d, const int32_t * first_i
         if (rc != QA_OK) return rc;
     }
     QA_HIP(hipStreamSynchronize(d->stream));
+    rc = persist_check(d);
+    if (rc != QA_OK) return rc;
     std::memcpy(out_ids, d->h_ids, sizeof(int32_t) * static_cast<size_t>(n_steps) * S);
+    return QA_OK;
+}
+
+extern "C" int qa_decoder_set_persistent(qa_decoder * d, int32_t enable) {
+    if (!d) return fail(QA_ERR_INVALID, "qa_decoder_set_persistent: null decoder");
+    if (!enable) {
+        d->persist = false;
+        return QA_OK;
+    }
+    int32_t grid = 0;
+    int rc = persist_plan(persist_plan_in(d), &grid);
+    if (rc != QA_OK) return rc;
+    // the barrier wait bound in 100 MHz ticks (tests set a tiny bound to force the give-up path)
+    d->persist_wait_ticks = 20000000;
+    if (const char * e = std::getenv("QA_PERSIST_WAIT_TICKS")) d->persist_wait_ticks = std::strtoull(e, nullptr, 10);
+    if (!d->persist_layers) {
+        const qa_text_config & c = d->cfg;
+        const size_t nl = static_cast<size_t>(c.n_layers), H = static_cast<size_t>(c.hidden);
+        const size_t QD = static_cast<size_t>(c.n_heads) * kHeadDim, KD = static_cast<size_t>(c.n_kv_heads) * kHeadDim;
+        if (!d->persist_ws) {
+            rc = dmalloc_t(d->weight_allocs, (2 * nl - 1) * H, &d->persist_xbuf);
+            rc = rc ? rc : dmalloc_t(d->weight_allocs, nl * (QD + 2 * KD), &d->persist_qkv);
+            rc = rc ? rc : dmalloc_t(d->weight_allocs, nl * QD, &d->persist_attn);
+            rc = rc ? rc : dmalloc_t(d->weight_allocs, nl * static_cast<size_t>(c.intermediate), &d->persist_act);
+            const size_t ws_bytes = nl * persist_ws_stride(d->layout);
+            rc = rc ? rc : dmalloc(d->weight_allocs, ws_bytes, &d->persist_ws);
+            if (rc != QA_OK) return rc;
+            d->persist_ws_bytes = ws_bytes;
+            QA_HIP(hipMemsetAsync(d->persist_ws, 0, d->persist_ws_bytes, d->stream));
+        }
+        std::vector<PersistLayer> table(d->layers.size());
+        for (size_t l = 0; l < d->layers.size(); ++l) {
+            const DevLayer & L = d->layers[l];
+            PersistLayer & t = table[l];
+            t.qkv = L.qkv16 ? static_cast<const void *>(L.qkv16) : L.qkv;
+            t.o = L.o16 ? static_cast<const void *>(L.o16) : L.o;
+            t.gu = L.gu16 ? static_cast<const void *>(L.gu16) : L.gu;
+            t.down = L.down16 ? static_cast<const void *>(L.down16) : L.down;
+            t.attn_norm = L.attn_norm;
+            t.ffn_norm = L.ffn_norm;
+            t.q_norm = L.q_norm;
+            t.k_norm = L.k_norm;
+        }
+        void * p = nullptr;
+        rc = dmalloc(d->weight_allocs, sizeof(PersistLayer) * table.size(), &p);
+        if (rc != QA_OK) return rc;
+        QA_HIP(hipMemcpyAsync(p, table.data(), sizeof(PersistLayer) * table.size(), hipMemcpyHostToDevice, d->stream));
+        QA_HIP(hipStreamSynchronize(d->stream));
+        d->persist_layers = static_cast<PersistLayer *>(p);
+    }
+    // the barrier counters assume one grid per sync buffer: a new buffer (cleared) for a new grid
+    if (!d->persist_sync || grid != d->persist_grid) {
+        void * p = nullptr;
+        rc = dmalloc(d->weight_allocs, persist_sync_bytes(grid), &p);
+        if (rc != QA_OK) return rc;
+        d->persist_sync = static_cast<uint32_t *>(p);
+        d->persist_sync_bytes = persist_sync_bytes(grid);
+        QA_HIP(hipMemsetAsync(p, 0, d->persist_sync_bytes, d->stream));
+        d->persist_grid = grid;
+    }
+    QA_HIP(hipStreamSynchronize(d->stream));
+    d->persist = true;
     return QA_OK;
 }
 

@@ -90,6 +90,52 @@ int decode_step_attn_launch(const float * qkv, const float * q_norm_w, const flo
                             void * workspace, size_t workspace_bytes, hipStream_t stream);
 size_t decode_attn_workspace(int32_t n_streams, int32_t n_kv_heads, int32_t max_seq);
 
+// Persistent decode step (decode_persist.hip): every layer of one batch-1 token in one cooperative launch,
+// bit-identical to the eager step.  The layer table lives in device memory.
+struct PersistLayer {
+    const void * qkv;   // f32 rows, or their bf16 copies when b16
+    const void * o;
+    const void * gu;
+    const void * down;
+    const float * attn_norm;
+    const float * ffn_norm;
+    const float * q_norm;
+    const float * k_norm;
+};
+struct PersistPlanIn {
+    qa_kv_layout layout;
+    int32_t hidden = 0, q_dim = 0, inter = 0;
+    bool b16 = false;
+};
+// the grid (resident workgroups) for a decoder, or an error if no persistent kernel covers its shapes
+int persist_plan(const PersistPlanIn & in, int32_t * grid);
+size_t persist_sync_bytes(int32_t grid);
+// bytes of one layer's attention workspace in the persistent step (each layer has its own)
+size_t persist_ws_stride(const qa_kv_layout & layout);
+int persist_error_word_offset(int32_t grid);   // in uint32 words from the start of the sync buffer
+struct PersistLaunch {
+    PersistPlanIn plan;
+    int32_t grid = 0;
+    const PersistLayer * layers = nullptr;
+    int32_t n_layers = 0;
+    // every address is written at most once per launch, so each layer has its own buffers
+    float * x = nullptr;      // [hidden]: layer 0's input, the last layer's output
+    float * xbuf = nullptr;   // [2 n_layers - 1][hidden]
+    float * qkv = nullptr;    // [n_layers][q_dim + 2 kv_dim]
+    float * attn = nullptr;   // [n_layers][q_dim]
+    float * act = nullptr;    // [n_layers][inter]
+    void * cache = nullptr;
+    const int32_t * lens = nullptr;
+    int32_t max_len = 0;
+    int32_t n_heads = 0;
+    float eps = 0.0f, scale = 0.0f, rope_theta = 0.0f;
+    void * attn_ws = nullptr;    // [n_layers][persist_ws_stride], cleared before the first launch
+    size_t attn_ws_bytes = 0;
+    uint32_t * sync = nullptr;   // cleared before the first launch and after an abandoned one
+    uint64_t wait_ticks = 20000000;   // bound of each barrier wait (100 MHz ticks: 200 ms)
+};
+int persist_layers_launch(const PersistLaunch & a, hipStream_t stream);
+
 int prefill_attn_launch(const float * q, int32_t q_stride, const void * cache, const qa_kv_layout & layout,
                         int32_t layer, int32_t stream_idx, int32_t n_past, int32_t n_tokens, int32_t n_heads,
                         float scale, float * out, void * workspace, size_t workspace_bytes, hipStream_t stream);

@@ -147,6 +147,7 @@ SIGNATURES = {
     "qa_decoder_forward": (C.c_int, vp, fp, i32, i32, fp),
     "qa_decoder_generate": (C.c_int, vp, fp, i32, i32, ip, i32, ip, ip, ip, ip, fp),
     "qa_decoder_decode_streams": (C.c_int, vp, ip, i32, ip),
+    "qa_decoder_set_persistent": (C.c_int, vp, i32),
     "qa_decoder_fill_cache": (C.c_int, vp, i32, fp, fp, i32),
     "qa_decoder_layer_forward": (C.c_int, vp, i32, fp, i32, i32, fp),
     "qa_decoder_layer_forward_nocache": (C.c_int, vp, i32, fp, i32, fp),
@@ -428,6 +429,11 @@ class Decoder:
         out = np.zeros((max(n_steps, 1), self.n_streams), dtype=np.int32)
         check(lib.qa_decoder_decode_streams(self.handle, iptr(first), n_steps, iptr(out)))
         return out[:n_steps]
+
+    def set_persistent(self, enable: bool = True):
+        """Batch-1 decode steps as one persistent launch for all layers (qa_decoder_set_persistent); raises
+        QaError (QA_ERR_INVALID) where no persistent kernel covers the decoder's shapes."""
+        check(lib.qa_decoder_set_persistent(self.handle, 1 if enable else 0))
 
     def fill_cache(self, stream: int, k: np.ndarray, v: np.ndarray, length: int):
         k = np.ascontiguousarray(k, dtype=np.float32)

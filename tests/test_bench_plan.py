@@ -38,8 +38,8 @@ class Slot:
             raise OverflowError(f"roofline append at {self.cur} >= {self.cap}")
 
 
-def replay(prompt, warmup, steps, profile_steps, bf16_steps):
-    plan = bench.capacity_plan(prompt, warmup, steps, profile_steps, bf16_steps)
+def replay(prompt, warmup, steps, profile_steps, bf16_steps, persistent_steps=32):
+    plan = bench.capacity_plan(prompt, warmup, steps, profile_steps, bf16_steps, persistent_steps)
     main = Slot(plan["main"])
     for _ in range(3):                      # cold, steady-state and event-bracketed prefills
         main.forward(0, prompt)
@@ -53,6 +53,11 @@ def replay(prompt, warmup, steps, profile_steps, bf16_steps):
             side.forward(0, prompt)
         side.decode(warmup)
         side.decode(bf16_steps)
+    if persistent_steps:
+        pers = Slot(plan["persistent"])
+        pers.forward(0, prompt)
+        pers.decode(warmup)
+        pers.decode(persistent_steps)
     return plan
 
 
@@ -70,6 +75,7 @@ def test_driver_command_line():
     plan = replay(3913, 5, 20, 8, 64)
     assert plan["main"] >= 3913 + 5 + 20 + 8 + 1
     assert plan["bf16_exact"] >= 3913 + 5 + 64
+    assert plan["persistent"] >= 3913 + 5 + 32
 
 
 def test_plan_is_not_oversized():

@@ -1,0 +1,115 @@
+"""GPU tests of the persistent decode step (qa_decoder_set_persistent).
+
+Each batch-1 decode step of a persistent decoder runs every layer in one cooperative launch whose phases
+call the same device functions as the eager launches, so the ids, logits and lengths must equal the
+eager decoder's bit for bit.  The eager step is held to the oracle by the other GPU tests; the short
+cases here also compare the ids with the oracle directly.  Every call goes through the C ABI.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu(qa):
+    assert qa.device_count() > 0, "no HIP device: GPU tests need the MI355X"
+
+
+def decode(qa, model, cap, cache, x, n_new, persistent):
+    """Greedy generation, then a teacher-forced cached forward of one token after the prompt."""
+    with qa.Decoder(model, 1, cap, cache) as d:
+        if persistent:
+            d.set_persistent(True)
+        g = d.generate(x, n_new)
+        lens = d.device_lens().tolist()
+        cur = d.cur_len(0)
+        n = x.shape[0]
+        logits = d.forward(model.embed([g["ids"][0]]), n)
+        return g["ids"], logits, lens, cur, d.device_lens().tolist()
+
+
+@pytest.mark.parametrize("size", ["0.6B", "1.7B"])
+@pytest.mark.parametrize("cache", ["f16", "f32"])
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32-weights", "bf16-copies"])
+def test_persistent_step_bit_identical_short_cache(qa, orc, size, cache, bf16):
+    """A 36-position cache (scores and values chunks of 32): both model shapes, both cache dtypes, f32
+    weights and the bf16 copies of bf16-exact weights."""
+    shape = qa.QWEN3_ASR_0_6B if size == "0.6B" else qa.QWEN3_ASR_1_7B
+    ct = qa.QA_CACHE_F16 if cache == "f16" else qa.QA_CACHE_F32
+    m = qa.Model(shape, n_layers=2, bf16=bf16)
+    x = qa.prompt_input(m, 24, 6)
+    eager = decode(qa, m, 36, ct, x, 6, False)
+    pers = decode(qa, m, 36, ct, x, 6, True)
+    assert pers[0] == eager[0]
+    np.testing.assert_array_equal(pers[1], eager[1])
+    assert pers[2] == eager[2] == [35] and pers[3] == eager[3] == 35
+    assert pers[4] == eager[4] == [31]
+    om = orc.OracleModel.from_product_model(m)
+    ref = om.generate(x, 6, qa.STOP_IDS, om.cache(36, ct == qa.QA_CACHE_F16))
+    assert pers[0] == ref["ids"]
+
+
+@pytest.mark.parametrize("cap, audio", [(2600, 2547), (4200, 4137)], ids=["tiling-128-256", "tiling-144-256"])
+def test_persistent_step_bit_identical_long_cache(qa, cap, audio):
+    """Capacities whose tilings the benchmark decoders take (128- and 144-position scores chunks, 256-position
+    values chunks): about 10 and 16 merge participants per KV head, so the values phase's merge runs."""
+    m = qa.Model(qa.QWEN3_ASR_1_7B, n_layers=2)
+    x = qa.prompt_input(m, audio, 13)
+    eager = decode(qa, m, cap, qa.QA_CACHE_F16, x, 8, False)
+    pers = decode(qa, m, cap, qa.QA_CACHE_F16, x, 8, True)
+    assert pers[0] == eager[0]
+    np.testing.assert_array_equal(pers[1], eager[1])
+    assert pers[2:] == eager[2:]
+
+
+def test_persistent_decode_streams_matches_eager(qa):
+    """qa_decoder_decode_streams with one stream (the bench's decode loop) takes the persistent step too."""
+    m = qa.Model(qa.QWEN3_ASR_1_7B, n_layers=2)
+    x = qa.prompt_input(m, 24, 6)
+    out = []
+    for persistent in (False, True):
+        with qa.Decoder(m, 1, 64, qa.QA_CACHE_F16) as d:
+            if persistent:
+                d.set_persistent(True)
+            first = int(np.argmax(d.forward(x, 0)))
+            ids = d.decode_streams(np.array([first], np.int32), 20)
+            out.append((ids[:, 0].tolist(), d.device_lens().tolist(), d.cur_len(0)))
+    assert out[1] == out[0] and out[0][1] == [50] and out[0][2] == 50
+
+
+def test_persistent_step_refuses_uncovered_configs(qa):
+    m = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=2)
+    x = qa.prompt_input(m, 24, 6)
+    with qa.Decoder(m, 2, 36) as d:                  # more than one stream
+        with pytest.raises(qa.QaError) as e:
+            d.set_persistent(True)
+        assert e.value.code == qa.QA_ERR_INVALID
+    with qa.Decoder(m, 1, 1500) as d:                # 64/128-position chunks: no persistent kernel
+        with pytest.raises(qa.QaError) as e:
+            d.set_persistent(True)
+        assert e.value.code == qa.QA_ERR_INVALID and "no kernel" in str(e.value)
+        ids = d.generate(x, 4)["ids"]                # the decoder stays eager and correct
+    with qa.Decoder(m, 1, 1500) as d:
+        assert d.generate(x, 4)["ids"] == ids
+
+
+def test_persistent_step_gives_up_and_recovers(qa, monkeypatch):
+    """A wait bound of zero ticks (set from the host) makes the workgroups abandon the launch at a barrier:
+    every kernel still ends, the call reports QA_ERR_DEVICE, and the decoder clears its barrier and merge
+    state, so the next persistent generation equals the eager one."""
+    m = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=2)
+    x = qa.prompt_input(m, 24, 6)
+    with qa.Decoder(m, 1, 36) as d:
+        ref = d.generate(x, 6)["ids"]
+    with qa.Decoder(m, 1, 36) as d:
+        monkeypatch.setenv("QA_PERSIST_WAIT_TICKS", "0")
+        d.set_persistent(True)
+        with pytest.raises(qa.QaError) as e:
+            d.generate(x, 6)
+        assert e.value.code == qa.QA_ERR_DEVICE and "barrier" in str(e.value)
+        monkeypatch.delenv("QA_PERSIST_WAIT_TICKS")
+        d.set_persistent(True)
+        assert d.generate(x, 6)["ids"] == ref
+        d.set_persistent(False)
+        assert d.generate(x, 6)["ids"] == ref

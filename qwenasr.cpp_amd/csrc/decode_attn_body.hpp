@@ -215,6 +215,9 @@ __device__ inline int attended(const DecodeParams & p, int s) {
 
 template <typename CT, bool R16, int CHUNK, bool FUSED, bool COH>
 __device__ __forceinline__ void decode_scores_body(const DecodeParams & p, const RopeTable & rope, int bx, int by) {
+    // no contraction left to the compiler: the products that are fused are written as fma, so the per-launch
+    // kernel and the persistent step (where inlining differs) compute the same bits
+#pragma clang fp contract(off)
     constexpr int RPT = CHUNK / 16;   // rows per lane: 16 rows per workgroup pass
     const int g = bx % p.n_kv_heads;
     const int c = bx / p.n_kv_heads;
@@ -430,6 +433,9 @@ __device__ __forceinline__ void decode_scores_body(const DecodeParams & p, const
 
 template <typename CT, bool R16, int CHUNK, int SR, int MB, bool COH>
 __device__ __forceinline__ void decode_values_body(const DecodeParams & p, int bx, int by) {
+    // no contraction left to the compiler: the products that are fused are written as fma, so the per-launch
+    // kernel and the persistent step (where inlining differs) compute the same bits
+#pragma clang fp contract(off)
     constexpr int RPT = CHUNK / 16;
     const int g = bx % p.n_kv_heads;
     const int c = bx / p.n_kv_heads;
@@ -510,13 +516,13 @@ __device__ __forceinline__ void decode_values_body(const DecodeParams & p, int b
 #pragma unroll
     for (int u = 0; u < kStatRegs; ++u) {
         if (lane + u * kWave < n_stats) {
-            S0 += stat_sum(sa[u]) * static_cast<double>(expf(sa[u].x - M0));
-            S1 += stat_sum(sb[u]) * static_cast<double>(expf(sb[u].x - M1));
+            S0 = fma(stat_sum(sa[u]), static_cast<double>(expf(sa[u].x - M0)), S0);
+            S1 = fma(stat_sum(sb[u]), static_cast<double>(expf(sb[u].x - M1)), S1);
         }
     }
     for (int i = lane + kStatRegs * kWave; i < n_stats; i += kWave) {
-        S0 += st0[i].s * static_cast<double>(expf(st0[i].m - M0));
-        S1 += st1[i].s * static_cast<double>(expf(st1[i].m - M1));
+        S0 = fma(st0[i].s, static_cast<double>(expf(st0[i].m - M0)), S0);
+        S1 = fma(st1[i].s, static_cast<double>(expf(st1[i].m - M1)), S1);
     }
     S0 = wave_sum_d_all(S0);
     S1 = wave_sum_d_all(S1);

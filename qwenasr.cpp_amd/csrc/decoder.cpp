@@ -687,8 +687,11 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
     if (hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking) != hipSuccess) {
         return bail(fail(QA_ERR_DEVICE, "hipStreamCreate failed"));
     }
+    // no atomics-based GEMM algorithms: their sums land in a different order from run to run, and the
+    // prefill's results (and everything decoded after it) are then not repeatable
     if (rocblas_create_handle(&d->blas) != rocblas_status_success ||
-        rocblas_set_stream(d->blas, d->stream) != rocblas_status_success) {
+        rocblas_set_stream(d->blas, d->stream) != rocblas_status_success ||
+        rocblas_set_atomics_mode(d->blas, rocblas_atomics_not_allowed) != rocblas_status_success) {
         return bail(fail(QA_ERR_DEVICE, "rocblas handle creation failed"));
     }
 

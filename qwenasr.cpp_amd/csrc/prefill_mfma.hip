@@ -521,7 +521,10 @@ __device__ inline void run_item(const MfmaParams & p, const Item & it, _Float16 
     if (it.cut) {
         // Publish this part's O (thread-major: element e of every thread is 512 consecutive float4; with a single
         // pass also the max and sum of the thread's columns), then count; the second part to arrive combines
-        // both, in part order, so the result is the same whichever part arrives second.
+        // both, in part order, so the result is the same whichever part arrives second.  That needs every
+        // product rounded before the sum: a contracted (fused) product would be the merging part's own, and
+        // the result would depend on which part arrived second (measured: runs differed in the last query tiles).
+#pragma clang fp contract(off)
         const int64_t unit = static_cast<int64_t>(g) * (p.n_qt - p.qt_cut) + (it.qt - p.qt_cut);
         uint64_t * mine = reinterpret_cast<uint64_t *>(p.partial + (unit * 2 + it.j) * kPfPartialFloats);
         const uint64_t * other = reinterpret_cast<const uint64_t *>(p.partial + (unit * 2 + (it.j ^ 1)) * kPfPartialFloats);

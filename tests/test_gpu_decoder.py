@@ -303,3 +303,27 @@ def test_drop_in_tool_generate(qa, orc):
     r = subprocess.run([tool, "--size", "0.6b", "--layers", "1", "--device", "cpu", "--generate", "2"],
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 1 and "not available" in r.stderr
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32-weights", "bf16-copies"])
+def test_prefill_is_repeatable(qa, bf16):
+    """Three decoders prefill the same 4150-position prompt: the caches and the logits are equal bit for bit.
+    The prefill attention splits its last query tiles into two parts over the keys and the part that
+    arrives second merges both; the merge rounds every product before the sum, so the result does not
+    depend on which part arrives second (with the products fused, the last tiles' rows differed between
+    runs, and every later token with them)."""
+    m = qa.Model(qa.QWEN3_ASR_1_7B, n_layers=2, bf16=bf16)
+    cap, T = 4200, 4150
+    x = qa.prompt_input(m, T - 13, 13)
+    caches, logits = [], []
+    for _ in range(3):
+        with qa.Decoder(m, 1, cap, qa.QA_CACHE_F16) as dec:
+            logits.append(dec.forward(x, 0))
+            ptr, lay = dec.cache()
+            n = lay.n_layers * 2 * lay.n_streams * lay.n_kv_heads * lay.max_seq * lay.head_dim
+            c = np.empty(n, np.float16)
+            qa.check(qa.lib.qa_copy_to_host(c.ctypes.data, ptr, n * 2))
+            caches.append(c.reshape(2, 2, 8, cap, 128)[:, :, :, :T])
+    for r in (1, 2):
+        np.testing.assert_array_equal(caches[r], caches[0])
+        np.testing.assert_array_equal(logits[r], logits[0])

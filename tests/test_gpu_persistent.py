@@ -50,12 +50,19 @@ def test_persistent_step_bit_identical_short_cache(qa, orc, size, cache, bf16):
     assert pers[0] == ref["ids"]
 
 
-@pytest.mark.parametrize("cap, audio", [(2600, 2547), (4200, 4137)], ids=["tiling-128-256", "tiling-144-256"])
-def test_persistent_step_bit_identical_long_cache(qa, cap, audio):
-    """Capacities whose tilings the benchmark decoders take (128- and 144-position scores chunks, 256-position
-    values chunks): about 10 and 16 merge participants per KV head, so the values phase's merge runs."""
+# (capacity, prompt): one capacity per batch-1 tiling the decoder can pick (scores chunk / values chunk /
+# statistics register slots / merge loads), from 32/64 up to 128/256 with 4 slots of statistics
+LONG = [(600, 560, "32-64"), (1200, 1150, "32-128"), (1500, 1450, "64-128"), (2200, 2150, "64-256"),
+        (2600, 2560, "128-256"), (4200, 4150, "144-256"), (4800, 4750, "160-256"), (5500, 5450, "192-256"),
+        (7000, 6950, "128-256-mb16"), (9000, 8950, "128-256-sr2"), (17000, 16950, "128-256-sr4")]
+
+
+@pytest.mark.parametrize("cap, prompt, tiling", LONG, ids=[t for _, _, t in LONG])
+def test_persistent_step_bit_identical_long_cache(qa, cap, prompt, tiling):
+    """The tilings of longer caches: several scores blocks and values merge participants per KV head, so the
+    values phase's merge runs (1.7B shape, 2 layers, f16 cache)."""
     m = qa.Model(qa.QWEN3_ASR_1_7B, n_layers=2)
-    x = qa.prompt_input(m, audio, 13)
+    x = qa.prompt_input(m, prompt - 13, 13)
     eager = decode(qa, m, cap, qa.QA_CACHE_F16, x, 8, False)
     pers = decode(qa, m, cap, qa.QA_CACHE_F16, x, 8, True)
     assert pers[0] == eager[0]
@@ -80,17 +87,19 @@ def test_persistent_decode_streams_matches_eager(qa):
 
 def test_persistent_step_refuses_uncovered_configs(qa):
     m = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=2)
-    x = qa.prompt_input(m, 24, 6)
     with qa.Decoder(m, 2, 36) as d:                  # more than one stream
         with pytest.raises(qa.QaError) as e:
             d.set_persistent(True)
-        assert e.value.code == qa.QA_ERR_INVALID
-    with qa.Decoder(m, 1, 1500) as d:                # 64/128-position chunks: no persistent kernel
+        assert e.value.code == qa.QA_ERR_INVALID and "single-stream" in str(e.value)
+    # a shape with no persistent kernel (intermediate 4096): refused, and the decoder stays eager and correct
+    odd = qa.Model(qa.ModelSize("custom", hidden=1024, intermediate=4096, vocab=4096), n_layers=2)
+    x = qa.prompt_input(odd, 24, 6)
+    with qa.Decoder(odd, 1, 36) as d:
         with pytest.raises(qa.QaError) as e:
             d.set_persistent(True)
         assert e.value.code == qa.QA_ERR_INVALID and "no kernel" in str(e.value)
-        ids = d.generate(x, 4)["ids"]                # the decoder stays eager and correct
-    with qa.Decoder(m, 1, 1500) as d:
+        ids = d.generate(x, 4)["ids"]
+    with qa.Decoder(odd, 1, 36) as d:
         assert d.generate(x, 4)["ids"] == ids
 
 

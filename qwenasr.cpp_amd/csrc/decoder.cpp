@@ -776,6 +776,11 @@ extern "C" int qa_decoder_create(const qa_text_config * cfg, const qa_model_weig
     }
     rc = ensure_rows(d, n_streams);
     if (rc != QA_OK) return bail(rc);
+    // QA_DECODE_PERSISTENT=1: the persistent decode step for callers that cannot call qa_decoder_set_persistent
+    // (the drop-in API and its tools); a decoder it does not cover stays eager
+    if (const char * e = std::getenv("QA_DECODE_PERSISTENT"); e && std::strcmp(e, "1") == 0) {
+        (void)qa_decoder_set_persistent(d, 1);
+    }
     *out = d;
     return QA_OK;
 }

@@ -72,6 +72,23 @@ def test_harness_generate_command(checkpoint):
     assert int(meta["total_tokens"]) == ref["total_tokens"] and int(meta["generated_tokens"]) == len(ids)
 
 
+def test_harness_generate_command_persistent(checkpoint):
+    """The same harness command with QA_DECODE_PERSISTENT=1 in the environment: the drop-in's decoder runs each
+    decode step as one persistent launch, and the generated ids are the oracle's (and the eager run's)."""
+    model, om, x, gguf, wav, _ = checkpoint
+    n = 8
+    env = dict(os.environ, QA_DECODE_PERSISTENT="1")
+    cmd = harness_generate_argv(gguf, wav, n, system="Transcribe.", language="English")
+    print("run:", " ".join(map(str, cmd[1:])), "(QA_DECODE_PERSISTENT=1)", flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=300, env=env)
+    assert r.returncode == 0, r.stderr
+    meta = parse_kv(r.stdout)
+    ids = [int(v) for v in meta["generated_ids"].split(",") if v]
+    stops = [model.cfg.vocab - 5, model.cfg.vocab - 7, model.cfg.vocab - 5]
+    ref = om.generate(x, n, stops, om.cache(156 + n, f16=False))
+    assert ids == ref["ids"], (ids, ref["ids"], ref["margins"])
+
+
 def test_harness_generate_command_bf16_checkpoint(tmp_path, qa, orc, greedy):
     """A GGUF holding bf16-exact weights (what the reference's converter writes from the released bf16
     checkpoint, convert.py:386-387) through the drop-in: the decoder keeps bf16 weight copies and the

@@ -682,8 +682,8 @@ def main():
         return r
 
     def ms_decode_packed():
-        # the opt-in packed f32 GEMMs (QA_GR_PACKED=1, read at decoder creation): q|k|v, o and the LM head on
-        # weights reordered for the f32 MFMA; another summation order than the default kernels
+        # the opt-in packed f32 GEMMs (QA_GR_PACKED=1, read at decoder creation): q|k|v and o on weights reordered
+        # for the f32 MFMA (the LM head is packed by default); another summation order than the default kernels
         os.environ["QA_GR_PACKED"] = "1"
         try:
             r = multistream_decode(qa, model, args.multistream_steps)

@@ -622,14 +622,15 @@ int pack_weights_bf16(qa_decoder * d) {
     return rc;
 }
 
-// QA_GR_PACKED=1, multi-stream decoders on f32 weights: the q|k|v and o rows of every layer and the LM head
-// packed for gemm_packed.hip's MFMA GEMMs (2.65 GB beside the 6.88 GB of f32 weights for the 1.7B model).
-// Opt-in: they sum in another order than gemm_rows32_kernel, and on config 4 that order takes the oracle's
-// runner-up at one near-tie (stream 11, step 36, oracle top-2 margin 4.3e-4), where the default kernel agrees.
+// Multi-stream decoders on f32 weights: the LM head packed for gemm_packed.hip's 128-row MFMA kernel (1.24 GB
+// beside the 6.88 GB of f32 weights for the 1.7B model; config-4 step 4.04 -> 3.99 ms, all 2048 oracle ids kept).
+// QA_GR_PACKED=1 also packs the q|k|v and o rows of every layer (1.41 GB more; 3.83 ms).  That part is opt-in:
+// its sums run in another order than gemm_rows32_kernel's, and on config 4 it takes the oracle's runner-up at one
+// near-tie (stream 11, step 36, oracle top-2 margin 4.3e-4), where the default kernels agree.
 int pack_weights_mfma(qa_decoder * d) {
     if (d->n_streams < 2 || d->layers.empty() || d->layers[0].qkv16) return QA_OK;
     const char * e = std::getenv("QA_GR_PACKED");
-    if (!e || std::strcmp(e, "1") != 0) return QA_OK;
+    const bool layers = e && std::strcmp(e, "1") == 0;
     const qa_text_config & c = d->cfg;
     const int32_t H = c.hidden, QD = c.n_heads * kHeadDim, KD = c.n_kv_heads * kHeadDim;
     int rc = QA_OK;
@@ -638,7 +639,7 @@ int pack_weights_mfma(qa_decoder * d) {
         rc = dmalloc_t(d->weight_allocs, static_cast<size_t>(N) * K, dst);
         if (rc == QA_OK) rc = pack_f32_launch(src, N, K, *dst, d->stream);
     };
-    if (packed_gemm_shape_ok(QD + 2 * KD, H, false) && packed_gemm_shape_ok(H, QD, false)) {
+    if (layers && packed_gemm_shape_ok(QD + 2 * KD, H, false) && packed_gemm_shape_ok(H, QD, false)) {
         for (DevLayer & L : d->layers) {
             pack(L.qkv, QD + 2 * KD, H, &L.qkv_p);
             pack(L.o, H, QD, &L.o_p);

@@ -169,7 +169,7 @@ def _with_env(name, value, fn):
 
 def test_config4_packed_f32_gemms(qa, greedy):
     """QA_GR_PACKED=1 (read at decoder creation): config 4 with the f32 weights on the packed multi-stream GEMMs
-    (q|k|v, o and LM head on weights reordered for the f32 MFMA, gemm_packed.hip).  They sum in another order
+    (q|k|v and o on weights reordered for the f32 MFMA, gemm_packed.hip; the LM head is packed by default).  They sum in another order
     than the default kernels, so the comparison runs in its own tie group (at most one accepted near-tie), and the
     bookkeeping stays exact."""
     from qwenasr_amd import configs

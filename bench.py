@@ -278,12 +278,12 @@ def multistream_roofline(qa, cfg, reps: int, lens=None, label: str = "config 4 s
                         f"(mean {float(lens.mean()) + 1:.0f}), one layer's decode-step attention per launch pair"}
 
 
-def kernel_only(which: str, reps: int, weights: str = "f32"):
+def kernel_only(which: str, reps: int, weights: str = "f32", length: int = 4186):
     """One hot-path kernel on synthetic inputs at the config-3 shape, for rocprofv3 passes (the counters
     of every dispatch are then the kernel's alone).  append: the prefill K/V append of 3913 positions
     (q/k norm + RoPE, f16 cache write); prefill: causal prefill attention over 3913 positions of one
     layer (f16 cache, n_past 0); decode-attn / decode-attn-f32: the decode-step attention of one layer
-    at L = 4186 over an f16 / f32 cache, rotating 28 layer caches; decode-step: config 3 end to end at
+    at L = length (default 4186, capacity L + 8) over an f16 / f32 cache, rotating 28 layer caches; decode-step: config 3 end to end at
     batch 1 (prefill once, then reps greedy decode tokens), decode-step-persistent the same with every
     layer of a token in one persistent launch; multistream: the config-4 decode step of 32
     streams (end to end); multistream-attn: the decode-step attention of 32 streams at L = 4096 (reps x
@@ -329,7 +329,7 @@ def kernel_only(which: str, reps: int, weights: str = "f32"):
         import qwenasr_amd as qa
 
         cfg = qa.QWEN3_ASR_1_7B.config()
-        L = 4186
+        L = length
         us = attn_pair_us(qa, cfg, L, qa.QA_CACHE_F32, max(1, reps // cfg.n_layers))
         print(json.dumps(dict(kernel=which, avg_us=round(us, 3), algorithmic_bytes_per_launch=8192 * L + 16384)),
               flush=True)
@@ -374,7 +374,7 @@ def kernel_only(which: str, reps: int, weights: str = "f32"):
         flops = 4.0 * cfg.n_heads * cfg.head_dim * T * (T + 1) / 2
         unit = dict(useful_gflop_per_launch=round(flops / 1e9, 3))
     else:
-        L = 4186
+        L = length
         lay = qa.KvLayout(cfg.n_layers, 1, cfg.n_kv_heads, cfg.head_dim, L + 8, qa.QA_CACHE_F16)
         cache = qa.DeviceArray(qa.lib.qa_kv_cache_bytes(C.byref(lay)), np.uint8)
         q_dim, kv_dim = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
@@ -575,13 +575,15 @@ def main():
                                          "multistream-attn", "decode-step", "decode-step-persistent"],
                     help="only run one hot-path kernel on synthetic inputs (short program for rocprofv3 passes)")
     ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--kernel-len", type=int, default=4186,
+                    help="attended positions of the decode-attn / decode-attn-f32 kernel modes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the KV-cache path would shard by "
               "KV head or by stream); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     if args.kernel:
-        kernel_only(args.kernel, args.kernel_reps, args.weights)
+        kernel_only(args.kernel, args.kernel_reps, args.weights, args.kernel_len)
         return
     if args.copy_calibration:
         copy_calibration()

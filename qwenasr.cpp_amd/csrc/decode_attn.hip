@@ -123,7 +123,7 @@ bool launch_both(const Chunks & ch, bool fused, int32_t n_kv, int32_t n_streams,
 
 int launch_decode(DecodeParams p, bool fused, const RopeTable & rope, const qa_kv_layout & layout,
                   int32_t n_streams, void * workspace, size_t workspace_bytes, hipStream_t stream) {
-    const Chunks ch = pick_chunks(layout.n_streams, layout.n_kv_heads, layout.max_seq);
+    const Chunks ch = pick_chunks(layout);
     if (ch.values != 32 && ch.values != 64 && ch.values != 128 && ch.values != 256) {
         return fail(QA_ERR_INVALID, "decode attention: no values kernel for the chosen chunk");
     }

@@ -664,10 +664,11 @@ __device__ __forceinline__ void decode_values_body(const DecodeParams & p, int b
 // Positions per workgroup of each kernel.  The scores kernel has no merge; its chunk trades workgroup
 // count (dispatch and per-workgroup overhead) against the load size of one workgroup.  The values
 // kernel's chunks are the merge participants of one (stream, KV head), so it uses chunks large enough
-// to keep them at <= 16 per unit (every participant increments the same counter).  The choice
-// depends on the cache capacity only, never on a call's length, so a captured decode step (grids
-// sized by capacity) and an eager one (grids sized by the longest stream) run the same tiling and
-// produce the same bits.  QA_DECODE_CHUNK / QA_DECODE_VCHUNK override the choice (tuning).
+// to keep them at <= 16 per unit (every participant increments the same counter), or <= 32 where that
+// still fits one workgroup per CU (below).  The choice depends on the cache layout only (capacity,
+// streams, cache dtype), never on a call's length, so a captured decode step (grids sized by capacity)
+// and an eager one (grids sized by the longest stream) run the same tiling and produce the same bits.
+// QA_DECODE_CHUNK / QA_DECODE_VCHUNK override the choice (tuning).
 struct Chunks {
     int scores, values;
 };
@@ -681,9 +682,10 @@ int env_chunk(const char * name, bool values) {
     return !values && (v == 144 || v == 160 || v == 192) ? v : 0;
 }
 
-Chunks pick_chunks(int32_t n_streams, int32_t n_kv, int32_t capacity) {
+Chunks pick_chunks(const qa_kv_layout & layout) {
     static const int forced_s = env_chunk("QA_DECODE_CHUNK", false);
     static const int forced_v = env_chunk("QA_DECODE_VCHUNK", true);
+    const int32_t capacity = layout.max_seq;
     Chunks ch{};
     // scores: the smallest chunk that keeps the grid at about one workgroup per CU, else 128 (measured
     // at batch 1: 32 is best up to ~1k positions, 64 at 2k, 128 from 4k on, 11.1 vs 12.2 us at 4186;
@@ -692,7 +694,7 @@ Chunks pick_chunks(int32_t n_streams, int32_t n_kv, int32_t capacity) {
     // CU: the CUs holding two would set the time (measured at batch 1: 10.1 vs 10.5 us at 4186, 10.6 vs
     // 11.2 at 5000, 10.9 vs 11.4 at 6000).  From 6145 on 128 stays: at 8000 a 256-position chunk (one
     // workgroup per CU) times the same as 128 (about two on every CU).
-    const int64_t units = static_cast<int64_t>(n_streams) * n_kv;
+    const int64_t units = static_cast<int64_t>(layout.n_streams) * layout.n_kv_heads;
     ch.scores = 128;
     for (int c = 32; c < 128; c *= 2) {
         if (units * ((capacity + c - 1) / c) <= 320) {
@@ -709,8 +711,19 @@ Chunks pick_chunks(int32_t n_streams, int32_t n_kv, int32_t capacity) {
         }
     }
     if (forced_s) ch.scores = forced_s;
+    // values: at most 16 participants per unit; then half that chunk (up to 32 participants) where the
+    // grid still holds at most one workgroup per CU, for f32 caches and for f16 caches at 256 positions
+    // (V rows of 64 KB per workgroup).  Measured at batch 1 (pair time, 28 rotated layer caches): f32
+    // cache 8.27 against 8.81 us at 700 positions, 9.66 against 10.33 at 1500, 10.23 against 10.82 at
+    // 2000, 11.45 against 13.13 at 2100, 13.60 against 15.42 at 3947; f16 cache 8.99 against 9.43 us at
+    // 2100, 8.95 against 9.17 at 3000, 9.60 against 9.84 at 3947; f16 rows of 64-128 positions lost (7.98
+    // against 8.25 us at 700, 8.37 against 8.55 at 2000), and so did 32 streams (config-4 shapes, 49.1
+    // against 50.2 us), whose grid holds thousands of workgroups.
     int v = 32;
     while (v < 256 && (capacity + v - 1) / v > 16) v *= 2;
+    const bool f32 = layout.cache_type == QA_CACHE_F32;
+    const int half = v / 2;
+    if (half >= 32 && (f32 || v == 256) && units * ((capacity + half - 1) / half) <= 256) v = half;
     ch.values = forced_v ? forced_v : v;
     if (ch.values < ch.scores) ch.values = ch.scores > 128 ? 256 : ch.scores;   // values chunks: 32 ... 256
     return ch;

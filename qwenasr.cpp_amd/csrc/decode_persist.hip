@@ -38,7 +38,7 @@ int persist_plan(const PersistPlanIn & in, int32_t * grid) {
         if (rc != QA_ERR_INVALID) break;
     }
     if (rc == QA_ERR_INVALID) {
-        const Chunks ch = pick_chunks(in.layout.n_streams, in.layout.n_kv_heads, in.layout.max_seq);
+        const Chunks ch = pick_chunks(in.layout);
         return fail(QA_ERR_INVALID, "persistent decode step: no kernel for this model shape (hidden " +
                                         std::to_string(in.hidden) + ", q_dim " + std::to_string(in.q_dim) +
                                         ", intermediate " + std::to_string(in.inter) + ") and tiling (scores chunk " +

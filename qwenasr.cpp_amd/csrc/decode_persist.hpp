@@ -208,20 +208,29 @@ struct Variant {
     Variant{H4, 8, I4, B, F, S, V, SRV, MBV,                                                                \
             decode_layers_kernel<H4, 8, I4, B, std::conditional_t<F, _Float16, float>, F, S, V, SRV, MBV>}
 
-// Every batch-1 tiling pick_chunks can choose (capacities 1 to 65536), for one weight type.
-#define QA_PERSIST_TILINGS(H4, I4, B, F)                                                                    \
-    QA_PERSIST_VARIANT(H4, I4, B, F, 32, 32, 1, 8), QA_PERSIST_VARIANT(H4, I4, B, F, 32, 64, 1, 8),           \
-        QA_PERSIST_VARIANT(H4, I4, B, F, 32, 128, 1, 8), QA_PERSIST_VARIANT(H4, I4, B, F, 64, 128, 1, 8),     \
-        QA_PERSIST_VARIANT(H4, I4, B, F, 64, 256, 1, 8), QA_PERSIST_VARIANT(H4, I4, B, F, 128, 256, 1, 8),    \
-        QA_PERSIST_VARIANT(H4, I4, B, F, 144, 256, 1, 16), QA_PERSIST_VARIANT(H4, I4, B, F, 160, 256, 1, 16), \
-        QA_PERSIST_VARIANT(H4, I4, B, F, 192, 256, 1, 16), QA_PERSIST_VARIANT(H4, I4, B, F, 128, 256, 1, 16), \
-        QA_PERSIST_VARIANT(H4, I4, B, F, 128, 256, 2, 40), QA_PERSIST_VARIANT(H4, I4, B, F, 128, 256, 4, 40), \
-        QA_PERSIST_VARIANT(H4, I4, B, F, 128, 256, 8, 40)
+// Every batch-1 tiling pick_chunks can choose (capacities 1 to 65536) for one cache dtype and weight type:
+// (scores chunk, values chunk, statistics register slots, merge loads).
+#define QA_PERSIST_TILINGS_F16(H4, I4, B)                                                                   \
+    QA_PERSIST_VARIANT(H4, I4, B, true, 32, 32, 1, 8), QA_PERSIST_VARIANT(H4, I4, B, true, 32, 64, 1, 8),     \
+        QA_PERSIST_VARIANT(H4, I4, B, true, 32, 128, 1, 8), QA_PERSIST_VARIANT(H4, I4, B, true, 64, 128, 1, 8), \
+        QA_PERSIST_VARIANT(H4, I4, B, true, 64, 128, 1, 16), QA_PERSIST_VARIANT(H4, I4, B, true, 128, 128, 1, 16), \
+        QA_PERSIST_VARIANT(H4, I4, B, true, 144, 256, 1, 16), QA_PERSIST_VARIANT(H4, I4, B, true, 160, 256, 1, 16), \
+        QA_PERSIST_VARIANT(H4, I4, B, true, 192, 256, 1, 16), QA_PERSIST_VARIANT(H4, I4, B, true, 128, 256, 1, 16), \
+        QA_PERSIST_VARIANT(H4, I4, B, true, 128, 256, 2, 40), QA_PERSIST_VARIANT(H4, I4, B, true, 128, 256, 4, 40), \
+        QA_PERSIST_VARIANT(H4, I4, B, true, 128, 256, 8, 40)
+#define QA_PERSIST_TILINGS_F32(H4, I4, B)                                                                   \
+    QA_PERSIST_VARIANT(H4, I4, B, false, 32, 32, 1, 8), QA_PERSIST_VARIANT(H4, I4, B, false, 32, 32, 1, 16),  \
+        QA_PERSIST_VARIANT(H4, I4, B, false, 32, 64, 1, 16), QA_PERSIST_VARIANT(H4, I4, B, false, 64, 64, 1, 16), \
+        QA_PERSIST_VARIANT(H4, I4, B, false, 64, 128, 1, 16), QA_PERSIST_VARIANT(H4, I4, B, false, 128, 128, 1, 16), \
+        QA_PERSIST_VARIANT(H4, I4, B, false, 144, 256, 1, 16), QA_PERSIST_VARIANT(H4, I4, B, false, 160, 256, 1, 16), \
+        QA_PERSIST_VARIANT(H4, I4, B, false, 192, 256, 1, 16), QA_PERSIST_VARIANT(H4, I4, B, false, 128, 256, 1, 16), \
+        QA_PERSIST_VARIANT(H4, I4, B, false, 128, 256, 2, 40), QA_PERSIST_VARIANT(H4, I4, B, false, 128, 256, 4, 40), \
+        QA_PERSIST_VARIANT(H4, I4, B, false, 128, 256, 8, 40)
 
 // The variant of `table` for a decoder, or null.
 inline const Variant * find_in(const Variant * table, size_t n, const PersistPlanIn & in) {
     if (in.hidden % 256 || in.q_dim % 256 || in.inter % 256) return nullptr;
-    const Chunks ch = pick_chunks(in.layout.n_streams, in.layout.n_kv_heads, in.layout.max_seq);
+    const Chunks ch = pick_chunks(in.layout);
     const int sr = values_stat_regs(in.layout.max_seq, ch.scores);
     const int mb = values_merge_loads(in.layout.max_seq, ch.values);
     const bool f16 = in.layout.cache_type == QA_CACHE_F16;
@@ -290,12 +299,12 @@ inline int launch_variant(const Variant * v, const PersistLaunch & a, hipStream_
 
 }  // namespace
 
-// One translation unit per (model shape, cache dtype) instantiates its 26 kernels (13 tilings x f32 weights
-// and bf16 copies) and defines persist_find_NAME (QA_OK and the resident workgroups per CU if it holds the
-// decoder's kernel, QA_ERR_INVALID otherwise) and persist_launch_NAME.
-#define QA_PERSIST_UNIT(NAME, H4, I4, F)                                                                    \
+// One translation unit per (model shape, cache dtype: F16 or F32) instantiates its 26 kernels (13 tilings x
+// f32 weights and bf16 copies) and defines persist_find_NAME (QA_OK and the resident workgroups per CU if it
+// holds the decoder's kernel, QA_ERR_INVALID otherwise) and persist_launch_NAME.
+#define QA_PERSIST_UNIT(NAME, H4, I4, CACHE)                                                                \
     namespace {                                                                                             \
-    const Variant kUnit[] = {QA_PERSIST_TILINGS(H4, I4, false, F), QA_PERSIST_TILINGS(H4, I4, true, F)};     \
+    const Variant kUnit[] = {QA_PERSIST_TILINGS_##CACHE(H4, I4, false), QA_PERSIST_TILINGS_##CACHE(H4, I4, true)}; \
     }                                                                                                       \
     int persist_find_##NAME(const PersistPlanIn & in, int * per_cu) {                                       \
         const Variant * v = find_in(kUnit, sizeof(kUnit) / sizeof(kUnit[0]), in);                           \

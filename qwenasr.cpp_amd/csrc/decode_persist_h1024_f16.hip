@@ -3,5 +3,5 @@
 #include "decode_persist.hpp"
 
 namespace qa {
-QA_PERSIST_UNIT(h1024_f16, 4, 12, true)
+QA_PERSIST_UNIT(h1024_f16, 4, 12, F16)
 }  // namespace qa

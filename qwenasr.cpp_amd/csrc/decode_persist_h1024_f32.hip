@@ -3,5 +3,5 @@
 #include "decode_persist.hpp"
 
 namespace qa {
-QA_PERSIST_UNIT(h1024_f32, 4, 12, false)
+QA_PERSIST_UNIT(h1024_f32, 4, 12, F32)
 }  // namespace qa

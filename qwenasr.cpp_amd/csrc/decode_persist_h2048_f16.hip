@@ -3,5 +3,5 @@
 #include "decode_persist.hpp"
 
 namespace qa {
-QA_PERSIST_UNIT(h2048_f16, 8, 24, true)
+QA_PERSIST_UNIT(h2048_f16, 8, 24, F16)
 }  // namespace qa

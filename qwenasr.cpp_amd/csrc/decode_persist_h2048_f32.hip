@@ -3,5 +3,5 @@
 #include "decode_persist.hpp"
 
 namespace qa {
-QA_PERSIST_UNIT(h2048_f32, 8, 24, false)
+QA_PERSIST_UNIT(h2048_f32, 8, 24, F32)
 }  // namespace qa

@@ -50,24 +50,51 @@ def test_persistent_step_bit_identical_short_cache(qa, orc, size, cache, bf16):
     assert pers[0] == ref["ids"]
 
 
-# (capacity, prompt): one capacity per batch-1 tiling the decoder can pick (scores chunk / values chunk /
-# statistics register slots / merge loads), from 32/64 up to 128/256 with 4 slots of statistics
-LONG = [(600, 560, "32-64"), (1200, 1150, "32-128"), (1500, 1450, "64-128"), (2200, 2150, "64-256"),
-        (2600, 2560, "128-256"), (4200, 4150, "144-256"), (4800, 4750, "160-256"), (5500, 5450, "192-256"),
-        (7000, 6950, "128-256-mb16"), (9000, 8950, "128-256-sr2"), (17000, 16950, "128-256-sr4")]
+# (capacity, prompt): one capacity per batch-1 tiling the decoder can pick for each cache dtype (scores chunk /
+# values chunk / statistics register slots / merge loads); the 36-position cache of the test above takes
+# 32 / 32 / 1 / 8
+LONG_F16 = [(600, 560, "32-64"), (1200, 1150, "32-128"), (1500, 1450, "64-128"), (2200, 2150, "64-128-mb16"),
+            (2600, 2560, "128-128"), (4200, 4150, "144-256"), (4800, 4750, "160-256"), (5500, 5450, "192-256"),
+            (7000, 6950, "128-256-mb16"), (9000, 8950, "128-256-sr2"), (17000, 16950, "128-256-sr4"),
+            (33000, 32950, "128-256-sr8")]
+LONG_F32 = [(900, 860, "32-32-mb16"), (1200, 1150, "32-64"), (1800, 1750, "64-64"), (2300, 2250, "64-128"),
+            (3000, 2950, "128-128"), (5000, 4950, "160-256")]
+LONG = [(cap, prompt, f"f16-{t}", "f16") for cap, prompt, t in LONG_F16] + \
+       [(cap, prompt, f"f32-{t}", "f32") for cap, prompt, t in LONG_F32]
 
 
-@pytest.mark.parametrize("cap, prompt, tiling", LONG, ids=[t for _, _, t in LONG])
-def test_persistent_step_bit_identical_long_cache(qa, cap, prompt, tiling):
+@pytest.mark.parametrize("cap, prompt, tiling, cache", LONG, ids=[t for _, _, t, _ in LONG])
+def test_persistent_step_bit_identical_long_cache(qa, cap, prompt, tiling, cache):
     """The tilings of longer caches: several scores blocks and values merge participants per KV head, so the
-    values phase's merge runs (1.7B shape, 2 layers, f16 cache)."""
+    values phase's merge runs (1.7B shape, 2 layers)."""
     m = qa.Model(qa.QWEN3_ASR_1_7B, n_layers=2)
+    ct = qa.QA_CACHE_F16 if cache == "f16" else qa.QA_CACHE_F32
     x = qa.prompt_input(m, prompt - 13, 13)
-    eager = decode(qa, m, cap, qa.QA_CACHE_F16, x, 8, False)
-    pers = decode(qa, m, cap, qa.QA_CACHE_F16, x, 8, True)
+    print(f"persistent long cache {tiling}: capacity {cap}, prompt {prompt}", flush=True)
+    eager = decode(qa, m, cap, ct, x, 8, False)
+    pers = decode(qa, m, cap, ct, x, 8, True)
     assert pers[0] == eager[0]
     np.testing.assert_array_equal(pers[1], eager[1])
     assert pers[2:] == eager[2:]
+
+
+# every capacity at which the batch-1 tiling changes, and the largest covered
+EDGES = [1, 512, 513, 1024, 1025, 1280, 1281, 2048, 2049, 2560, 2561, 4096, 4097, 4608, 4609, 5120, 5121, 6144, 6145,
+         8192, 8193, 16384, 16385, 32768, 32769, 65536]
+
+
+@pytest.mark.parametrize("size", ["0.6B", "1.7B"])
+@pytest.mark.parametrize("cache", ["f16", "f32"])
+def test_persistent_step_covers_every_capacity(qa, size, cache):
+    """Both model shapes and cache dtypes have a persistent kernel for every tiling, at the capacities where
+    the tiling changes (small vocabulary: only the layer kernels matter here)."""
+    base = qa.QWEN3_ASR_0_6B if size == "0.6B" else qa.QWEN3_ASR_1_7B
+    shape = qa.ModelSize(base.name + "-v4096", hidden=base.hidden, intermediate=base.intermediate, vocab=4096)
+    m = qa.Model(shape, n_layers=1)
+    ct = qa.QA_CACHE_F16 if cache == "f16" else qa.QA_CACHE_F32
+    for cap in EDGES:
+        with qa.Decoder(m, 1, cap, ct) as d:
+            d.set_persistent(True)
 
 
 def test_persistent_decode_streams_matches_eager(qa):

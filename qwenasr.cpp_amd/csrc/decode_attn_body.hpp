@@ -689,15 +689,21 @@ Chunks pick_chunks(const qa_kv_layout & layout) {
     Chunks ch{};
     // scores: the smallest chunk that keeps the grid at about one workgroup per CU, else 128 (measured
     // at batch 1: 32 is best up to ~1k positions, 64 at 2k, 128 from 4k on, 11.1 vs 12.2 us at 4186;
-    // 128 also for 32 streams).  Where 128-position chunks would put a second workgroup on some CUs
+    // 128 also for 32 streams).  "About": at most 256 workgroups for f16 rows, whose pair time rises when
+    // some CUs hold two (batch 1: 64 against 32 positions 8.07 vs 8.57 us at 1200, 128 against 64 8.62 vs
+    // 9.13 at 2300 and 8.73 vs 9.26 at 2550); at most 320 for f32 rows, twice the bytes per position, where
+    // more and smaller workgroups time the same or better (11.74-11.90 vs 12.24 us at 2500 for 32-64 against
+    // 128 positions).  Where 128-position chunks would put a second workgroup on some CUs
     // (8 units: capacities 4097 to 6144), the smallest of 144, 160 and 192 that keeps one workgroup per
     // CU: the CUs holding two would set the time (measured at batch 1: 10.1 vs 10.5 us at 4186, 10.6 vs
     // 11.2 at 5000, 10.9 vs 11.4 at 6000).  From 6145 on 128 stays: at 8000 a 256-position chunk (one
     // workgroup per CU) times the same as 128 (about two on every CU).
     const int64_t units = static_cast<int64_t>(layout.n_streams) * layout.n_kv_heads;
+    const bool f32 = layout.cache_type == QA_CACHE_F32;
+    const int64_t fill = f32 ? 320 : 256;
     ch.scores = 128;
     for (int c = 32; c < 128; c *= 2) {
-        if (units * ((capacity + c - 1) / c) <= 320) {
+        if (units * ((capacity + c - 1) / c) <= fill) {
             ch.scores = c;
             break;
         }
@@ -721,7 +727,6 @@ Chunks pick_chunks(const qa_kv_layout & layout) {
     // against 50.2 us), whose grid holds thousands of workgroups.
     int v = 32;
     while (v < 256 && (capacity + v - 1) / v > 16) v *= 2;
-    const bool f32 = layout.cache_type == QA_CACHE_F32;
     const int half = v / 2;
     if (half >= 32 && (f32 || v == 256) && units * ((capacity + half - 1) / half) <= 256) v = half;
     ch.values = forced_v ? forced_v : v;

@@ -212,8 +212,7 @@ struct Variant {
 // (scores chunk, values chunk, statistics register slots, merge loads).
 #define QA_PERSIST_TILINGS_F16(H4, I4, B)                                                                   \
     QA_PERSIST_VARIANT(H4, I4, B, true, 32, 32, 1, 8), QA_PERSIST_VARIANT(H4, I4, B, true, 32, 64, 1, 8),     \
-        QA_PERSIST_VARIANT(H4, I4, B, true, 32, 128, 1, 8), QA_PERSIST_VARIANT(H4, I4, B, true, 64, 128, 1, 8), \
-        QA_PERSIST_VARIANT(H4, I4, B, true, 64, 128, 1, 16), QA_PERSIST_VARIANT(H4, I4, B, true, 128, 128, 1, 16), \
+        QA_PERSIST_VARIANT(H4, I4, B, true, 64, 128, 1, 8), QA_PERSIST_VARIANT(H4, I4, B, true, 128, 128, 1, 16), \
         QA_PERSIST_VARIANT(H4, I4, B, true, 144, 256, 1, 16), QA_PERSIST_VARIANT(H4, I4, B, true, 160, 256, 1, 16), \
         QA_PERSIST_VARIANT(H4, I4, B, true, 192, 256, 1, 16), QA_PERSIST_VARIANT(H4, I4, B, true, 128, 256, 1, 16), \
         QA_PERSIST_VARIANT(H4, I4, B, true, 128, 256, 2, 40), QA_PERSIST_VARIANT(H4, I4, B, true, 128, 256, 4, 40), \
@@ -299,8 +298,8 @@ inline int launch_variant(const Variant * v, const PersistLaunch & a, hipStream_
 
 }  // namespace
 
-// One translation unit per (model shape, cache dtype: F16 or F32) instantiates its 26 kernels (13 tilings x
-// f32 weights and bf16 copies) and defines persist_find_NAME (QA_OK and the resident workgroups per CU if it
+// One translation unit per (model shape, cache dtype: F16 or F32) instantiates its kernels (11 tilings of an
+// f16 cache or 13 of an f32 cache, x f32 weights and bf16 copies) and defines persist_find_NAME (QA_OK and the resident workgroups per CU if it
 // holds the decoder's kernel, QA_ERR_INVALID otherwise) and persist_launch_NAME.
 #define QA_PERSIST_UNIT(NAME, H4, I4, CACHE)                                                                \
     namespace {                                                                                             \

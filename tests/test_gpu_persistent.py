@@ -53,10 +53,9 @@ def test_persistent_step_bit_identical_short_cache(qa, orc, size, cache, bf16):
 # (capacity, prompt): one capacity per batch-1 tiling the decoder can pick for each cache dtype (scores chunk /
 # values chunk / statistics register slots / merge loads); the 36-position cache of the test above takes
 # 32 / 32 / 1 / 8
-LONG_F16 = [(600, 560, "32-64"), (1200, 1150, "32-128"), (1500, 1450, "64-128"), (2200, 2150, "64-128-mb16"),
-            (2600, 2560, "128-128"), (4200, 4150, "144-256"), (4800, 4750, "160-256"), (5500, 5450, "192-256"),
-            (7000, 6950, "128-256-mb16"), (9000, 8950, "128-256-sr2"), (17000, 16950, "128-256-sr4"),
-            (33000, 32950, "128-256-sr8")]
+LONG_F16 = [(600, 560, "32-64"), (1500, 1450, "64-128"), (2600, 2560, "128-128-mb16"), (4200, 4150, "144-256"),
+            (4800, 4750, "160-256"), (5500, 5450, "192-256"), (7000, 6950, "128-256-mb16"), (9000, 8950, "128-256-sr2"),
+            (17000, 16950, "128-256-sr4"), (33000, 32950, "128-256-sr8")]
 LONG_F32 = [(900, 860, "32-32-mb16"), (1200, 1150, "32-64"), (1800, 1750, "64-64"), (2300, 2250, "64-128"),
             (3000, 2950, "128-128"), (5000, 4950, "160-256")]
 LONG = [(cap, prompt, f"f16-{t}", "f16") for cap, prompt, t in LONG_F16] + \

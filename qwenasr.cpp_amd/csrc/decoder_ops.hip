@@ -837,24 +837,51 @@ __global__ void add_inplace_kernel(float * y, const float * x, size_t n) {
 
 // stats (optional): stats[k][r] = sum of squares of columns 32 k .. 32 k + 31 of row r (the partial
 // layout gemm_rows32_kernel takes for its RMSNorm input; r < 32)
-__global__ void embed_rows_kernel(const float * table, int n_rows, int dim, const int32_t * ids, float * out,
-                                  double * stats) {
+// Row `row` of the next step's input: the embedding row t (zeros unless valid) copied to o, and, with
+// stats, the row's sums of squares per 32-column group (in double, the columns in increasing order),
+// stored at stats[32 * group + row] for the fused RMSNorm input of the multi-stream GEMM.  256 threads;
+// each pass issues all its loads (8 per thread, 2048 columns) before the first use and stages the
+// values in LDS for the sums, so a row costs one memory round trip per 2048 columns.
+constexpr int kGatherCols = 2048;
+
+__device__ void gather_row(const float * t, bool valid, int dim, float * o, double * stats, int row) {
+#pragma clang fp contract(off)
+    __shared__ float s_row[kGatherCols];
+    for (int base = 0; base < dim; base += kGatherCols) {
+        const int n = min(kGatherCols, dim - base);
+        float v[kGatherCols / 256];
+#pragma unroll
+        for (int u = 0; u < kGatherCols / 256; ++u) v[u] = t[base + min(static_cast<int>(threadIdx.x) + 256 * u, n - 1)];
+#pragma unroll
+        for (int u = 0; u < kGatherCols / 256; ++u) {
+            const int i = static_cast<int>(threadIdx.x) + 256 * u;
+            const float x = valid ? v[u] : 0.0f;
+            if (i < n) {
+                o[base + i] = x;
+                s_row[i] = x;
+            }
+        }
+        if (!stats) continue;
+        __syncthreads();
+        for (int k = threadIdx.x; 32 * k < n; k += 256) {
+            double ss = 0.0;
+            for (int i = 32 * k; i < min(32 * k + 32, n); ++i) {
+                const double x = s_row[i];
+                ss = fma(x, x, ss);
+            }
+            stats[32 * (base / 32 + k) + row] = ss;
+        }
+        __syncthreads();   // s_row is refilled by the next pass
+    }
+}
+
+__global__ __launch_bounds__(256) void embed_rows_kernel(const float * table, int n_rows, int dim, const int32_t * ids,
+                                                         float * out, double * stats) {
     const int r = blockIdx.x;
     const int id = ids[r];
-    float * o = out + static_cast<int64_t>(r) * dim;
     const bool valid = id >= 0 && id < n_rows;
-    const float * t = table + static_cast<int64_t>(valid ? id : 0) * dim;
-    for (int i = threadIdx.x; i < dim; i += blockDim.x) o[i] = valid ? t[i] : 0.0f;
-    if (stats) {
-        for (int k = threadIdx.x; 32 * k < dim; k += blockDim.x) {
-            double ss = 0.0;
-            for (int i = 32 * k; i < min(32 * k + 32, dim); ++i) {
-                const float v = valid ? t[i] : 0.0f;
-                ss += static_cast<double>(v) * v;
-            }
-            stats[32 * k + r] = ss;
-        }
-    }
+    gather_row(table + static_cast<int64_t>(valid ? id : 0) * dim, valid, dim, out + static_cast<int64_t>(r) * dim,
+               stats, r);
 }
 
 __global__ void advance_lens_kernel(int32_t * lens, int n, int delta) {
@@ -876,6 +903,10 @@ __device__ inline Cand better(Cand a, Cand b) {
 }
 
 constexpr int kArgmaxBlocks = 64;
+// uint32 words between the rows' block counters: one 256-byte line each.  Device-scope atomics on one
+// line are serialised, so with the counters of 32 rows packed into one line the 2048 increments of a
+// 32-row pick queued behind each other (32 us per config-4 step, against 8 us for one row).
+constexpr int kArgmaxCounterStride = 64;
 constexpr int kArgmaxBatch = 10;   // loads per thread in flight: a 1.7B vocabulary chunk (2374) in one round
 constexpr int32_t kNoIndex = 0x7fffffff;
 
@@ -936,9 +967,10 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float * logits, int v
         __hip_atomic_store(partial + row * kArgmaxBlocks + blockIdx.x, pack_cand(b), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        const uint32_t old = __hip_atomic_fetch_add(counters + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t * ctr = counters + static_cast<int64_t>(row) * kArgmaxCounterStride;
+        const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         is_last = old == kArgmaxBlocks - 1;
-        if (is_last) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (is_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!is_last) return;
@@ -960,19 +992,8 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float * logits, int v
     __syncthreads();
     const int id = s_id;
     const bool valid = id >= 0 && id < vocab;
-    const float * t = tail.embd + static_cast<int64_t>(valid ? id : 0) * tail.dim;
-    float * o = tail.x + static_cast<int64_t>(row) * tail.dim;
-    for (int i = threadIdx.x; i < tail.dim; i += 256) o[i] = valid ? t[i] : 0.0f;
-    if (tail.stats) {
-        for (int k = threadIdx.x; 32 * k < tail.dim; k += 256) {
-            double ss = 0.0;
-            for (int i = 32 * k; i < min(32 * k + 32, tail.dim); ++i) {
-                const float v = valid ? t[i] : 0.0f;
-                ss += static_cast<double>(v) * v;
-            }
-            tail.stats[32 * k + row] = ss;
-        }
-    }
+    gather_row(tail.embd + static_cast<int64_t>(valid ? id : 0) * tail.dim, valid, tail.dim,
+               tail.x + static_cast<int64_t>(row) * tail.dim, tail.stats, row);
 }
 
 }  // namespace
@@ -1122,7 +1143,7 @@ int gemm_rows_launch(const float * W, int32_t N, int32_t K, const float * X, int
 }
 
 size_t argmax_workspace_bytes(int32_t rows) {
-    return (sizeof(Cand) * kArgmaxBlocks + sizeof(uint32_t)) * static_cast<size_t>(rows) + 256;
+    return (sizeof(Cand) * kArgmaxBlocks + sizeof(uint32_t) * kArgmaxCounterStride) * static_cast<size_t>(rows) + 256;
 }
 
 int argmax_launch(const float * logits, int32_t rows, int32_t vocab, int32_t * ids, void * workspace,

@@ -91,6 +91,10 @@ struct qa_decoder {
     int32_t * d_ids = nullptr;
     int32_t * h_ids = nullptr;   // pinned
     int32_t * h_ids_dev = nullptr;   // the same memory as the device addresses it
+    // qa_decoder_generate's pipeline: completion events of the two decode steps in flight, and (margins
+    // only) two pinned logits rows, allocated at first use
+    hipEvent_t gen_ev[2] = {nullptr, nullptr};
+    float * h_logits = nullptr;
     float * staging = nullptr;
     size_t staging_bytes = 0;
     float scale = 0.0f;
@@ -576,10 +580,10 @@ int decode_step(qa_decoder * d, int32_t rows, bool embed, int32_t * host_ids = n
     return QA_OK;
 }
 
-float top2_margin(const std::vector<float> & v, int32_t best) {
+float top2_margin(const float * v, int32_t n, int32_t best) {
     float second = -INFINITY;
-    for (size_t i = 0; i < v.size(); ++i) {
-        if (static_cast<int32_t>(i) != best && v[i] > second) second = v[i];
+    for (int32_t i = 0; i < n; ++i) {
+        if (i != best && v[i] > second) second = v[i];
     }
     return v[best] - second;
 }
@@ -799,6 +803,10 @@ extern "C" void qa_decoder_destroy(qa_decoder * d) {
     if (d->staging) (void)hipFree(d->staging);
     if (d->cache) (void)hipFree(d->cache);
     if (d->h_ids) (void)hipHostFree(d->h_ids);
+    if (d->h_logits) (void)hipHostFree(d->h_logits);
+    for (hipEvent_t e : d->gen_ev) {
+        if (e) (void)hipEventDestroy(e);
+    }
     if (d->blas) rocblas_destroy_handle(d->blas);
     if (d->stream) (void)hipStreamDestroy(d->stream);
     delete d;
@@ -866,37 +874,63 @@ extern "C" int qa_decoder_generate(qa_decoder * d, const float * x, int32_t n_to
     int rc = ensure_rows(d, n_tokens);
     if (rc != QA_OK) return rc;
     const int32_t V = d->cfg.vocab;
-    std::vector<float> host_logits;
+    for (hipEvent_t & e : d->gen_ev) {
+        if (!e) QA_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    }
+    if (margins && !d->h_logits) {
+        QA_HIP(hipHostMalloc(reinterpret_cast<void **>(&d->h_logits), sizeof(float) * 2 * static_cast<size_t>(V)));
+    }
+    // Pipelined loop: decode step e + 1 (which feeds id e, already on the device) is queued before the host
+    // reads id e, so the device never waits for the host's stop check.  Step k writes its id into pinned slot
+    // k % 2 and (margins) its logits into pinned row k % 2, then records gen_ev[k % 2]; the host reads slot
+    // e % 2 after gen_ev[e % 2], and step e + 2 reuses that slot only after.  When id e ends the loop (stop id,
+    // out of range), the one step queued beyond it is rolled back: the length returns to the fed tokens, as if
+    // it had never run (its K/V row lies past the length, where no call reads before writing it again).
     QA_HIP(hipMemcpyAsync(d->x, x, sizeof(float) * n_tokens * d->cfg.hidden, hipMemcpyHostToDevice, d->stream));
     rc = forward_device(d, n_tokens, 0, true);
     if (rc != QA_OK) return rc;
-    for (int32_t step = 0; step < max_new; ++step) {
-        QA_HIP(hipMemcpyAsync(d->h_ids, d->d_ids, sizeof(int32_t), hipMemcpyDeviceToHost, d->stream));
-        if (margins) {
-            host_logits.resize(static_cast<size_t>(V));
-            QA_HIP(hipMemcpyAsync(host_logits.data(), d->logits, sizeof(float) * V, hipMemcpyDeviceToHost, d->stream));
+    QA_HIP(hipMemcpyAsync(d->h_ids, d->d_ids, sizeof(int32_t), hipMemcpyDeviceToHost, d->stream));
+    if (margins) QA_HIP(hipMemcpyAsync(d->h_logits, d->logits, sizeof(float) * V, hipMemcpyDeviceToHost, d->stream));
+    QA_HIP(hipEventRecord(d->gen_ev[0], d->stream));
+    int32_t queued = 0;   // decode steps queued; step k (1-based) produces id k
+    int32_t fed = 0;      // ids appended to the cache by the steps the loop keeps
+    for (int32_t e = 0; e < max_new; ++e) {
+        if (queued == e && e + 1 < max_new) {
+            const int32_t k = e + 1;
+            rc = decode_step(d, 1, k == 1, d->h_ids_dev + (k % 2));
+            if (rc != QA_OK) return rc;
+            if (margins) {
+                QA_HIP(hipMemcpyAsync(d->h_logits + static_cast<size_t>(k % 2) * V, d->logits, sizeof(float) * V,
+                                      hipMemcpyDeviceToHost, d->stream));
+            }
+            QA_HIP(hipEventRecord(d->gen_ev[k % 2], d->stream));
+            queued = k;
         }
-        QA_HIP(hipStreamSynchronize(d->stream));
-        const int32_t id = d->h_ids[0];
-        if (id < 0 || id >= V) {
-            rc = persist_check(d);
-            return rc != QA_OK ? rc : fail(QA_ERR_RANGE, "generated token id is out of range");
+        QA_HIP(hipEventSynchronize(d->gen_ev[e % 2]));
+        const int32_t id = d->h_ids[e % 2];
+        bool stop = id < 0 || id >= V;
+        if (!stop) {
+            if (margins) margins[e] = top2_margin(d->h_logits + static_cast<size_t>(e % 2) * V, V, id);
+            out_ids[(*n_out)++] = id;
+            *total_tokens = n_tokens + *n_out;
+            for (int32_t k = 0; k < n_stop; ++k) stop = stop || stop_ids[k] == id;
+            if (stop) *stopped = 1;
         }
-        if (margins) margins[step] = top2_margin(host_logits, id);
-        out_ids[(*n_out)++] = id;
-        *total_tokens = n_tokens + *n_out;
-        bool stop = false;
-        for (int32_t k = 0; k < n_stop; ++k) stop = stop || stop_ids[k] == id;
-        if (stop) {
-            *stopped = 1;
-            break;
-        }
-        if (step + 1 >= max_new) break;
-        rc = decode_step(d, 1, step == 0);
-        if (rc != QA_OK) return rc;
+        if (stop) break;
+        fed = e + 1;
     }
     QA_HIP(hipStreamSynchronize(d->stream));
-    return persist_check(d);
+    if (queued > fed) {
+        // the step queued beyond the last kept id: length back to n_tokens + fed (device and host)
+        rc = set_values_launch(d->d_lens, 1, n_tokens + fed, d->stream);
+        if (rc != QA_OK) return rc;
+        d->cur_len[0] = n_tokens + fed;
+        QA_HIP(hipStreamSynchronize(d->stream));
+    }
+    rc = persist_check(d);
+    if (rc != QA_OK) return rc;
+    if (*n_out < max_new && !*stopped) return fail(QA_ERR_RANGE, "generated token id is out of range");
+    return QA_OK;
 }
 
 extern "C" int qa_decoder_decode_streams(qa_decoder * d, const int32_t * first_ids, int32_t n_steps, int32_t * out_ids) {

@@ -98,6 +98,31 @@ def test_small_model_greedy_matches_oracle(qa, orc, greedy, f16):
         close(logits, ref_logits, atol=2e-3, rtol_l2=1e-3)
 
 
+@pytest.mark.parametrize("persistent", [False, True], ids=["eager", "persistent"])
+def test_generate_stop_rolls_back_the_queued_step(qa, persistent):
+    """qa_decoder_generate queues the step after id e before it reads id e.  A stop at e undoes that step:
+    the length (host and device) counts the fed ids only, and the next call on the same decoder gives what
+    a fresh decoder gives.  Stops at the first id (the prefill's pick), at a middle one and at the last."""
+    model = qa.Model(qa.QWEN3_ASR_0_6B, n_layers=2)
+    x = qa.prompt_input(model, 20, 6)
+    N = 10
+    with qa.Decoder(model, 1, 26 + N) as fresh:
+        full = fresh.generate(x, N, stop_ids=())
+    assert len(full["ids"]) == N and not full["stopped"]
+    with qa.Decoder(model, 1, 26 + N) as dec:
+        if persistent:
+            dec.set_persistent(True)
+        for e in (0, 4, N - 1):
+            out = dec.generate(x, N, stop_ids=[full["ids"][e]])
+            first = full["ids"].index(full["ids"][e])
+            assert out["stopped"] and out["ids"] == full["ids"][:first + 1]
+            assert out["total_tokens"] == 26 + first + 1
+            assert dec.cur_len(0) == 26 + first and dec.device_lens().tolist() == [26 + first]
+        again = dec.generate(x, N, stop_ids=())
+        assert again["ids"] == full["ids"] and dec.cur_len(0) == 26 + N - 1
+        assert dec.device_lens().tolist() == [26 + N - 1]
+
+
 @pytest.mark.parametrize("index,bf16", [(1, False), (2, False), (3, False), (3, True)])
 def test_config_greedy_matches_golden(qa, greedy, index, bf16):
     """Configs 1-3 with seeded N(0, 0.02) f32 weights (the f32 kernels), and config 3 -- the bench

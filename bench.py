@@ -482,6 +482,27 @@ def prefill_gemm_roofline(cfg, T: int, fam_ms: dict):
             "positions": T, "ms": ms}
 
 
+def decode_weight_rooflines(cfg, elem: int, fam_ms: dict):
+    """HBM rooflines of the batch-1 decode step's weight streams, from the event-bracketed kernel families of
+    one token (the families include the gaps between their launches, so the rates are lower bounds):
+    projections = the q|k|v, o, gate|up and down GEMVs of every layer (elem bytes per parameter), lm_head = the
+    final RMSNorm + LM head GEMV + greedy pick (vocab x hidden parameters)."""
+    H, QD, KD, I = cfg.hidden, cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim, cfg.intermediate
+    layer = (QD + 2 * KD) * H + H * QD + 2 * I * H + H * I
+    out = {}
+    for key, fam, nbytes, kernel in (
+            ("projections", "projections", elem * layer * cfg.n_layers,
+             "gemv_kernel: q|k|v (RMSNorm input), o (+ residual), gate|up (RMSNorm input, SwiGLU), down (+ residual), "
+             "every layer of one token"),
+            ("lm_head", "logits", elem * cfg.vocab * H, "gemv_kernel: final RMSNorm + LM head, then argmax_kernel")):
+        ms = fam_ms[fam]
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[key] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kernel,
+                    "bytes_per_token": nbytes, "ms_per_token": ms}
+    return out
+
+
 def guarded(result: dict, key: str, fn):
     """Runs one secondary leg; a failure is recorded under result[key] = {"error": ...} instead of ending
     the run, so the measurements taken before it still reach the JSON line."""
@@ -616,7 +637,8 @@ def main():
     log(f"timed {args.steps} decode steps at context {ctx0}..{ctx0 + args.steps} ({weights_streamed} weights "
         f"streamed): {dt * 1e3:.1f} ms ({main_leg['ms_per_step']:.4f} ms/token); per-step device ms by family "
         f"{main_leg['family_ms_per_step']}")
-    wbytes = weight_bytes(model, 2 if dec.weights_bf16 else 4)
+    elem = 2 if dec.weights_bf16 else 4
+    wbytes = weight_bytes(model, elem)
     attn_us, L, attn_bytes, n_launch = attention_roofline(qa, dec, args.roofline_reps)
     dec.close()
     achieved = attn_bytes / (attn_us * 1e-6) / 1e9
@@ -654,6 +676,8 @@ def main():
         "family_ms_per_step": main_leg["family_ms_per_step"],
         "weight_bytes_per_token": wbytes,
         "weight_stream_gbs": round(wbytes / (dt / args.steps) / 1e9, 1),
+        "roofline_weights": (decode_weight_rooflines(model.cfg, elem, main_leg["family_ms_per_step"])
+                             if main_leg["family_ms_per_step"] else None),
         "capacity_plan": plan,
     }
 

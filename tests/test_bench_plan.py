@@ -132,3 +132,20 @@ def test_prefill_rooflines():
     g = bench.prefill_gemm_roofline(cfg, 3913, {"projections": 30.0})
     assert g["flop_per_layer"] == 6 * 3913 * params
     assert abs(g["achieved"] - 28 * 6 * 3913 * params / 30e-3 / 1e12) < 0.1
+
+
+def test_decode_weight_rooflines():
+    """The batch-1 weight-stream objects: 1.7B layer projections are 50.33 M parameters (q|k|v 2048 x 4096, o 2048 x
+    2048, gate|up 2 x 6144 x 2048, down 2048 x 6144), the LM head 151936 x 2048."""
+    import qwenasr_amd as qa
+
+    cfg = qa.QWEN3_ASR_1_7B.config()
+    r = bench.decode_weight_rooflines(cfg, 4, {"projections": 1.0, "logits": 0.2})
+    layer = 2048 * 4096 + 2048 * 2048 + 2 * 6144 * 2048 + 6144 * 2048
+    assert layer == 50331648
+    assert r["projections"]["bytes_per_token"] == 4 * 28 * layer
+    assert abs(r["projections"]["achieved"] - 4 * 28 * layer / 1e-3 / 1e9) < 0.1
+    assert r["lm_head"]["bytes_per_token"] == 4 * 151936 * 2048
+    assert abs(r["lm_head"]["frac"] - 4 * 151936 * 2048 / 0.2e-3 / 1e9 / 8000) < 1e-4
+    r16 = bench.decode_weight_rooflines(cfg, 2, {"projections": 1.0, "logits": 0.2})
+    assert r16["projections"]["bytes_per_token"] * 2 == r["projections"]["bytes_per_token"]

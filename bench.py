@@ -748,7 +748,7 @@ def main():
              "tok_s": round(args.persistent_steps / dt_p, 3),
              "over_eager": round(dt_p / args.persistent_steps / (dt / args.steps), 3),
              "ids_equal_eager": got[:n] == main_leg["ids"][:n], "ids_compared": n,
-             "mechanism": "one cooperative launch of 256 resident workgroups per token for all layers (grid "
+             "mechanism": "one launch of 256 resident workgroups per token for all layers (grid "
                           "barriers between the six phases of a layer), then the LM head and the pick"}
         log(f"persistent decode step: {r['ms_per_step']:.4f} ms/token ({r['over_eager']:.2f}x the eager step), "
             f"ids equal to the eager run: {r['ids_equal_eager']} ({n} compared)")

@@ -421,7 +421,7 @@ int qa_decoder_decode_streams(qa_decoder * dec, const int32_t * first_ids, int32
 
 /* Decode-step capture without a graph (text-decoder.cpp:1658-1739 rebuilds and schedules a graph per
  * token): with enable = 1, every batch-1 decode step of this decoder (generate, and cached forwards of
- * one token) runs all its layers as ONE persistent cooperative launch, whose resident workgroups walk
+ * one token) runs all its layers as ONE persistent launch (one workgroup per CU), whose workgroups walk
  * the layers' six phases behind grid barriers, driven by the device-side length; the LM head and the
  * pick follow as two launches.  Results are bit-identical to the eager step (same device code per
  * phase).  QA_ERR_INVALID if no persistent kernel is instantiated for the decoder's shapes (streams,

@@ -3,8 +3,8 @@
 //
 // The reference rebuilds and re-schedules its GGML graph for every token (text-decoder.cpp:1658-1739).
 // The eager step of this library already replaces that with a fixed sequence of launches driven by
-// device-side lengths (six per layer).  This kernel replaces the sequence itself: one cooperative launch
-// of G resident workgroups walks the 28 layers, each layer in six phases separated by grid barriers:
+// device-side lengths (six per layer).  This kernel replaces the sequence itself: one launch of G resident
+// workgroups walks the 28 layers, each layer in six phases separated by grid barriers:
 //   q|k|v GEMV (RMSNorm input) -> scores (append + q/k prep) -> values (+ merge) -> o GEMV (+ residual)
 //   -> gate|up GEMV (RMSNorm input, SwiGLU) -> down GEMV (+ residual).
 // Each phase runs the eager kernel's device function (gemv_body.hpp, decode_attn_body.hpp) over the same
@@ -290,9 +290,14 @@ inline int launch_variant(const Variant * v, const PersistLaunch & a, hipStream_
     P.n_groups = (a.grid + kGroup - 1) / kGroup;
     P.wait_ticks = a.wait_ticks;
     RopeTable rope = make_rope_table(a.rope_theta);
+    // A plain launch: the grid is one workgroup per CU and the occupancy check at enable time showed that one
+    // fits, so on a device this stream has to itself every workgroup is resident from the start (a workgroup
+    // kept out by other work would end the launch through the bounded waits, not hang it).  A cooperative
+    // launch would guarantee residency, but it takes the device's global wave-sync resource, which one
+    // process at a time can hold: while one process held it, another's cooperative launch failed.
     void * args[] = {&P, &rope};
-    QA_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(v->fn), dim3(static_cast<unsigned>(a.grid)),
-                                      dim3(256), args, 0, stream));
+    QA_HIP(hipLaunchKernel(reinterpret_cast<const void *>(v->fn), dim3(static_cast<unsigned>(a.grid)), dim3(256),
+                           args, 0, stream));
     return QA_OK;
 }
 

@@ -90,7 +90,7 @@ int decode_step_attn_launch(const float * qkv, const float * q_norm_w, const flo
                             void * workspace, size_t workspace_bytes, hipStream_t stream);
 size_t decode_attn_workspace(int32_t n_streams, int32_t n_kv_heads, int32_t max_seq);
 
-// Persistent decode step (decode_persist.hip): every layer of one batch-1 token in one cooperative launch,
+// Persistent decode step (decode_persist.hip): every layer of one batch-1 token in one launch,
 // bit-identical to the eager step.  The layer table lives in device memory.
 struct PersistLayer {
     const void * qkv;   // f32 rows, or their bf16 copies when b16

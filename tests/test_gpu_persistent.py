@@ -1,6 +1,6 @@
 """GPU tests of the persistent decode step (qa_decoder_set_persistent).
 
-Each batch-1 decode step of a persistent decoder runs every layer in one cooperative launch whose phases
+Each batch-1 decode step of a persistent decoder runs every layer in one launch whose phases
 call the same device functions as the eager launches, so the ids, logits and lengths must equal the
 eager decoder's bit for bit.  The eager step is held to the oracle by the other GPU tests; the short
 cases here also compare the ids with the oracle directly.  Every call goes through the C ABI.

@@ -293,8 +293,9 @@ inline int launch_variant(const Variant * v, const PersistLaunch & a, hipStream_
     // A plain launch: the grid is one workgroup per CU and the occupancy check at enable time showed that one
     // fits, so on a device this stream has to itself every workgroup is resident from the start (a workgroup
     // kept out by other work would end the launch through the bounded waits, not hang it).  A cooperative
-    // launch would guarantee residency, but it takes the device's global wave-sync resource, which one
-    // process at a time can hold: while one process held it, another's cooperative launch failed.
+    // launch would guarantee residency, but after one process had made cooperative launches, another
+    // process's cooperative launch failed (hipErrorIllegalState), as if the device-wide wave-sync resource
+    // that cooperative launches take stayed with the first process.
     void * args[] = {&P, &rope};
     QA_HIP(hipLaunchKernel(reinterpret_cast<const void *>(v->fn), dim3(static_cast<unsigned>(a.grid)), dim3(256),
                            args, 0, stream));

@@ -835,8 +835,6 @@ __global__ void add_inplace_kernel(float * y, const float * x, size_t n) {
     }
 }
 
-// stats (optional): stats[k][r] = sum of squares of columns 32 k .. 32 k + 31 of row r (the partial
-// layout gemm_rows32_kernel takes for its RMSNorm input; r < 32)
 // Row `row` of the next step's input: the embedding row t (zeros unless valid) copied to o, and, with
 // stats, the row's sums of squares per 32-column group (in double, the columns in increasing order),
 // stored at stats[32 * group + row] for the fused RMSNorm input of the multi-stream GEMM.  256 threads;
@@ -875,6 +873,8 @@ __device__ void gather_row(const float * t, bool valid, int dim, float * o, doub
     }
 }
 
+// out[r] = table[ids[r]] (zeros for ids out of range); stats (optional): stats[k][r] = sum of squares of columns
+// 32 k .. 32 k + 31 of row r (the partial layout gemm_rows32_kernel takes for its RMSNorm input; r < 32)
 __global__ __launch_bounds__(256) void embed_rows_kernel(const float * table, int n_rows, int dim, const int32_t * ids,
                                                          float * out, double * stats) {
     const int r = blockIdx.x;

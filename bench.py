@@ -281,8 +281,8 @@ def multistream_roofline(qa, cfg, reps: int, lens=None, label: str = "config 4 s
 def kernel_only(which: str, reps: int, weights: str = "f32", length: int = 4186):
     """One hot-path kernel on synthetic inputs at the config-3 shape, for rocprofv3 passes (the counters
     of every dispatch are then the kernel's alone).  append: the prefill K/V append of 3913 positions
-    (q/k norm + RoPE, f16 cache write); prefill: causal prefill attention over 3913 positions of one
-    layer (f16 cache, n_past 0); decode-attn / decode-attn-f32: the decode-step attention of one layer
+    (q/k norm + RoPE, f16 cache write); prefill / prefill-f32: causal prefill attention over 3913 positions
+    of one layer (f16 / f32 cache, n_past 0); decode-attn / decode-attn-f32: the decode-step attention of one layer
     at L = length (default 4186, capacity L + 8) over an f16 / f32 cache, rotating 28 layer caches; decode-step: config 3 end to end at
     batch 1 (prefill once, then reps greedy decode tokens), decode-step-persistent the same with every
     layer of a token in one persistent launch; multistream: the config-4 decode step of 32
@@ -359,9 +359,10 @@ def kernel_only(which: str, reps: int, weights: str = "f32", length: int = 4186)
                                          n_past.ptr, 1, T, cfg.n_heads, cfg.rope_theta, cfg.rms_norm_eps, None))
         # read q|k|v rows (f32), write q (f32) and the K and V rows (f16)
         unit = dict(algorithmic_bytes_per_launch=T * ((q_dim + 2 * kv_dim) * 4 + q_dim * 4 + 2 * kv_dim * 2))
-    elif which == "prefill":
+    elif which in ("prefill", "prefill-f32"):
         T = 3913
-        lay = qa.KvLayout(2, 1, cfg.n_kv_heads, cfg.head_dim, T + 8, qa.QA_CACHE_F16)
+        ct = qa.QA_CACHE_F16 if which == "prefill" else qa.QA_CACHE_F32
+        lay = qa.KvLayout(2, 1, cfg.n_kv_heads, cfg.head_dim, T + 8, ct)
         cache = qa.DeviceArray(qa.lib.qa_kv_cache_bytes(C.byref(lay)), np.uint8)
         q = qa.DeviceArray.from_numpy(np.random.default_rng(3).standard_normal((T, cfg.n_heads * cfg.head_dim)).astype(np.float32))
         out = qa.DeviceArray((T, cfg.n_heads * cfg.head_dim))
@@ -592,7 +593,7 @@ def main():
                          "layer of a token in one launch), a secondary object of the line; 0: skip")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 10 times (reference for HBM traffic counters)")
-    ap.add_argument("--kernel", choices=["append", "prefill", "decode-attn", "decode-attn-f32", "multistream",
+    ap.add_argument("--kernel", choices=["append", "prefill", "prefill-f32", "decode-attn", "decode-attn-f32", "multistream",
                                          "multistream-attn", "decode-step", "decode-step-persistent"],
                     help="only run one hot-path kernel on synthetic inputs (short program for rocprofv3 passes)")
     ap.add_argument("--kernel-reps", type=int, default=20)
